@@ -1,0 +1,240 @@
+"""ctypes binding of libbq.so (include/bq.h) over torch device tensors.
+
+torch supplies device memory and the current HIP stream; every computation runs
+in libbq's HIP kernels.  There is no fallback: if libbq.so is missing or the
+GPU is absent, calls raise.
+
+Host-side mirror of the reference's launchers (engine/src/bruce.cu):
+    gemv                  launch_gemv            :5624
+    verify_fused          launch_verify_fused    :7141
+    q6_verify_fused       launch_q6_verify_fused :7231
+    gemm_q6k_dp           launch_gemm_q6k_dp     :7285
+    try_mmq               try_launch_mmq         :7366
+    gemm_b / gemm_b_fused launch_gemm_b(_fused)  :7421-7568
+    repack_q5k            q5k_prepack_launch     :4832
+    repack_q6k(_host)     q6k_repack_host        :4783
+    quantize_q8           k_q8_quant / k_q8_rows :518, :1081
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbq.so")
+
+BQ_OK, BQ_UNSUPPORTED, BQ_EINVAL = 0, 1, 2
+TYPE_Q5_K, TYPE_Q6_K = 13, 14
+Q5K_BYTES, Q6K_BYTES = 176, 210
+
+EXPORTS = [
+    "bq_init", "bq_strerror", "bq_version", "bq_quantize_q8", "bq_fill_xdh", "bq_gemv",
+    "bq_verify_fused", "bq_q6_verify_fused", "bq_gemm_q6k_dp", "bq_gemm_q6k_raw", "bq_try_mmq",
+    "bq_gemm_q6k_mma", "bq_gemm_b", "bq_gemm_b_fused", "bq_repack_q5k", "bq_repack_q5k_bytes",
+    "bq_repack_q5k_min_bytes", "bq_repack_q6k", "bq_repack_q6k_host", "bq_repack_q6k_bytes",
+]
+
+
+class BqError(RuntimeError):
+    def __init__(self, code, what):
+        self.code = code
+        super().__init__(f"{what}: {strerror(code)} ({code})")
+
+
+class Weight(ctypes.Structure):
+    """bq_weight == the reference's TensorW {d, dp, dm, type, K, N} (bruce.cu:78)."""
+    _fields_ = [("raw", ctypes.c_void_p), ("rep", ctypes.c_void_p), ("rep_min", ctypes.c_void_p),
+                ("ggml_type", ctypes.c_uint32), ("K", ctypes.c_int32), ("N", ctypes.c_int32)]
+
+
+_lib = None
+
+
+def load(path=LIB_PATH):
+    """Load libbq.so (raises if it is not built).  Imports torch first so the
+    HIP runtime libbq links against is torch's own."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    import torch  # noqa: F401  (one HIP runtime per process)
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built: run __graft_entry__.build()")
+    L = ctypes.CDLL(path)
+    P, I, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    WP = ctypes.POINTER(Weight)
+    sig = {
+        "bq_init": (I, []),
+        "bq_strerror": (ctypes.c_char_p, [I]),
+        "bq_version": (ctypes.c_char_p, []),
+        "bq_quantize_q8": (I, [P, I, I, P, P, P, P, P]),
+        "bq_fill_xdh": (I, [P, P, I, P, P]),
+        "bq_gemv": (I, [P, WP, P, P, P, P]),
+        "bq_verify_fused": (I, [P, P, I, I, P, P, P, I, P]),
+        "bq_q6_verify_fused": (I, [P, P, I, I, P, P, I, P]),
+        "bq_gemm_q6k_dp": (I, [P, WP, I, P, P, I, P]),
+        "bq_gemm_q6k_raw": (I, [P, WP, I, P, P, I, P]),
+        "bq_try_mmq": (I, [P, P, I, I, P, P, P, P, P]),
+        "bq_gemm_q6k_mma": (I, [P, WP, I, P, P, P]),
+        "bq_gemm_b": (I, [P, WP, I, P, P, P, P, P]),
+        "bq_gemm_b_fused": (I, [P, P, I, I, P, P, P, P, P]),
+        "bq_repack_q5k": (I, [P, I, I, P, P, P]),
+        "bq_repack_q5k_bytes": (S, [I, I]),
+        "bq_repack_q5k_min_bytes": (S, [I, I]),
+        "bq_repack_q6k": (I, [P, I, I, P, P]),
+        "bq_repack_q6k_host": (I, [P, I, I, P]),
+        "bq_repack_q6k_bytes": (S, [I, I]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+def strerror(code):
+    return load().bq_strerror(code).decode()
+
+
+def _check(code, what):
+    if code != BQ_OK:
+        raise BqError(code, what)
+    return code
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need_gpu(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("libbq entry points take device tensors")
+
+
+def make_weight(raw=None, ggml_type=TYPE_Q5_K, K=0, N=0, rep=None, rep_min=None):
+    """Build a bq_weight; the tensors must stay alive while it is used."""
+    w = Weight(_ptr(raw).value if raw is not None else None,
+               _ptr(rep).value if rep is not None else None,
+               _ptr(rep_min).value if rep_min is not None else None, ggml_type, K, N)
+    w._keep = (raw, rep, rep_min)
+    return w
+
+
+# ---------------------------------------------------------------- quantizer
+def quantize_q8(x, with_xdh=False):
+    """x fp32 [rows, K] (device) -> xq int8 [rows,K], xd fp32 [rows,K/32], xsum int32, (xdh)."""
+    import torch
+    _need_gpu(x)
+    x = x.contiguous()
+    rows, K = x.shape
+    xq = torch.empty((rows, K), dtype=torch.int8, device=x.device)
+    xd = torch.empty((rows, K // 32), dtype=torch.float32, device=x.device)
+    xs = torch.empty((rows, K // 32), dtype=torch.int32, device=x.device)
+    xdh = torch.empty((rows, K // 32), dtype=torch.int16, device=x.device) if with_xdh else None
+    _check(load().bq_quantize_q8(_ptr(x), rows, K, _ptr(xq), _ptr(xd), _ptr(xs), _ptr(xdh), _stream()),
+           "bq_quantize_q8")
+    return (xq, xd, xs, xdh) if with_xdh else (xq, xd, xs)
+
+
+def fill_xdh(xd, xsum, out=None):
+    import torch
+    if out is None:
+        out = torch.empty(xd.shape, dtype=torch.int16, device=xd.device)
+    _check(load().bq_fill_xdh(_ptr(xd), _ptr(xsum), xd.numel(), _ptr(out), _stream()), "bq_fill_xdh")
+    return out
+
+
+# ---------------------------------------------------------------- GEMV / verify
+def gemv(y, w, xq, xd, xsum):
+    _check(load().bq_gemv(_ptr(y), ctypes.byref(w), _ptr(xq), _ptr(xd), _ptr(xsum), _stream()), "bq_gemv")
+    return y
+
+
+def _arrays(ys, ws):
+    n = len(ws)
+    yarr = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+    warr = (ctypes.POINTER(Weight) * n)(*[ctypes.pointer(w) for w in ws])
+    return yarr, warr
+
+
+def verify_fused(ys, ws, rows, xq, xd, xsum, xoff=0):
+    """Returns the raw code (BQ_UNSUPPORTED means nothing ran, as the reference's false)."""
+    yarr, warr = _arrays(ys, ws)
+    r = load().bq_verify_fused(yarr, warr, len(ws), rows, _ptr(xq), _ptr(xd), _ptr(xsum), xoff, _stream())
+    if r not in (BQ_OK, BQ_UNSUPPORTED):
+        raise BqError(r, "bq_verify_fused")
+    return r
+
+
+def q6_verify_fused(ys, ws, rows, xq, xd, xoff=0):
+    yarr, warr = _arrays(ys, ws)
+    r = load().bq_q6_verify_fused(yarr, warr, len(ws), rows, _ptr(xq), _ptr(xd), xoff, _stream())
+    if r not in (BQ_OK, BQ_UNSUPPORTED):
+        raise BqError(r, "bq_q6_verify_fused")
+    return r
+
+
+def gemm_q6k_dp(y, w, rows, xq, xd, xoff=0):
+    return _check(load().bq_gemm_q6k_dp(_ptr(y), ctypes.byref(w), rows, _ptr(xq), _ptr(xd), xoff, _stream()),
+                  "bq_gemm_q6k_dp")
+
+
+def gemm_q6k_raw(y, w, rows, xq, xd, xoff=0):
+    return _check(load().bq_gemm_q6k_raw(_ptr(y), ctypes.byref(w), rows, _ptr(xq), _ptr(xd), xoff, _stream()),
+                  "bq_gemm_q6k_raw")
+
+
+# ---------------------------------------------------------------- prefill GEMM
+def try_mmq(ys, ws, rows, xq, xd, xsum, xdh=None):
+    yarr, warr = _arrays(ys, ws)
+    r = load().bq_try_mmq(yarr, warr, len(ws), rows, _ptr(xq), _ptr(xd), _ptr(xsum), _ptr(xdh), _stream())
+    if r not in (BQ_OK, BQ_UNSUPPORTED):
+        raise BqError(r, "bq_try_mmq")
+    return r
+
+
+def gemm_q6k_mma(y, w, rows, xq, xd):
+    return _check(load().bq_gemm_q6k_mma(_ptr(y), ctypes.byref(w), rows, _ptr(xq), _ptr(xd), _stream()),
+                  "bq_gemm_q6k_mma")
+
+
+def gemm_b(y, w, rows, xq, xd, xsum, xdh=None):
+    return _check(load().bq_gemm_b(_ptr(y), ctypes.byref(w), rows, _ptr(xq), _ptr(xd), _ptr(xsum),
+                                   _ptr(xdh), _stream()), "bq_gemm_b")
+
+
+def gemm_b_fused(ys, ws, rows, xq, xd, xsum, xdh=None):
+    yarr, warr = _arrays(ys, ws)
+    return _check(load().bq_gemm_b_fused(yarr, warr, len(ws), rows, _ptr(xq), _ptr(xd), _ptr(xsum),
+                                         _ptr(xdh), _stream()), "bq_gemm_b_fused")
+
+
+# ---------------------------------------------------------------- repacks
+def repack_q5k(raw, K, N):
+    """raw uint8 device [N, K/256*176] -> (W144 uint8 [K/128, N, 144], Dm int16 [N, K/32])."""
+    import torch
+    w144 = torch.empty((K // 128, N, 144), dtype=torch.uint8, device=raw.device)
+    dm = torch.empty((N, K // 32), dtype=torch.int16, device=raw.device)
+    _check(load().bq_repack_q5k(_ptr(raw), K, N, _ptr(w144), _ptr(dm), _stream()), "bq_repack_q5k")
+    return w144, dm
+
+
+def repack_q6k(raw, K, N):
+    import torch
+    out = torch.empty((N, K // 128, 160), dtype=torch.uint8, device=raw.device)
+    _check(load().bq_repack_q6k(_ptr(raw), K, N, _ptr(out), _stream()), "bq_repack_q6k")
+    return out
+
+
+def repack_q6k_host(raw_np, K, N):
+    """Host twin on numpy arrays (no device)."""
+    import numpy as np
+    raw_np = np.ascontiguousarray(raw_np, np.uint8)
+    out = np.empty((N, K // 128, 160), np.uint8)
+    _check(load().bq_repack_q6k_host(raw_np.ctypes.data_as(ctypes.c_void_p), K, N,
+                                     out.ctypes.data_as(ctypes.c_void_p)), "bq_repack_q6k_host")
+    return out

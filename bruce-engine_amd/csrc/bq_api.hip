@@ -1,0 +1,338 @@
+// bq_api.hip -- the C ABI of libbq (include/bq.h): argument checks, dispatch.
+//
+// Mirrors the reference's host launchers in engine/src/bruce.cu (launch_gemv
+// :5624, launch_verify_fused :7141, launch_q6_verify_fused :7231,
+// launch_gemm_q6k_dp :7285, try_launch_mmq :7366, launch_gemm_b_fused :7421,
+// launch_gemm_b :7428, q5k_prepack_launch :4832, q6k_repack_host :4783) with
+// three deliberate differences: buffers are passed explicitly instead of read
+// from a global model, nothing calls exit() (errors are return codes), and
+// unsupported shapes return BQ_UNSUPPORTED before anything is enqueued.
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+
+#include "../../include/bq.h"
+#include "bq_internal.hpp"
+
+using namespace bq;
+
+namespace {
+
+struct DevInfo {
+    size_t lds_per_block = 65536;
+    int cus = 256;
+};
+
+std::once_flag g_once;
+DevInfo g_dev;
+int g_init_status = BQ_OK;
+
+int from_hip(hipError_t e) { return e == hipSuccess ? BQ_OK : -(int)e; }
+
+int ensure_init() {
+    std::call_once(g_once, [] {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) { g_init_status = -(int)hipErrorNoDevice; return; }
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, dev) != hipSuccess) { g_init_status = -(int)hipErrorNoDevice; return; }
+        g_dev.lds_per_block = prop.sharedMemPerBlock;
+        g_dev.cus = prop.multiProcessorCount;
+    });
+    return g_init_status;
+}
+
+bool weight_ok(const bq_weight* w) { return w && w->K > 0 && w->N > 0 && (w->K % 256) == 0; }
+
+// Run a multi-row GEMV in row chunks that fit the per-block LDS limit.
+int gemv_rows(GemvKind kind, PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
+              const int32_t* xsum, hipStream_t st) {
+    int r0 = 0;
+    while (r0 < rows) {
+        int c = std::min(rows - r0, (int)BQ_MAX_ROWS);
+        while (c > 1 && gemv_lds_bytes(kind, c, K) > g_dev.lds_per_block) --c;
+        if (gemv_lds_bytes(kind, c, K) > g_dev.lds_per_block) return BQ_UNSUPPORTED;
+        PartTable q = pt;
+        for (int p = 0; p < pt.nparts; ++p) q.Y[p] = pt.Y[p] + (size_t)r0 * pt.N[p];
+        const int nb = K / 32;
+        hipError_t e = launch_gemv(kind, q, c, K, xq + (size_t)r0 * K, xd + (size_t)r0 * nb,
+                                   xsum ? xsum + (size_t)r0 * nb : nullptr, st);
+        if (e != hipSuccess) return from_hip(e);
+        r0 += c;
+    }
+    return BQ_OK;
+}
+
+PartTable one_part(float* y, const void* W, int N) {
+    PartTable pt;
+    memset(&pt, 0, sizeof(pt));
+    pt.W[0] = W;
+    pt.Y[0] = y;
+    pt.N[0] = N;
+    pt.nparts = 1;
+    return pt;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bq_init(void) { return ensure_init(); }
+
+const char* bq_version(void) { return "bq 0.1 gfx950"; }
+
+const char* bq_strerror(int code) {
+    if (code == BQ_OK) return "ok";
+    if (code == BQ_UNSUPPORTED) return "unsupported shape or type (nothing enqueued)";
+    if (code == BQ_EINVAL) return "invalid argument";
+    if (code < 0) return hipGetErrorString((hipError_t)(-code));
+    return "unknown bq error";
+}
+
+int bq_quantize_q8(const float* x, int rows, int K, int8_t* xq, float* xd, int32_t* xsum,
+                   uint16_t* xdh, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (rows < 0 || K <= 0 || (K % 32) != 0) return BQ_EINVAL;
+    if (rows == 0) return BQ_OK;
+    if (!x || !xq || !xd || !xsum) return BQ_EINVAL;
+    return from_hip(launch_quant_q8(x, rows, K, xq, xd, xsum, xdh, (hipStream_t)st));
+}
+
+int bq_fill_xdh(const float* xd, const int32_t* xsum, int n, uint16_t* xdh, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (n < 0) return BQ_EINVAL;
+    if (n == 0) return BQ_OK;
+    if (!xd || !xsum || !xdh) return BQ_EINVAL;
+    return from_hip(launch_fill_xdh(xd, xsum, n, xdh, (hipStream_t)st));
+}
+
+int bq_gemm_q6k_dp(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
+                   int xoff, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (!weight_ok(w) || !y || !xq || !xd || xoff < 0) return BQ_EINVAL;
+    if (w->ggml_type != BQ_TYPE_Q6_K || !w->rep) return BQ_UNSUPPORTED;
+    if (rows < 1 || rows > BQ_MAX_ROWS) return BQ_UNSUPPORTED;
+    const int K = w->K;
+    return gemv_rows(GemvKind::Q6KRep, one_part(y, w->rep, w->N), rows, K, xq + (size_t)xoff * K,
+                     xd + (size_t)xoff * (K / 32), nullptr, (hipStream_t)st);
+}
+
+int bq_gemm_q6k_raw(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
+                    int xoff, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (!weight_ok(w) || !y || !xq || !xd || xoff < 0) return BQ_EINVAL;
+    if (w->ggml_type != BQ_TYPE_Q6_K || !w->raw) return BQ_UNSUPPORTED;
+    if (rows < 1 || rows > BQ_MAX_ROWS) return BQ_UNSUPPORTED;
+    const int K = w->K;
+    return gemv_rows(GemvKind::Q6KRaw, one_part(y, w->raw, w->N), rows, K, xq + (size_t)xoff * K,
+                     xd + (size_t)xoff * (K / 32), nullptr, (hipStream_t)st);
+}
+
+int bq_gemv(float* y, const bq_weight* w, const int8_t* xq, const float* xd, const int32_t* xsum,
+            bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (!weight_ok(w) || !y || !xq || !xd) return BQ_EINVAL;
+    if (w->ggml_type == BQ_TYPE_Q6_K) {
+        if (w->rep) return bq_gemm_q6k_dp(y, w, 1, xq, xd, 0, st);
+        return bq_gemm_q6k_raw(y, w, 1, xq, xd, 0, st);
+    }
+    if (w->ggml_type != BQ_TYPE_Q5_K || !w->raw) return BQ_UNSUPPORTED;
+    if (!xsum) return BQ_EINVAL;
+    return gemv_rows(GemvKind::Q5K, one_part(y, w->raw, w->N), 1, w->K, xq, xd, xsum, (hipStream_t)st);
+}
+
+int bq_verify_fused(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
+                    const int8_t* xq, const float* xd, const int32_t* xsum, int xoff,
+                    bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (rows < 1 || rows > BQ_MAX_ROWS || nparts < 1 || nparts > BQ_MAX_PARTS) return BQ_UNSUPPORTED;
+    if (!ys || !ws || !xq || !xd || !xsum || xoff < 0 || !ws[0]) return BQ_EINVAL;
+    const int K = ws[0]->K;
+    if (K <= 0 || (K % 256) != 0) return BQ_UNSUPPORTED;
+    PartTable pt;
+    memset(&pt, 0, sizeof(pt));
+    for (int p = 0; p < nparts; ++p) {
+        const bq_weight* w = ws[p];
+        if (!w || !w->raw || !ys[p] || w->ggml_type != BQ_TYPE_Q5_K) return BQ_UNSUPPORTED;
+        if (w->K != K || w->N <= 0 || (w->N % 16) != 0) return BQ_UNSUPPORTED;
+        pt.W[p] = w->raw;
+        pt.Y[p] = ys[p];
+        pt.N[p] = w->N;
+    }
+    pt.nparts = nparts;
+    return gemv_rows(GemvKind::Q5K, pt, rows, K, xq + (size_t)xoff * K, xd + (size_t)xoff * (K / 32),
+                     xsum + (size_t)xoff * (K / 32), (hipStream_t)st);
+}
+
+int bq_q6_verify_fused(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
+                       const int8_t* xq, const float* xd, int xoff, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (rows < 2 || rows > BQ_MAX_ROWS || nparts < 1 || nparts > BQ_MAX_PARTS) return BQ_UNSUPPORTED;
+    if (!ys || !ws || !xq || !xd || xoff < 0 || !ws[0]) return BQ_EINVAL;
+    const int K = ws[0]->K;
+    if (K <= 0 || (K % 256) != 0) return BQ_UNSUPPORTED;
+    PartTable pt;
+    memset(&pt, 0, sizeof(pt));
+    for (int p = 0; p < nparts; ++p) {
+        const bq_weight* w = ws[p];
+        if (!w || !w->rep || !ys[p] || w->ggml_type != BQ_TYPE_Q6_K) return BQ_UNSUPPORTED;
+        if (w->K != K || w->N <= 0 || (w->N % 16) != 0) return BQ_UNSUPPORTED;
+        pt.W[p] = w->rep;
+        pt.Y[p] = ys[p];
+        pt.N[p] = w->N;
+    }
+    pt.nparts = nparts;
+    return gemv_rows(GemvKind::Q6KRep, pt, rows, K, xq + (size_t)xoff * K, xd + (size_t)xoff * (K / 32),
+                     nullptr, (hipStream_t)st);
+}
+
+int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
+               const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
+               bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (nparts < 1 || nparts > BQ_MAX_PARTS || rows < 96) return BQ_UNSUPPORTED;
+    if (!ys || !ws || !ws[0] || !xq || !xd || !xsum) return BQ_EINVAL;
+    const int K = ws[0]->K;
+    PartTable pt;
+    memset(&pt, 0, sizeof(pt));
+    bool prepacked = true;
+    for (int p = 0; p < nparts; ++p) {
+        const bq_weight* w = ws[p];
+        if (!w || !w->raw || !ys[p] || w->ggml_type != BQ_TYPE_Q5_K) return BQ_UNSUPPORTED;
+        if (w->K != K || w->N <= 0 || (w->N % 128) != 0) return BQ_UNSUPPORTED;
+        if (!w->rep || !w->rep_min || (K % 512) != 0) prepacked = false;
+        pt.Y[p] = ys[p];
+        pt.N[p] = w->N;
+    }
+    if (K <= 0 || (K % 256) != 0) return BQ_UNSUPPORTED;
+    if (prepacked && !xdh) prepacked = false;
+    pt.nparts = nparts;
+    hipStream_t s = (hipStream_t)st;
+    if (prepacked) {
+        for (int p = 0; p < nparts; ++p) {
+            pt.W[p] = ws[p]->rep;
+            pt.aux[p] = ws[p]->rep_min;
+        }
+        hipError_t e = launch_fill_xdh(xd, xsum, rows * (K / 32), xdh, s);
+        if (e != hipSuccess) return from_hip(e);
+        return from_hip(launch_mmq_q5k_144(pt, rows, K, xq, xd, xdh, s));
+    }
+    for (int p = 0; p < nparts; ++p) pt.W[p] = ws[p]->raw;
+    return from_hip(launch_mmq_q5k_raw(pt, rows, K, xq, xd, xsum, s));
+}
+
+int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
+                    bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (!weight_ok(w) || !y || !xq || !xd || rows < 1) return BQ_EINVAL;
+    if (w->ggml_type != BQ_TYPE_Q6_K || !w->rep || (w->N % 128) != 0) return BQ_UNSUPPORTED;
+    return from_hip(launch_mmq_q6k(one_part(y, w->rep, w->N), rows, w->K, xq, xd, (hipStream_t)st));
+}
+
+int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
+              const int32_t* xsum, uint16_t* xdh, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (!weight_ok(w) || !y || !xq || !xd || rows < 0) return BQ_EINVAL;
+    if (rows == 0) return BQ_OK;
+    const bool q5 = w->ggml_type == BQ_TYPE_Q5_K, q6 = w->ggml_type == BQ_TYPE_Q6_K;
+    if (!q5 && !q6) return BQ_UNSUPPORTED;
+    if (q5 && !xsum) return BQ_EINVAL;
+    if (rows > BQ_MAX_ROWS) {
+        if (q5) {
+            float* ys[1] = {y};
+            const bq_weight* wsp[1] = {w};
+            const int r = bq_try_mmq(ys, wsp, 1, rows, xq, xd, xsum, xdh, st);
+            if (r != BQ_UNSUPPORTED) return r;
+        } else if (w->rep && (w->N % 128) == 0) {
+            return bq_gemm_q6k_mma(y, w, rows, xq, xd, st);
+        }
+    }
+    // 1..8-row kernels, in 8-row chunks
+    const int K = w->K, nb = K / 32;
+    for (int r0 = 0; r0 < rows; r0 += BQ_MAX_ROWS) {
+        const int c = std::min(rows - r0, (int)BQ_MAX_ROWS);
+        float* yc = y + (size_t)r0 * w->N;
+        int r;
+        if (q6) {
+            r = w->rep ? bq_gemm_q6k_dp(yc, w, c, xq, xd, r0, st) : bq_gemm_q6k_raw(yc, w, c, xq, xd, r0, st);
+        } else {
+            PartTable pt = one_part(yc, w->raw, w->N);
+            r = gemv_rows(GemvKind::Q5K, pt, c, K, xq + (size_t)r0 * K, xd + (size_t)r0 * nb,
+                          xsum + (size_t)r0 * nb, (hipStream_t)st);
+        }
+        if (r != BQ_OK) return r;
+    }
+    return BQ_OK;
+}
+
+int bq_gemm_b_fused(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
+                    const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
+                    bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (!ys || !ws || nparts < 1 || nparts > BQ_MAX_PARTS) return BQ_EINVAL;
+    if (rows > BQ_MAX_ROWS) {
+        const int r = bq_try_mmq(ys, ws, nparts, rows, xq, xd, xsum, xdh, st);
+        if (r != BQ_UNSUPPORTED) return r;
+    }
+    for (int p = 0; p < nparts; ++p) {
+        const int r = bq_gemm_b(ys[p], ws[p], rows, xq, xd, xsum, xdh, st);
+        if (r != BQ_OK) return r;
+    }
+    return BQ_OK;
+}
+
+size_t bq_repack_q5k_bytes(int K, int N) { return (size_t)(K / 128) * N * 144; }
+size_t bq_repack_q5k_min_bytes(int K, int N) { return (size_t)N * (K / 32) * 2; }
+size_t bq_repack_q6k_bytes(int K, int N) { return (size_t)N * (K / 128) * 160; }
+
+int bq_repack_q5k(const void* raw, int K, int N, void* w144, uint16_t* dm, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (!raw || !w144 || !dm || K <= 0 || N <= 0 || (K % 256) != 0) return BQ_EINVAL;
+    return from_hip(launch_repack_q5k(raw, K, N, w144, dm, (hipStream_t)st));
+}
+
+int bq_repack_q6k(const void* raw, int K, int N, void* w160, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (!raw || !w160 || K <= 0 || N <= 0 || (K % 256) != 0) return BQ_EINVAL;
+    return from_hip(launch_repack_q6k(raw, K, N, w160, (hipStream_t)st));
+}
+
+// Host repack (q6k_repack_host, bruce.cu:4783-4811).  Plain C++, no device.
+int bq_repack_q6k_host(const void* rawv, int K, int N, void* dstv) {
+    if (!rawv || !dstv || K <= 0 || N <= 0 || (K % 256) != 0) return BQ_EINVAL;
+    const uint8_t* raw = (const uint8_t*)rawv;
+    uint8_t* dst = (uint8_t*)dstv;
+    const int nsb = K / 256, nst = K / 128;
+    for (int n = 0; n < N; ++n)
+        for (int s = 0; s < nst; ++s) {
+            const uint8_t* b = raw + ((size_t)n * nsb + s / 2) * 210;
+            const int hh = s & 1;
+            uint8_t* o = dst + ((size_t)n * nst + s) * 160;
+            const uint16_t hb = (uint16_t)(b[208] | (b[209] << 8));
+            // binary16 -> binary32 with denormals (exponent 0 -> m * 2^-24)
+            const uint32_t e = (hb >> 10) & 0x1F, m = hb & 0x3FF;
+            float d;
+            if (e == 0) {
+                d = (float)m * 5.9604644775390625e-8f;
+                if (hb & 0x8000) d = -d;
+            } else {
+                const uint32_t bits = ((uint32_t)(hb & 0x8000) << 16) |
+                                      (e == 31 ? (0x7F800000u | (m << 13)) : (((e + 112u) << 23) | (m << 13)));
+                memcpy(&d, &bits, 4);
+            }
+            for (int k = 0; k < 128; ++k) {
+                const int u = k >> 5, l = k & 31;
+                const uint8_t q = b[64 * hh + 32 * (u & 1) + l];
+                const int lo = (u < 2) ? (q & 0xF) : (q >> 4);
+                const int hi = (b[128 + 32 * hh + l] >> (2 * u)) & 3;
+                o[k] = (uint8_t)(int8_t)((lo | (hi << 4)) - 32);
+            }
+            for (int g = 0; g < 8; ++g) {
+                const float v = d * (float)(int8_t)b[192 + 8 * hh + g];
+                memcpy(o + 128 + 4 * g, &v, 4);
+            }
+        }
+    return BQ_OK;
+}
+
+}  // extern "C"

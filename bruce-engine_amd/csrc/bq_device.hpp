@@ -1,0 +1,96 @@
+// bq_device.hpp -- device helpers shared by the gfx950 kernels of libbq.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define BQ_DEV __device__ __forceinline__
+
+namespace bq {
+
+constexpr int kQ5Bytes = 176;  // GGUF Q5_K block (256 values)
+constexpr int kQ6Bytes = 210;  // GGUF Q6_K block (256 values)
+constexpr int kW144 = 144;     // Q5_K repack stage (128 values)
+constexpr int kW160 = 160;     // Q6_K repack stage (128 values)
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+BQ_DEV float h2f(uint32_t bits16) {
+    // v_cvt_f32_f16: exact, fp16 denormals included
+    const _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+    return (float)h;
+}
+
+BQ_DEV uint16_t f2h_rn(float f) {
+    // f is first rounded to fp32 (the reference's __float2half(a * b) rounds
+    // twice); the empty asm stops the compiler from fusing the producing
+    // multiply into a single-rounding mixed-precision v_mad_mix* instruction.
+    asm volatile("" : "+v"(f));
+    const _Float16 h = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+// bit pattern -> float.  Takes the word by value: __builtin_bit_cast applied
+// directly to an ext_vector element reinterprets element 0, not the element.
+BQ_DEV float as_float(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// signed int8x4 dot product with int32 accumulate (v_dot4_i32_i8)
+BQ_DEV int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// 16-byte load of read-once weight data
+BQ_DEV u32x4 ld16(const void* p) { return *(const u32x4*)p; }
+BQ_DEV u32x4 ld16_stream(const void* p) {
+    return __builtin_nontemporal_load((const u32x4*)p);
+}
+
+// 16 bytes starting at a 2-byte aligned address, built from dword-aligned loads
+// (v_alignbyte_b32 funnel shift).  Reads only [p & ~3, p + 18) when p % 4 == 2,
+// [p, p + 16) when p % 4 == 0.
+BQ_DEV u32x4 ld16_a2(const uint8_t* p) {
+    const uintptr_t a = (uintptr_t)p;
+    const uint32_t* w = (const uint32_t*)(a & ~(uintptr_t)3);
+    if ((a & 2) == 0) {
+        u32x4 r;
+        __builtin_memcpy(&r, w, 16);
+        return r;
+    }
+    uint32_t v[5];
+    __builtin_memcpy(v, w, 20);
+    u32x4 r;
+    r.x = __builtin_amdgcn_alignbyte(v[1], v[0], 2);
+    r.y = __builtin_amdgcn_alignbyte(v[2], v[1], 2);
+    r.z = __builtin_amdgcn_alignbyte(v[3], v[2], 2);
+    r.w = __builtin_amdgcn_alignbyte(v[4], v[3], 2);
+    return r;
+}
+
+// Wave64 sum.  Butterfly over the 64 lanes; every lane ends with the total.
+BQ_DEV float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+BQ_DEV int wave_sum_i(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// 6-bit scale and min of Q5_K sub-block j from the three scale words
+// (s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11]); GGUF layout:
+// j < 4: sc = s[j] & 63, m = s[j+4] & 63; j >= 4: low nibbles from s[j+4],
+// top two bits from s[j-4] / s[j].  Branch-free for divergent j.
+BQ_DEV void q5k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, uint32_t& sc, uint32_t& m) {
+    const int sh = 8 * (j & 3);
+    const uint32_t a = (s0 >> sh) & 0xFF, b = (s1 >> sh) & 0xFF, c = (s2 >> sh) & 0xFF;
+    const uint32_t lo_sc = a & 63, lo_m = b & 63;
+    const uint32_t hi_sc = (c & 0xF) | ((a >> 6) << 4);
+    const uint32_t hi_m = (c >> 4) | ((b >> 6) << 4);
+    sc = j < 4 ? lo_sc : hi_sc;
+    m = j < 4 ? lo_m : hi_m;
+}
+
+}  // namespace bq

@@ -1,0 +1,499 @@
+// bq_gemm.hip -- 128x128-tile int8 MFMA prefill GEMMs for gfx950.
+//
+// Reference semantics (engine/src/bruce.cu):
+//   k_gemm_mmq_q5k_144 :6604-6792  Y = sum_g (ds*xd)*dot + sum_g f16(Dm)*f16(xdh)
+//   k_gemm_mmq_q5k     :6367-6593  Y = sum_g fma(ds*xd, dot, -dm*(xd*xsum))   (fp32 min term)
+//   k_gemm_mma_q6k_128 :6943-7063  Y = sum_g32 xd * (s_lo*dot16_lo + s_hi*dot16_hi)
+//
+// MI355X design:
+//   * Workgroup = 4 waves, tile = 128 weight rows x 128 tokens, each wave a
+//     64x64 sub-tile of 2x2 v_mfma_i32_32x32x32_i8 (K = 32 = one Q5_K scale
+//     group per instruction, so the per-group scale is applied once per MFMA).
+//   * K advances in 128-value stages.  Weights and activations of a stage are
+//     staged in LDS with a 144-byte row stride (128 codes + 16 B pad: 4-dword
+//     bank offset per row, conflict-free 128-bit reads); the next stage is
+//     prefetched into registers while the current one is computed.
+//   * The k order inside an MFMA operand is irrelevant to the sum as long as A
+//     and B use the same order, so each lane simply loads 16 contiguous bytes.
+//   * Scales are staged q-major (sWs[q][row]) so a lane's 4 consecutive
+//     accumulator rows read their scales with one ds_read_b128.
+//   * Min term: W144 path -- fp16 v_mfma_f32_32x32x16_f16 over (Dm, xdh), once
+//     per tile before the main loop (the reference's fp16 semantics); raw path
+//     -- exact fp32 v_mfma_f32_32x32x2_f32 on (dmin*m, -(xd*xsum)) per stage.
+//   * Blocks are mapped XCD-major: block b runs on XCD b % 8, and each XCD gets
+//     a contiguous range of tiles (token tiles fastest) so the tiles that share
+//     a weight panel share one L2.
+#include "bq_device.hpp"
+#include "bq_internal.hpp"
+
+namespace bq {
+
+constexpr int kTM = 128;   // tokens per tile
+constexpr int kTN = 128;   // weight rows per tile
+constexpr int kRS = 144;   // LDS row stride (bytes)
+constexpr int kXcds = 8;
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+enum class MmqMode { Q5W144, Q5Raw };
+
+#ifdef BQ_MMQ_DEBUG
+__device__ uint8_t g_dbg[65536];
+extern "C" int bq_dbg_copy(void* dst) { return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_dbg), 65536); }
+#endif
+
+struct TileMap {
+    int mt, nt;  // token tile, weight-row tile (over concatenated parts)
+};
+
+BQ_DEV bool map_tile(int b, int ntm, int ntn, TileMap& t) {
+    const int ntiles = ntm * ntn;
+    const int per = (ntiles + kXcds - 1) / kXcds;
+    const int idx = (b % kXcds) * per + b / kXcds;
+    if (idx >= ntiles) return false;
+    t.mt = idx % ntm;
+    t.nt = idx / ntm;
+    return true;
+}
+
+BQ_DEV int part_of_ntile(const PartTable& pt, int& nbase) {
+    int p = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxParts; ++i)
+        if (i < pt.nparts && nbase >= pt.N[p]) { nbase -= pt.N[p]; p = i; }
+    return p;
+}
+
+// LDS layout for one stage
+struct Smem {
+    uint8_t w[kTN * kRS];      // weight codes, row stride 144
+    uint8_t x[kTM * kRS];      // token codes, row stride 144
+    float ws[4 * kTN];         // ds   [q][row]
+    float xs[4 * kTM];         // xd   [q][tok]
+    float wm[4 * kTN];         // raw: dmin*m      [q][row]
+    float xm[4 * kTM];         // raw: -(xd*xsum)  [q][tok]
+};
+
+template <MmqMode MODE>
+__global__ void __launch_bounds__(256, 2)
+k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
+          const float* __restrict__ xd, const int32_t* __restrict__ xsum,
+          const uint16_t* __restrict__ xdh) {
+    __shared__ __attribute__((aligned(16))) Smem sm;
+    TileMap tm;
+    if (!map_tile(blockIdx.x, ntm, ntn, tm)) return;
+    int nbase = tm.nt * kTN;
+    const int p = part_of_ntile(pt, nbase);
+    const int Nloc = pt.N[p];
+    const uint8_t* __restrict__ W = (const uint8_t*)pt.W[p];
+    const int m0 = tm.mt * kTM;
+    const int nb = K >> 5, nst = K >> 7, nsb = K >> 8;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wn = wave >> 1, wm = wave & 1;
+    const int l32 = lane & 31, lh = lane >> 5;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+    if constexpr (MODE == MmqMode::Q5W144) {
+        // min term: sum_g f16(Dm[n][g]) * f16(xdh[m][g]) on fp16 MFMA, K/32 % 16 == 0
+        const uint16_t* __restrict__ Dm = (const uint16_t*)pt.aux[p];
+        for (int g0 = 0; g0 < nb; g0 += 16) {
+            f16x8 a[2], b[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int n = nbase + wn * 64 + nt * 32 + l32;
+                a[nt] = *(const f16x8*)(Dm + (size_t)n * nb + g0 + 8 * lh);
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const int m = m0 + wm * 64 + mt * 32 + l32;
+                if (m < rows) b[mt] = *(const f16x8*)(xdh + (size_t)m * nb + g0 + 8 * lh);
+                else b[mt] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[nt], b[mt], acc[nt][mt], 0, 0, 0);
+        }
+    }
+
+    // ---- register prefetch of one stage -------------------------------------
+    // tokens: 1024 chunks of 16 B (tok = c >> 3, part = c & 7), 4 per thread;
+    // token scales: threads 0..127 load xd[tok][4s..4s+3] (+ xsum for raw).
+    u32x4 px[4];
+    f32x4 pxd;
+    i32x4 pxs;
+    // weights, W144: 1152 chunks of 16 B (row = c / 9, part = c % 9), <= 5 per thread
+    u32x4 pw[5];
+    // weights, raw: thread -> (row = tid >> 1, 64-value half hv = tid & 1)
+    u32x4 rqs0, rqs1, rqh0, rqh1, rhdr;
+
+    auto load_stage = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + 256 * i, tok = c >> 3, part = c & 7;
+            const int m = m0 + tok;
+            if (m < rows) px[i] = ld16(xq + (size_t)m * K + 128 * s + 16 * part);
+            else px[i] = (u32x4){0, 0, 0, 0};
+        }
+        if (tid < kTM) {
+            const int m = m0 + tid;
+            if (m < rows) {
+                pxd = *(const f32x4*)(xd + (size_t)m * nb + 4 * s);
+                if constexpr (MODE == MmqMode::Q5Raw) pxs = *(const i32x4*)(xsum + (size_t)m * nb + 4 * s);
+            } else {
+                pxd = (f32x4){0.f, 0.f, 0.f, 0.f};
+                pxs = (i32x4){0, 0, 0, 0};
+            }
+        }
+        if constexpr (MODE == MmqMode::Q5W144) {
+            const uint8_t* src = W + ((size_t)s * Nloc + nbase) * kW144;
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                const int c = tid + 256 * i;
+                if (c < kTN * 9) pw[i] = ld16(src + 16 * c);
+            }
+        } else {
+            const int row = tid >> 1, hv = tid & 1;
+            const uint8_t* blk = W + ((size_t)(nbase + row) * nsb + (s >> 1)) * kQ5Bytes;
+            const int j0 = 4 * (s & 1) + 2 * hv;  // sub-blocks j0, j0 + 1
+            rhdr = ld16(blk);
+            rqh0 = ld16(blk + 16);
+            rqh1 = ld16(blk + 32);
+            rqs0 = ld16(blk + 48 + 32 * (j0 >> 1));
+            rqs1 = ld16(blk + 64 + 32 * (j0 >> 1));
+        }
+    };
+
+    auto store_stage = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + 256 * i, tok = c >> 3, part = c & 7;
+            *(u32x4*)(sm.x + tok * kRS + 16 * part) = px[i];
+        }
+        if (tid < kTM) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sm.xs[q * kTM + tid] = pxd[q];
+            if constexpr (MODE == MmqMode::Q5Raw) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) sm.xm[q * kTM + tid] = -(pxd[q] * (float)pxs[q]);
+            }
+        }
+        if constexpr (MODE == MmqMode::Q5W144) {
+#pragma unroll
+            for (int i = 0; i < 5; ++i) {
+                const int c = tid + 256 * i;
+                if (c < kTN * 9) {
+                    const int row = c / 9, part = c - 9 * row;
+                    if (part < 8) {
+                        *(u32x4*)(sm.w + row * kRS + 16 * part) = pw[i];
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) sm.ws[q * kTN + row] = as_float(pw[i][q]);
+                    }
+                }
+            }
+        } else {
+            const int row = tid >> 1, hv = tid & 1;
+            const int j0 = 4 * (s & 1) + 2 * hv;
+            // codes of sub-blocks j0 (low nibbles) and j0+1 (high nibbles), 32 each
+            u32x4 lo0, lo1, hi0, hi1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                lo0[i] = (rqs0[i] & 0x0F0F0F0Fu) | (((rqh0[i] >> j0) & 0x01010101u) << 4);
+                lo1[i] = (rqs1[i] & 0x0F0F0F0Fu) | (((rqh1[i] >> j0) & 0x01010101u) << 4);
+                hi0[i] = ((rqs0[i] >> 4) & 0x0F0F0F0Fu) | (((rqh0[i] >> (j0 + 1)) & 0x01010101u) << 4);
+                hi1[i] = ((rqs1[i] >> 4) & 0x0F0F0F0Fu) | (((rqh1[i] >> (j0 + 1)) & 0x01010101u) << 4);
+            }
+            uint8_t* dst = sm.w + row * kRS + 64 * hv;
+            *(u32x4*)(dst + 0) = lo0;
+            *(u32x4*)(dst + 16) = lo1;
+            *(u32x4*)(dst + 32) = hi0;
+            *(u32x4*)(dst + 48) = hi1;
+            const float d = h2f(rhdr.x & 0xFFFF), dmin = h2f(rhdr.x >> 16);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                uint32_t sc, mm;
+                q5k_scale_min(rhdr.y, rhdr.z, rhdr.w, j0 + e, sc, mm);
+                const int q = 2 * hv + e;
+                sm.ws[q * kTN + row] = d * (float)sc;
+                sm.wm[q * kTN + row] = dmin * (float)mm;
+            }
+        }
+    };
+
+    load_stage(0);
+    for (int s = 0; s < nst; ++s) {
+        __syncthreads();  // everyone is done reading the previous stage
+        store_stage(s);
+        __syncthreads();
+#ifdef BQ_MMQ_DEBUG
+        if (s == 0 && blockIdx.x == 0) {
+            for (int i = tid; i < (int)sizeof(Smem); i += 256) g_dbg[i] = ((const uint8_t*)&sm)[i];
+            return;
+        }
+#endif
+        if (s + 1 < nst) load_stage(s + 1);
+
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            i32x4 a[2], b[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+                a[nt] = *(const i32x4*)(sm.w + (wn * 64 + nt * 32 + l32) * kRS + 32 * q + 16 * lh);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+                b[mt] = *(const i32x4*)(sm.x + (wm * 64 + mt * 32 + l32) * kRS + 32 * q + 16 * lh);
+            float xs[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) xs[mt] = sm.xs[q * kTM + wm * 64 + mt * 32 + l32];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                float ws[16];
+#pragma unroll
+                for (int rg = 0; rg < 4; ++rg) {
+                    const f32x4 v = *(const f32x4*)(sm.ws + q * kTN + wn * 64 + nt * 32 + 8 * rg + 4 * lh);
+                    ws[4 * rg + 0] = v.x;
+                    ws[4 * rg + 1] = v.y;
+                    ws[4 * rg + 2] = v.z;
+                    ws[4 * rg + 3] = v.w;
+                }
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    const i32x16 zero = {0};
+                    const i32x16 dd = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[nt], b[mt], zero, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        acc[nt][mt][r] = __builtin_fmaf(ws[r] * xs[mt], (float)dd[r], acc[nt][mt][r]);
+                }
+            }
+        }
+        if constexpr (MODE == MmqMode::Q5Raw) {
+            // exact fp32 min term of the stage's four groups: two K=2 MFMAs per tile
+#pragma unroll
+            for (int qp = 0; qp < 2; ++qp) {
+                const int q = 2 * qp + lh;
+                float a[2], b[2];
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) a[nt] = sm.wm[q * kTN + wn * 64 + nt * 32 + l32];
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) b[mt] = sm.xm[q * kTM + wm * 64 + mt * 32 + l32];
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt)
+                        acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[nt], b[mt], acc[nt][mt], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- epilogue: Y[m][n], lane owns token column l32, rows 8*rg + 4*lh + 0..3
+    float* __restrict__ Y = pt.Y[p];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int m = m0 + wm * 64 + mt * 32 + l32;
+        if (m >= rows) continue;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const int n = nbase + wn * 64 + nt * 32 + 8 * rg + 4 * lh;
+                const f32x4 v = {acc[nt][mt][4 * rg], acc[nt][mt][4 * rg + 1], acc[nt][mt][4 * rg + 2],
+                                 acc[nt][mt][4 * rg + 3]};
+                *(f32x4*)(Y + (size_t)m * Nloc + n) = v;
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K over the W160 repack: K = 16 MFMA per 16-value scale group.
+// ---------------------------------------------------------------------------
+struct SmemQ6 {
+    uint8_t w[kTN * kRS];
+    uint8_t x[kTM * kRS];
+    float ws[8 * kTN];  // d*sc per 16-group [g16][row]
+    float xs[4 * kTM];  // xd [q][tok]
+};
+
+__global__ void __launch_bounds__(256, 2)
+k_mmq_q6k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
+          const float* __restrict__ xd) {
+    __shared__ __attribute__((aligned(16))) SmemQ6 sm;
+    TileMap tm;
+    if (!map_tile(blockIdx.x, ntm, ntn, tm)) return;
+    int nbase = tm.nt * kTN;
+    const int p = part_of_ntile(pt, nbase);
+    const int Nloc = pt.N[p];
+    const uint8_t* __restrict__ W = (const uint8_t*)pt.W[p];
+    const int m0 = tm.mt * kTM;
+    const int nb = K >> 5, nst = K >> 7;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wn = wave >> 1, wm = wave & 1;
+    const int l32 = lane & 31, lh = lane >> 5;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+    u32x4 px[4], pw[5];
+    f32x4 pxd;
+    auto load_stage = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + 256 * i, tok = c >> 3, part = c & 7;
+            const int m = m0 + tok;
+            if (m < rows) px[i] = ld16(xq + (size_t)m * K + 128 * s + 16 * part);
+            else px[i] = (u32x4){0, 0, 0, 0};
+        }
+        if (tid < kTM) {
+            const int m = m0 + tid;
+            pxd = (m < rows) ? *(const f32x4*)(xd + (size_t)m * nb + 4 * s) : (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+        // 128 rows x 10 chunks: row = c / 10, part = c % 10
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const int c = tid + 256 * i, row = c / 10, part = c - 10 * row;
+            pw[i] = ld16(W + ((size_t)(nbase + row) * nst + s) * kW160 + 16 * part);
+        }
+    };
+    auto store_stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + 256 * i, tok = c >> 3, part = c & 7;
+            *(u32x4*)(sm.x + tok * kRS + 16 * part) = px[i];
+        }
+        if (tid < kTM) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sm.xs[q * kTM + tid] = pxd[q];
+        }
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const int c = tid + 256 * i, row = c / 10, part = c - 10 * row;
+            if (part < 8) {
+                *(u32x4*)(sm.w + row * kRS + 16 * part) = pw[i];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    sm.ws[(4 * (part - 8) + e) * kTN + row] = as_float(pw[i][e]);
+            }
+        }
+    };
+
+    load_stage(0);
+    for (int s = 0; s < nst; ++s) {
+        __syncthreads();
+        store_stage();
+        __syncthreads();
+        if (s + 1 < nst) load_stage(s + 1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            long a[2][2], b[2][2];  // [tile][16-group half]
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    a[nt][h] = *(const long*)(sm.w + (wn * 64 + nt * 32 + l32) * kRS + 32 * q + 16 * h + 8 * lh);
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+                    b[mt][h] = *(const long*)(sm.x + (wm * 64 + mt * 32 + l32) * kRS + 32 * q + 16 * h + 8 * lh);
+            }
+            float xs[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) xs[mt] = sm.xs[q * kTM + wm * 64 + mt * 32 + l32];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                float w0[16], w1[16];
+#pragma unroll
+                for (int rg = 0; rg < 4; ++rg) {
+                    const int r0 = wn * 64 + nt * 32 + 8 * rg + 4 * lh;
+                    const f32x4 v0 = *(const f32x4*)(sm.ws + (2 * q) * kTN + r0);
+                    const f32x4 v1 = *(const f32x4*)(sm.ws + (2 * q + 1) * kTN + r0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        w0[4 * rg + e] = v0[e];
+                        w1[4 * rg + e] = v1[e];
+                    }
+                }
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    const i32x16 zero = {0};
+                    const i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a[nt][0], b[mt][0], zero, 0, 0, 0);
+                    const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a[nt][1], b[mt][1], zero, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        acc[nt][mt][r] = __builtin_fmaf(xs[mt], w0[r] * (float)d0[r] + w1[r] * (float)d1[r],
+                                                        acc[nt][mt][r]);
+                }
+            }
+        }
+    }
+
+    float* __restrict__ Y = pt.Y[p];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int m = m0 + wm * 64 + mt * 32 + l32;
+        if (m >= rows) continue;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const int n = nbase + wn * 64 + nt * 32 + 8 * rg + 4 * lh;
+                const f32x4 v = {acc[nt][mt][4 * rg], acc[nt][mt][4 * rg + 1], acc[nt][mt][4 * rg + 2],
+                                 acc[nt][mt][4 * rg + 3]};
+                *(f32x4*)(Y + (size_t)m * Nloc + n) = v;
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+static int ntile_count(const PartTable& pt) {
+    int n = 0;
+    for (int p = 0; p < pt.nparts; ++p) n += pt.N[p] / kTN;
+    return n;
+}
+
+static dim3 mmq_grid(int ntm, int ntn) {
+    const int ntiles = ntm * ntn;
+    const int per = (ntiles + kXcds - 1) / kXcds;
+    return dim3(per * kXcds);
+}
+
+hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
+                              const uint16_t* xdh, hipStream_t st) {
+    const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
+    if (ntm == 0 || ntn == 0) return hipSuccess;
+    hipLaunchKernelGGL((k_mmq_q5k<MmqMode::Q5W144>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
+                       rows, K, xq, xd, (const int32_t*)nullptr, xdh);
+    return hipGetLastError();
+}
+
+hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
+                              const int32_t* xsum, hipStream_t st) {
+    const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
+    if (ntm == 0 || ntn == 0) return hipSuccess;
+    hipLaunchKernelGGL((k_mmq_q5k<MmqMode::Q5Raw>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
+                       rows, K, xq, xd, xsum, (const uint16_t*)nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
+                          hipStream_t st) {
+    const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
+    if (ntm == 0 || ntn == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_mmq_q6k, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd);
+    return hipGetLastError();
+}
+
+}  // namespace bq

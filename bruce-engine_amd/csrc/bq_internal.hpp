@@ -1,0 +1,45 @@
+// bq_internal.hpp -- host-side declarations shared by the libbq translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace bq {
+
+constexpr int kMaxParts = 4;
+
+// Up to four matrices that share K and the activation rows, concatenated along
+// N (the reference's W0..W3 / Y0..Y3 / N0..N3 kernel arguments, bruce.cu:5815).
+// tile0[p] = first tile index of part p; filled by the launcher.
+struct PartTable {
+    const void* W[kMaxParts];
+    const void* aux[kMaxParts];  // per-part side array (Q5_K W144: Dm fp16)
+    float* Y[kMaxParts];
+    int N[kMaxParts];
+    int tile0[kMaxParts];
+    int nparts;
+    int ntiles;
+};
+
+enum class GemvKind { Q5K, Q6KRaw, Q6KRep };
+
+hipError_t launch_quant_q8(const float* x, int rows, int K, int8_t* xq, float* xd, int32_t* xsum,
+                           uint16_t* xdh, hipStream_t st);
+hipError_t launch_fill_xdh(const float* xd, const int32_t* xsum, int n, uint16_t* xdh, hipStream_t st);
+
+size_t gemv_lds_bytes(GemvKind kind, int rows, int K);
+hipError_t launch_gemv(GemvKind kind, PartTable pt, int rows, int K, const int8_t* xq,
+                       const float* xd, const int32_t* xsum, hipStream_t st);
+
+hipError_t launch_repack_q5k(const void* raw, int K, int N, void* w144, uint16_t* dm, hipStream_t st);
+hipError_t launch_repack_q6k(const void* raw, int K, int N, void* w160, hipStream_t st);
+
+// prefill GEMMs (128x128 tiles, int8 MFMA)
+hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
+                              const int32_t* xsum, hipStream_t st);
+hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
+                              const uint16_t* xdh, hipStream_t st);
+hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
+                          hipStream_t st);
+
+}  // namespace bq

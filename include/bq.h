@@ -1,0 +1,146 @@
+/*
+ * bq.h -- C ABI of the MI355X k-quant matmul path (libbq.so).
+ *
+ * Drop-in replacement for the quantized-matmul launchers of the reference
+ * engine (engine/src/bruce.cu).  Every entry point is stream-ordered, allocates
+ * nothing, never synchronises and never exits; all buffers are caller-owned
+ * device memory (weights, q8 activations, outputs, repack targets).
+ *
+ * Return codes: BQ_OK (0); BQ_UNSUPPORTED (1) = shape/type not handled, nothing
+ * was enqueued and the caller should fall back (the reference's `return false`,
+ * bruce.cu:7147-7161, :7366-7390); BQ_EINVAL (2) = bad argument (null pointer,
+ * K not a multiple of 256, ...); a negative value = -(hipError_t) of a failed
+ * launch.  bq_strerror() names each code.
+ *
+ * Layouts (GGUF blocks are read unchanged):
+ *   Q5_K  176 B / 256 values: d f16 | dmin f16 | scales[12] | qh[32] | qs[128]
+ *   Q6_K  210 B / 256 values: ql[128] | qh[64] | sc i8[16] | d f16
+ *   q8 activations (structure of arrays, bruce.cu:123-127):
+ *         xq int8 [rows][K], xd fp32 [rows][K/32], xsum int32 [rows][K/32]
+ *   W144  Q5_K repack, stage-major [K/128][N][144]: 128 u8 codes + 4 fp32 d*sc,
+ *         plus Dm fp16 [N][K/32] = half(-dmin*m)          (bruce.cu:5747-5789)
+ *   W160  Q6_K repack, row-major [N][K/128][160]: 128 int8 (code-32) + 8 fp32 d*sc
+ *                                                          (bruce.cu:4783-4811)
+ *   outputs fp32 y[row][N], fully overwritten.
+ */
+#ifndef BQ_H
+#define BQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* bq_stream_t; /* == hipStream_t; NULL = default stream */
+
+enum { BQ_OK = 0, BQ_UNSUPPORTED = 1, BQ_EINVAL = 2 };
+enum { BQ_TYPE_Q5_K = 13, BQ_TYPE_Q6_K = 14 }; /* GGML type ids (gguf.h:29-30) */
+enum { BQ_MAX_PARTS = 4, BQ_MAX_ROWS = 8 };
+
+/* Weight descriptor.  Mirrors `struct TensorW { d, dp, dm, type, K, N }`
+ * (bruce.cu:78): raw = GGUF blocks, rep = W144 (Q5_K) or W160 (Q6_K) repack or
+ * NULL, rep_min = Dm fp16 for Q5_K W144 or NULL. */
+typedef struct bq_weight {
+    const void* raw;
+    const void* rep;
+    const void* rep_min;
+    uint32_t ggml_type;
+    int32_t K, N;
+} bq_weight;
+
+/* Library set-up: reads the current device's limits.  Optional (every entry
+ * point calls it on first use); call it outside graph capture. */
+int bq_init(void);
+const char* bq_strerror(int code);
+const char* bq_version(void);
+
+/* ---- activation quantizer ------------------------------------------------
+ * Replaces k_q8_quant (bruce.cu:518-539, launched :7907) and k_q8_rows
+ * (bruce.cu:1081-1108, launched :7621); with xdh != NULL it also writes
+ * xdh = half(xd*xsum), replacing k_fill_xdh (bruce.cu:6598-6602, :7402).
+ * Per 32 values: d = amax*(1/127), id = d>0 ? 1/d : 0, q = clamp(rint(v*id),
+ * -127, 127), xsum = sum q.  Bit-exact with the reference.  K % 32 == 0. */
+int bq_quantize_q8(const float* x, int rows, int K, int8_t* xq, float* xd, int32_t* xsum,
+                   uint16_t* xdh, bq_stream_t st);
+/* xdh = half(xd*xsum) on its own (k_fill_xdh, bruce.cu:6598-6602). */
+int bq_fill_xdh(const float* xd, const int32_t* xsum, int n, uint16_t* xdh, bq_stream_t st);
+
+/* ---- decode GEMV ----------------------------------------------------------
+ * y[N] = W x for one activation row.  Replaces launch_gemv(y, w, x, st)
+ * (bruce.cu:5624-5640): Q5_K raw -> k_gemv_q5k (:384-440); Q6_K with a W160
+ * repack -> k_gemv_q6k_dp (:4452-4513), else raw Q6_K -> k_gemm_q6k (:4282). */
+int bq_gemv(float* y, const bq_weight* w, const int8_t* xq, const float* xd,
+            const int32_t* xsum, bq_stream_t st);
+
+/* Fused multi-matrix GEMV / verify GEMM: nparts (1..4) Q5_K matrices sharing
+ * K and the activation rows, rows 1..8, row r reads activation row xoff+r.
+ * Replaces launch_verify_fused (bruce.cu:7141-7229): rows==1 -> the fused GEMV
+ * k_gemv_q5k_fused (:5815-5887), rows 2..8 -> k_gemm_tc_verify_q5k (:5889-6076).
+ * Returns BQ_UNSUPPORTED (nothing enqueued) on non-Q5_K parts, mismatched K,
+ * K % 256 != 0, N % 16 != 0 or rows outside 1..8. */
+int bq_verify_fused(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
+                    const int8_t* xq, const float* xd, const int32_t* xsum, int xoff,
+                    bq_stream_t st);
+
+/* Q6_K multi-row (2..8) over the W160 repack, 1..4 parts.  Replaces
+ * launch_q6_verify_fused (bruce.cu:7231-7283; kernel k_gemm_tc_verify_q6k :6078). */
+int bq_q6_verify_fused(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
+                       const int8_t* xq, const float* xd, int xoff, bq_stream_t st);
+
+/* Q6_K GEMV over the W160 repack, rows 1..8.  Replaces launch_gemm_q6k_dp
+ * (bruce.cu:7285-7364; kernel k_gemv_q6k_dp :4452-4513). */
+int bq_gemm_q6k_dp(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
+                   int xoff, bq_stream_t st);
+
+/* Q6_K multi-row over the raw 210 B blocks, rows 1..8.  Replaces the Q6_K arm of
+ * launch_gemm_b_impl (bruce.cu:7108-7124; kernel k_gemm_q6k :4282-4362). */
+int bq_gemm_q6k_raw(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
+                    int xoff, bq_stream_t st);
+
+/* ---- prefill GEMM ----------------------------------------------------------
+ * Y_p[M][N_p] for nparts (1..4) Q5_K matrices, 128x128 tiles on int8 MFMA.
+ * Replaces try_launch_mmq (bruce.cu:7366-7419).  rows >= 96 (the reference's
+ * rule), N_p % 128 == 0, K % 256 == 0, else BQ_UNSUPPORTED.  If every part has
+ * rep/rep_min and K % 512 == 0 the W144 kernel runs (k_gemm_mmq_q5k_144
+ * :6604-6792, fp16 min term from Dm and xdh; xdh scratch [M][K/32] must be
+ * given and is written first, as k_fill_xdh does); otherwise the raw-Q5_K
+ * kernel runs (k_gemm_mmq_q5k :6367-6593, fp32 min term) and xdh is unused. */
+int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
+               const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
+               bq_stream_t st);
+
+/* Q6_K prefill GEMM over W160, rows >= 1, N % 128 == 0.  Replaces the
+ * k_gemm_mma_q6k_128 arm of launch_gemm_b (bruce.cu:7475-7521; kernel :6943-7063). */
+int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
+                    bq_stream_t st);
+
+/* Prompt-batch dispatcher.  Replaces launch_gemm_b (bruce.cu:7428-7568): rows
+ * <= 8 -> the verify / GEMV kernels above; rows > 8 -> the MFMA GEMMs, else
+ * 8-row chunks of the multi-row kernels.  Never returns BQ_UNSUPPORTED for a
+ * Q5_K/Q6_K weight with K % 256 == 0. */
+int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
+              const int32_t* xsum, uint16_t* xdh, bq_stream_t st);
+/* launch_gemm_b_fused (bruce.cu:7421-7426): one MMQ launch over the parts if
+ * possible, otherwise bq_gemm_b per part. */
+int bq_gemm_b_fused(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
+                    const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
+                    bq_stream_t st);
+
+/* ---- load-time repacks -----------------------------------------------------
+ * Q5_K raw -> W144 + Dm (k_q5k_prepack144, bruce.cu:5747-5789, launched by
+ * q5k_prepack_launch :4832-4838).  Bit-exact with the reference. */
+int bq_repack_q5k(const void* raw, int K, int N, void* w144, uint16_t* dm, bq_stream_t st);
+size_t bq_repack_q5k_bytes(int K, int N);     /* W144 bytes: (K/128)*N*144 */
+size_t bq_repack_q5k_min_bytes(int K, int N); /* Dm bytes:   N*(K/32)*2   */
+/* Q6_K raw -> W160 on the device (device twin of q6k_repack_host). */
+int bq_repack_q6k(const void* raw, int K, int N, void* w160, bq_stream_t st);
+/* Host version: q6k_repack_host (bruce.cu:4783-4811), same bytes. */
+int bq_repack_q6k_host(const void* raw, int K, int N, void* w160);
+size_t bq_repack_q6k_bytes(int K, int N);     /* N*(K/128)*160 */
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BQ_H */

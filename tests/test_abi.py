@@ -1,0 +1,64 @@
+"""CPU checks of the C ABI: libbq.so loads, exports every function that
+include/bq.h declares, and its host-only entry points match the oracle."""
+import ctypes
+import os
+import re
+
+import numpy as np
+
+from helpers import weights
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "bq.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_matches_exports():
+    import bq
+    L = bq.load()
+    names = declared_functions()
+    assert len(names) >= 18
+    for n in names:
+        assert hasattr(L, n), n
+    assert sorted(names) == sorted(bq.EXPORTS)
+
+
+def test_library_is_gfx950_hip():
+    import bq
+    data = open(bq.LIB_PATH, "rb").read()
+    assert b"gfx950" in data
+    assert bq.load().bq_version().decode().startswith("bq ")
+
+
+def test_strerror():
+    import bq
+    assert bq.strerror(0) == "ok"
+    assert "unsupported" in bq.strerror(1)
+
+
+def test_repack_q6k_host_matches_oracle(oracle):
+    import bq
+    for N, K in [(4, 256), (17, 1024)]:
+        raw = weights(77 + N, N, K, "q6k")
+        got = bq.repack_q6k_host(raw, K, N)
+        assert np.array_equal(got, oracle.repack_q6k_160(raw, K))
+
+
+def test_repack_sizes():
+    import bq
+    L = bq.load()
+    assert L.bq_repack_q5k_bytes(3072, 9216) == 31850496
+    assert L.bq_repack_q5k_min_bytes(3072, 9216) == 1769472
+    assert L.bq_repack_q6k_bytes(9216, 3072) == 35389440
+
+
+def test_host_repack_rejects_bad_shape():
+    import bq
+    L = bq.load()
+    buf = (ctypes.c_uint8 * 1024)()
+    assert L.bq_repack_q6k_host(buf, 100, 1, buf) == bq.BQ_EINVAL
+    assert L.bq_repack_q6k_host(None, 256, 1, buf) == bq.BQ_EINVAL

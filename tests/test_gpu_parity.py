@@ -1,0 +1,331 @@
+"""GPU parity of libbq (through its C ABI) against the CPU oracle.
+
+Tolerance (stated by BASELINE's north star): integer dots, codes and repacked
+layouts bit-exact; fp32 outputs within max relative error 1e-4, measured
+normwise per activation row (max |y - ref| / max |ref| over the row), against
+the oracle evaluated in double precision.
+"""
+import numpy as np
+import pytest
+
+from helpers import acts, dev, host, weights
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def _xq_dev(xq, xd, xs):
+    return dev(xq), dev(xd), dev(xs)
+
+
+# ---------------------------------------------------------------- quantizer
+@pytest.mark.parametrize("M,K", [(1, 3072), (3, 9216), (2048, 3072), (5, 32)])
+def test_quantizer_bitexact(bq, oracle, M, K):
+    import torch
+    x, (xq, xd, xs) = acts(100 + M, M, K)
+    x[0, :32] = 0.0                       # an all-zero group
+    if K > 64:
+        x[0, 32:64] = 0.0
+        x[0, 40] = 1e-30                  # a lone tiny value
+    xq, xd, xs = oracle.q8_rows(x)
+    gq, gd, gs, gh = bq.quantize_q8(dev(x), with_xdh=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(gq), xq)
+    assert np.array_equal(host(gd).view(np.uint32), xd.view(np.uint32))
+    assert np.array_equal(host(gs), xs)
+    assert np.array_equal(host(gh).view(np.uint16), oracle.fill_xdh(xd, xs))
+    gh2 = bq.fill_xdh(gd, gs)
+    assert np.array_equal(host(gh2).view(np.uint16), oracle.fill_xdh(xd, xs))
+
+
+# ---------------------------------------------------------------- repacks
+@pytest.mark.parametrize("N,K", [(128, 512), (300, 3072)])
+def test_repack_bitexact(bq, oracle, N, K):
+    import torch
+    raw5 = weights(200 + N, N, K, "q5k")
+    raw6 = weights(300 + N, N, K, "q6k")
+    w144, dm = bq.repack_q5k(dev(raw5), K, N)
+    w160 = bq.repack_q6k(dev(raw6), K, N)
+    torch.cuda.synchronize()
+    r144, rdm = oracle.repack_q5k_144(raw5, K)
+    r160 = oracle.repack_q6k_160(raw6, K)
+    assert np.array_equal(host(w144), r144)
+    assert np.array_equal(host(dm).view(np.uint16), rdm)
+    assert np.array_equal(host(w160), r160)
+
+
+# ---------------------------------------------------------------- integer dots (KAT)
+def test_q5k_int_dots_bitexact(bq, oracle):
+    """d = 1, dmin = 0 and a single nonzero 6-bit scale (=1) in group n % (K/32):
+    with xd = 1 the kernel output is exactly that group's integer dot."""
+    import torch
+    K, N = 1024, 256
+    raw = weights(401, N, K, "q5k").reshape(N, K // 256, 176).copy()
+    raw[:, :, 0:2] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)
+    raw[:, :, 2:4] = 0
+    raw[:, :, 4:16] = 0
+    for n in range(N):
+        g = n % (K // 32)
+        sb, j = g // 8, g % 8
+        if j < 4:
+            raw[n, sb, 4 + j] = 1
+        else:
+            raw[n, sb, 8 + j] = 1  # low nibble of scales[j + 4]
+    raw = raw.reshape(N, -1)
+    _, (xq, xd, xs) = acts(402, 1, K)
+    xd = np.ones_like(xd)
+    y = torch.empty(N, device="cuda")
+    w = bq.make_weight(dev(raw), bq.TYPE_Q5_K, K, N)
+    gq, gd, gs = _xq_dev(xq, xd, xs)
+    bq.gemv(y, w, gq, gd, gs)
+    torch.cuda.synchronize()
+    dots = oracle.dots_q5k(raw, xq)[0]
+    want = np.array([dots[n, n % (K // 32)] for n in range(N)], np.float32)
+    assert np.array_equal(host(y), want)
+
+
+def test_q6k_int_dots_bitexact(bq, oracle):
+    import torch
+    K, N = 1024, 256
+    raw = weights(403, N, K, "q6k").reshape(N, K // 256, 210).copy()
+    raw[:, :, 208:210] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)
+    raw[:, :, 192:208] = 0
+    for n in range(N):
+        g16 = n % (K // 16)
+        raw[n, g16 // 16, 192 + g16 % 16] = 1
+    raw = raw.reshape(N, -1)
+    _, (xq, xd, xs) = acts(404, 1, K)
+    xd = np.ones_like(xd)
+    dots = oracle.dots16_q6k(raw, xq)[0]
+    want = np.array([dots[n, n % (K // 16)] for n in range(N)], np.float32)
+    gq, gd = dev(xq), dev(xd)
+    y = torch.empty(N, device="cuda")
+    bq.gemm_q6k_raw(y, bq.make_weight(dev(raw), bq.TYPE_Q6_K, K, N), 1, gq, gd)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(y), want)
+    rep = bq.repack_q6k(dev(raw), K, N)
+    y2 = torch.empty(N, device="cuda")
+    bq.gemm_q6k_dp(y2, bq.make_weight(None, bq.TYPE_Q6_K, K, N, rep=rep), 1, gq, gd)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(y2), want)
+
+
+# ---------------------------------------------------------------- GEMV Q5_K
+@pytest.mark.parametrize("N,K", [(256, 1024), (3072, 3072), (400, 4096), (64, 2560)])
+def test_gemv_q5k(bq, oracle, N, K):
+    import torch
+    raw = weights(500 + N, N, K, "q5k")
+    _, (xq, xd, xs) = acts(501, 1, K)
+    ref = oracle.gemm_q5k(raw, xq, xd, xs)
+    y = torch.full((N,), float("nan"), device="cuda")
+    bq.gemv(y, bq.make_weight(dev(raw), bq.TYPE_Q5_K, K, N), *_xq_dev(xq, xd, xs))
+    torch.cuda.synchronize()
+    assert oracle.normwise_err(host(y), ref) < TOL
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 8])
+def test_verify_fused_parts(bq, oracle, rows):
+    """Config-2/5 style fused parts (gate+up, q/k/gate/v) and 2..8 verify rows."""
+    import torch
+    K = 3072
+    Ns = [512, 128, 1024, 256]
+    raws = [weights(600 + i, n, K, "q5k") for i, n in enumerate(Ns)]
+    _, (xq, xd, xs) = acts(610 + rows, rows + 1, K)
+    ws = [bq.make_weight(dev(r), bq.TYPE_Q5_K, K, n) for r, n in zip(raws, Ns)]
+    ys = [torch.full((rows, n), float("nan"), device="cuda") for n in Ns]
+    gq, gd, gs = _xq_dev(xq, xd, xs)
+    assert bq.verify_fused(ys, ws, rows, gq, gd, gs, xoff=1) == bq.BQ_OK
+    torch.cuda.synchronize()
+    for r, y in zip(raws, ys):
+        ref = oracle.gemm_q5k(r, xq[1:], xd[1:], xs[1:])
+        assert oracle.normwise_err(host(y), ref) < TOL
+
+
+def test_verify_config3_full(bq, oracle):
+    """Config 3: Q5_K 9216x3072, rows 1/2/4/8 sharing one weight stream."""
+    import torch
+    K, N = 3072, 9216
+    raw = weights(700, N, K, "q5k")
+    _, (xq, xd, xs) = acts(701, 8, K)
+    ref = oracle.gemm_q5k(raw, xq, xd, xs)
+    w = bq.make_weight(dev(raw), bq.TYPE_Q5_K, K, N)
+    gq, gd, gs = _xq_dev(xq, xd, xs)
+    for rows in (1, 2, 4, 8):
+        y = torch.full((rows, N), float("nan"), device="cuda")
+        assert bq.verify_fused([y], [w], rows, gq, gd, gs) == bq.BQ_OK
+        torch.cuda.synchronize()
+        assert oracle.normwise_err(host(y), ref[:rows]) < TOL, rows
+
+
+def test_verify_unsupported(bq):
+    import torch
+    K = 512
+    raw = torch.zeros((24, K // 256 * 176), dtype=torch.uint8, device="cuda")
+    w = bq.make_weight(raw, bq.TYPE_Q5_K, K, 24)     # N % 16 != 0
+    y = torch.zeros((1, 24), device="cuda")
+    xq = torch.zeros((9, K), dtype=torch.int8, device="cuda")
+    xd = torch.zeros((9, K // 32), device="cuda")
+    xs = torch.zeros((9, K // 32), dtype=torch.int32, device="cuda")
+    assert bq.verify_fused([y], [w], 1, xq, xd, xs) == bq.BQ_UNSUPPORTED
+    w2 = bq.make_weight(raw[:16], bq.TYPE_Q5_K, K, 16)
+    assert bq.verify_fused([y], [w2], 9, xq, xd, xs) == bq.BQ_UNSUPPORTED   # rows > 8
+    w6 = bq.make_weight(raw[:16], bq.TYPE_Q6_K, K, 16)
+    assert bq.verify_fused([y], [w6], 1, xq, xd, xs) == bq.BQ_UNSUPPORTED   # not Q5_K
+
+
+# ---------------------------------------------------------------- Q6_K GEMV
+@pytest.mark.parametrize("N,K,rows", [(3072, 9216, 1), (256, 3072, 3), (512, 1024, 8), (130, 768, 2)])
+def test_q6k_gemv(bq, oracle, N, K, rows):
+    import torch
+    raw = weights(800 + N, N, K, "q6k")
+    _, (xq, xd, xs) = acts(801, rows, K)
+    ref = oracle.gemm_q6k(raw, xq, xd)
+    graw = dev(raw)
+    gq, gd = dev(xq), dev(xd)
+    y = torch.full((rows, N), float("nan"), device="cuda")
+    bq.gemm_q6k_raw(y, bq.make_weight(graw, bq.TYPE_Q6_K, K, N), rows, gq, gd)
+    torch.cuda.synchronize()
+    assert oracle.normwise_err(host(y), ref) < TOL
+    rep = bq.repack_q6k(graw, K, N)
+    y2 = torch.full((rows, N), float("nan"), device="cuda")
+    bq.gemm_q6k_dp(y2, bq.make_weight(graw, bq.TYPE_Q6_K, K, N, rep=rep), rows, gq, gd)
+    torch.cuda.synchronize()
+    assert oracle.normwise_err(host(y2), ref) < TOL
+    if rows == 1:
+        y3 = torch.full((N,), float("nan"), device="cuda")
+        bq.gemv(y3, bq.make_weight(graw, bq.TYPE_Q6_K, K, N, rep=rep), gq, gd, None)
+        torch.cuda.synchronize()
+        assert oracle.normwise_err(host(y3), ref) < TOL
+
+
+def test_q6_verify_fused(bq, oracle):
+    import torch
+    K = 1024
+    Ns = [256, 128]
+    raws = [weights(900 + i, n, K, "q6k") for i, n in enumerate(Ns)]
+    _, (xq, xd, xs) = acts(902, 6, K)
+    ws = []
+    for r, n in zip(raws, Ns):
+        g = dev(r)
+        ws.append(bq.make_weight(g, bq.TYPE_Q6_K, K, n, rep=bq.repack_q6k(g, K, n)))
+    ys = [torch.full((6, n), float("nan"), device="cuda") for n in Ns]
+    assert bq.q6_verify_fused(ys, ws, 6, dev(xq), dev(xd)) == bq.BQ_OK
+    torch.cuda.synchronize()
+    for r, y in zip(raws, ys):
+        assert oracle.normwise_err(host(y), oracle.gemm_q6k(r, xq, xd)) < TOL
+
+
+# ---------------------------------------------------------------- prefill GEMM
+def _mmq_case(bq, oracle, seed, M, Ns, K, prepacked):
+    import torch
+    raws = [weights(seed + i, n, K, "q5k") for i, n in enumerate(Ns)]
+    _, (xq, xd, xs) = acts(seed + 50, M, K)
+    ws, keep = [], []
+    for r, n in zip(raws, Ns):
+        g = dev(r)
+        if prepacked:
+            w144, dm = bq.repack_q5k(g, K, n)
+            ws.append(bq.make_weight(g, bq.TYPE_Q5_K, K, n, rep=w144, rep_min=dm))
+        else:
+            ws.append(bq.make_weight(g, bq.TYPE_Q5_K, K, n))
+    ys = [torch.full((M, n), float("nan"), device="cuda") for n in Ns]
+    xdh = torch.empty((M, K // 32), dtype=torch.int16, device="cuda")
+    gq, gd, gs = _xq_dev(xq, xd, xs)
+    assert bq.try_mmq(ys, ws, M, gq, gd, gs, xdh) == bq.BQ_OK
+    torch.cuda.synchronize()
+    for r, n, y in zip(raws, Ns, ys):
+        if prepacked:
+            w144, dm = oracle.repack_q5k_144(r, K)
+            ref = oracle.gemm_q5k_144(w144, dm, xq, xd, oracle.fill_xdh(xd, xs), n)
+        else:
+            ref = oracle.gemm_q5k(r, xq, xd, xs)
+        assert oracle.normwise_err(host(y), ref) < TOL
+
+
+@pytest.mark.parametrize("prepacked", [False, True])
+def test_mmq_q5k(bq, oracle, prepacked):
+    _mmq_case(bq, oracle, 1000, 256, [256], 1024, prepacked)
+
+
+@pytest.mark.parametrize("prepacked", [False, True])
+def test_mmq_q5k_ragged_parts(bq, oracle, prepacked):
+    # 200 rows (not a multiple of the 128 tile), three parts
+    _mmq_case(bq, oracle, 1100, 200, [128, 256, 128], 1536, prepacked)
+
+
+def test_mmq_unsupported(bq):
+    import torch
+    K = 512
+    raw = torch.zeros((128, K // 256 * 176), dtype=torch.uint8, device="cuda")
+    w = bq.make_weight(raw, bq.TYPE_Q5_K, K, 128)
+    y = torch.zeros((64, 128), device="cuda")
+    xq = torch.zeros((64, K), dtype=torch.int8, device="cuda")
+    xd = torch.zeros((64, K // 32), device="cuda")
+    xs = torch.zeros((64, K // 32), dtype=torch.int32, device="cuda")
+    assert bq.try_mmq([y], [w], 64, xq, xd, xs) == bq.BQ_UNSUPPORTED  # rows < 96
+
+
+def test_mmq_q6k(bq, oracle):
+    import torch
+    K, N, M = 1024, 256, 160
+    raw = weights(1200, N, K, "q6k")
+    _, (xq, xd, xs) = acts(1201, M, K)
+    g = dev(raw)
+    w = bq.make_weight(g, bq.TYPE_Q6_K, K, N, rep=bq.repack_q6k(g, K, N))
+    y = torch.full((M, N), float("nan"), device="cuda")
+    bq.gemm_q6k_mma(y, w, M, dev(xq), dev(xd))
+    torch.cuda.synchronize()
+    assert oracle.normwise_err(host(y), oracle.gemm_q6k(raw, xq, xd)) < TOL
+
+
+def test_mmq_config4_full_slices(bq, oracle):
+    """Config 4 at full size (M = 2048, N = 9216, K = 3072, both tiers); the
+    oracle checks a sample of 48 token rows x 192 weight rows of the output."""
+    import torch
+    K, N, M = 3072, 9216, 2048
+    raw = weights(1300, N, K, "q5k")
+    _, (xq, xd, xs) = acts(1301, M, K)
+    g = dev(raw)
+    w144, dm = bq.repack_q5k(g, K, N)
+    gq, gd, gs = _xq_dev(xq, xd, xs)
+    xdh = torch.empty((M, K // 32), dtype=torch.int16, device="cuda")
+    rng = np.random.default_rng(7)
+    mi = np.sort(rng.choice(M, 48, replace=False))
+    ni = np.sort(rng.choice(N, 192, replace=False))
+    for prepacked in (False, True):
+        w = bq.make_weight(g, bq.TYPE_Q5_K, K, N, rep=w144 if prepacked else None,
+                           rep_min=dm if prepacked else None)
+        y = torch.full((M, N), float("nan"), device="cuda")
+        assert bq.try_mmq([y], [w], M, gq, gd, gs, xdh) == bq.BQ_OK
+        torch.cuda.synchronize()
+        yh = host(y)
+        assert np.isfinite(yh).all()
+        sub = raw[ni]
+        if prepacked:
+            r144, rdm = oracle.repack_q5k_144(sub, K)
+            ref = oracle.gemm_q5k_144(r144, rdm, xq[mi], xd[mi], oracle.fill_xdh(xd[mi], xs[mi]), len(ni))
+        else:
+            ref = oracle.gemm_q5k(sub, xq[mi], xd[mi], xs[mi])
+        assert oracle.normwise_err(yh[np.ix_(mi, ni)], ref) < TOL, prepacked
+
+
+# ---------------------------------------------------------------- dispatcher
+@pytest.mark.parametrize("rows", [3, 20, 130])
+def test_gemm_b_dispatch(bq, oracle, rows):
+    import torch
+    K, N = 1024, 256
+    raw5 = weights(1400, N, K, "q5k")
+    raw6 = weights(1401, N, K, "q6k")
+    _, (xq, xd, xs) = acts(1402, rows, K)
+    gq, gd, gs = _xq_dev(xq, xd, xs)
+    xdh = torch.empty((rows, K // 32), dtype=torch.int16, device="cuda")
+    g5 = dev(raw5)
+    y = torch.full((rows, N), float("nan"), device="cuda")
+    bq.gemm_b(y, bq.make_weight(g5, bq.TYPE_Q5_K, K, N), rows, gq, gd, gs, xdh)
+    torch.cuda.synchronize()
+    assert oracle.normwise_err(host(y), oracle.gemm_q5k(raw5, xq, xd, xs)) < TOL
+    g6 = dev(raw6)
+    y6 = torch.full((rows, N), float("nan"), device="cuda")
+    bq.gemm_b(y6, bq.make_weight(g6, bq.TYPE_Q6_K, K, N, rep=bq.repack_q6k(g6, K, N)), rows, gq, gd, gs, xdh)
+    torch.cuda.synchronize()
+    assert oracle.normwise_err(host(y6), oracle.gemm_q6k(raw6, xq, xd)) < TOL
