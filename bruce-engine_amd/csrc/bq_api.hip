@@ -38,6 +38,7 @@ int ensure_init() {
         if (hipGetDeviceProperties(&prop, dev) != hipSuccess) { g_init_status = -(int)hipErrorNoDevice; return; }
         g_dev.lds_per_block = prop.sharedMemPerBlock;
         g_dev.cus = prop.multiProcessorCount;
+        gemv_set_cus(g_dev.cus);
     });
     return g_init_status;
 }

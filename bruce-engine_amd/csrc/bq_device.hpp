@@ -41,7 +41,11 @@ BQ_DEV float as_float(uint32_t u) { return __builtin_bit_cast(float, u); }
 BQ_DEV int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 // 16-byte load of read-once weight data
+#ifdef BQ_EXP_NT
+BQ_DEV u32x4 ld16(const void* p) { return __builtin_nontemporal_load((const u32x4*)p); }
+#else
 BQ_DEV u32x4 ld16(const void* p) { return *(const u32x4*)p; }
+#endif
 BQ_DEV u32x4 ld16_stream(const void* p) {
     return __builtin_nontemporal_load((const u32x4*)p);
 }

@@ -6,33 +6,32 @@
 //   Q6_K  y[n] = sum_{16-groups} xd[g32] * (d*sc16) * sum (q-32)*xq
 //         k_gemm_q6k :4282-4362 (raw 210 B), k_gemv_q6k_dp :4452-4513 (160 B repack)
 //
-// MI355X design (not the reference's warp mapping):
-//   * The weight matrix is a flat stream of 16-byte chunks.  A wave owns a tile
-//     of T consecutive weight rows of one part and walks its "lane tasks"
-//     (row, block, chunk) in address order, 64 per step, so every load
-//     instruction of a wave covers a dense ~1.4 KiB span of HBM.
-//   * Q5_K lane task = one 16-byte chunk of qs (two 16-value halves of a
-//     sub-block pair) + the matching 16 bytes of qh + the 16-byte block header
-//     (d, dmin, scales).  Three 128-bit loads, 32 values, 8 v_dot4_i32_i8.
-//   * A row has K/32 lane tasks; T rows per tile with T*K/32 % 64 == 0 keep
-//     every lane busy (K = 3072 -> T = 2, three full steps).
-//   * Activations (int8 codes, fp32 scales, sums) of all MR rows are staged in
-//     LDS once per workgroup; every weight byte is read once for all MR rows.
-//   * Per-row partial sums are reduced across the wave with xor shuffles.
+// MI355X design (one decode GEMV is 6-40 MB: about one HBM latency x
+// bandwidth product, so every load is issued up front and consumed in order):
+//   * Lane task = 64 consecutive weight values of one row (two Q5_K sub-blocks,
+//     half a Q6_K repack stage, or a 4 x 16 slice of a raw Q6_K block); a row
+//     has K/64 tasks.
+//   * One weight row per 16-lane DPP row: a wave owns 4 rows ("tile"), lanes
+//     16g..16g+15 walk the tasks of row g, 16 per step, at most 3 steps per
+//     wave (longer rows are split over KS waves of one workgroup).  Row sums
+//     are reduced with four DPP row shifts; K slices are combined through LDS.
+//   * Activations are copied to LDS with direct-to-LDS DMA loads issued before
+//     the weight loads; each wave then waits only for its own DMA (vmcnt =
+//     number of weight loads issued after it) before the workgroup barrier, so
+//     all weight bytes are in flight before any wave waits, and step s is
+//     computed as soon as its loads have returned.
 #include "bq_device.hpp"
 #include "bq_internal.hpp"
 
+#include <stdlib.h>
+
+#include <algorithm>
 #include <type_traits>
 
 namespace bq {
 
-// rows per wave tile: every row has K/32 lane tasks, so T*K/32 % 64 == 0 keeps
-// all 64 lanes busy on every step (K % 2048 -> 1, K % 1024 -> 2, else 4)
-static int tile_rows(int K) {
-    if (K % 2048 == 0) return 1;
-    if (K % 1024 == 0) return 2;
-    return 4;
-}
+constexpr int kRowsPerTile = 4;    // one row per 16-lane DPP row
+constexpr int kTasksPerStep = 16;  // tasks of one row per step
 
 BQ_DEV int find_part(const PartTable& pt, int tile) {
     int p = 0;
@@ -42,331 +41,422 @@ BQ_DEV int find_part(const PartTable& pt, int tile) {
     return p;
 }
 
-// ---------------------------------------------------------------------------
-// Weight-format policies.  A lane task covers 32 values of one weight row:
-//   Task  -- the raw bytes a lane loads for it (registers)
-//   load  -- issue the task's global loads
-//   dot   -- its contribution to activation row m (LDS-staged activations)
-// ---------------------------------------------------------------------------
+// sum over the 16 lanes of a DPP row; lane 15 of the row ends with the total
+BQ_DEV float row16_sum(float v) {
+    int x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true));  // row_shr:1
+    x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true));  // row_shr:2
+    x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true));  // row_shr:4
+    x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true));  // row_shr:8
+    return v;
+}
+
+// 4 bytes of 5-bit codes of Q5_K sub-block j: low/high nibble (hi) of qs with
+// bit j of each qh byte as bit 4.  alignbit(qh, qh, j - 4) rotates bit j of
+// every byte onto bit 4 of the same byte.
+BQ_DEV uint32_t q5_codes(uint32_t qs, uint32_t qh, int j, bool hi) {
+    const uint32_t nib = (hi ? (qs >> 4) : qs) & 0x0F0F0F0Fu;
+    const uint32_t rot = __builtin_amdgcn_alignbit(qh, qh, (uint32_t)(j - 4) & 31u);
+    return (rot & 0x10101010u) | nib;
+}
+
 struct ActLds {            // activations of MR rows staged in LDS
     const int8_t* x;       // [MR][K] int8 codes
     const float* xd;       // [MR][K/32]
-    const float* aux;      // Q5_K: float(xsum) [MR][K/32]; Q6_K raw: 32*sum16 as int [MR][K/16]
+    const int32_t* xs;     // Q5_K only: xsum [MR][K/32]
 };
 
+// ---------------------------------------------------------------------------
+// Weight-format policies: Task = registers one lane loads for one 64-value
+// task; load() issues them, dot() adds the task's contribution to each
+// activation row.
+// ---------------------------------------------------------------------------
 struct FmtQ5K {
-    static constexpr int kAuxPerRow32 = 1;   // float(xsum) per 32-group
-    struct Task { u32x4 hdr, qh, qs; };
-    // r = index of the task inside its row: super-block r >> 3, qs chunk r & 7
-    static BQ_DEV void load(Task& t, const uint8_t* W, int row, int r, int K) {
-        const uint8_t* blk = W + ((size_t)row * (K >> 8) + (r >> 3)) * kQ5Bytes;
-        const int c = r & 7;
-        t.hdr = ld16(blk);
-        t.qh = ld16(blk + 16 + 16 * (c & 1));
-        t.qs = ld16(blk + 48 + 16 * c);
+    static constexpr int kLoads = 5;  // VMEM instructions per task
+    struct Task { u32x4 hdr, qh0, qh1, qs0, qs1; };
+    // task t: super-block t >> 2, sub-block pair t & 3
+    static BQ_DEV void load(Task& a, const uint8_t* row, int t) {
+        const uint8_t* blk = row + (t >> 2) * kQ5Bytes;
+        const int jp = t & 3;
+        a.hdr = ld16(blk);
+        a.qh0 = ld16(blk + 16);
+        a.qh1 = ld16(blk + 32);
+        a.qs0 = ld16(blk + 48 + 32 * jp);
+        a.qs1 = ld16(blk + 64 + 32 * jp);
     }
-    // Precomputed per-task operands, shared by all activation rows.
-    struct Prep { uint32_t u0[4], u1[4]; float ds0, ds1, dm0, dm1; int xo, g0; };
-    static BQ_DEV void prep(Prep& q, const Task& t, int r) {
-        const int sb = r >> 3, c = r & 7;
-        const int j0 = (c >> 1) * 2, j1 = j0 + 1, half = c & 1;
+    // 6-bit scale / min of sub-block j from the header words (y = scales[0..3],
+    // z = scales[4..7], w = scales[8..11]) with two 4+2-bit field extracts each:
+    // j < 4: sc = y.byte(j) & 63, m = z.byte(j) & 63; j >= 4: low nibbles of
+    // w.byte(j-4), top two bits from y.byte(j-4) / z.byte(j-4).
+    static BQ_DEV void scale_min(const u32x4& hdr, int j, uint32_t& sc, uint32_t& m) {
+        const bool lo = j < 4;
+        const uint32_t b = 8u * (uint32_t)(j & 3);
+        const uint32_t s2 = lo ? b + 4 : b + 6;
+        sc = __builtin_amdgcn_ubfe(lo ? hdr.y : hdr.w, b, 4) | (__builtin_amdgcn_ubfe(hdr.y, s2, 2) << 4);
+        m = __builtin_amdgcn_ubfe(lo ? hdr.z : hdr.w, lo ? b : b + 4, 4) | (__builtin_amdgcn_ubfe(hdr.z, s2, 2) << 4);
+    }
+    template <int MR>
+    static BQ_DEV void dot(const Task& a, const uint8_t*, int t, const ActLds& act, int K, float (&acc)[MR]) {
+        const int jp = t & 3, j0 = 2 * jp, j1 = j0 + 1;
         uint32_t sc0, m0, sc1, m1;
-        q5k_scale_min(t.hdr.y, t.hdr.z, t.hdr.w, j0, sc0, m0);
-        q5k_scale_min(t.hdr.y, t.hdr.z, t.hdr.w, j1, sc1, m1);
-        const float d = h2f(t.hdr.x & 0xFFFF), dmin = h2f(t.hdr.x >> 16);
-        q.ds0 = d * (float)sc0;
-        q.ds1 = d * (float)sc1;
-        // the min term of a sub-block is added once, by the lane holding its first half
-        q.dm0 = half ? 0.f : dmin * (float)m0;
-        q.dm1 = half ? 0.f : dmin * (float)m1;
+        scale_min(a.hdr, j0, sc0, m0);
+        scale_min(a.hdr, j1, sc1, m1);
+        const float d = h2f(a.hdr.x & 0xFFFF), dmin = h2f(a.hdr.x >> 16);
+        const float ds0 = d * (float)sc0, ds1 = d * (float)sc1;
+        const float dm0 = dmin * (float)m0, dm1 = dmin * (float)m1;
+        uint32_t u0[8], u1[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            q.u0[i] = (t.qs[i] & 0x0F0F0F0Fu) | (((t.qh[i] >> j0) & 0x01010101u) << 4);
-            q.u1[i] = ((t.qs[i] >> 4) & 0x0F0F0F0Fu) | (((t.qh[i] >> j1) & 0x01010101u) << 4);
+            u0[i] = q5_codes(a.qs0[i], a.qh0[i], j0, false);
+            u0[i + 4] = q5_codes(a.qs1[i], a.qh1[i], j0, false);
+            u1[i] = q5_codes(a.qs0[i], a.qh0[i], j1, true);
+            u1[i + 4] = q5_codes(a.qs1[i], a.qh1[i], j1, true);
         }
-        q.g0 = sb * 8 + j0;
-        q.xo = sb * 256 + 32 * j0 + 16 * half;
-    }
-    static BQ_DEV float dot(const Prep& q, const ActLds& a, int m, int K) {
         const int nb = K >> 5;
-        const u32x4 x0 = *(const u32x4*)(a.x + m * K + q.xo);
-        const u32x4 x1 = *(const u32x4*)(a.x + m * K + q.xo + 32);
-        int s0 = 0, s1 = 0;
+        const int g0 = (t >> 2) * 8 + j0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            s0 = dot4((int)q.u0[i], (int)x0[i], s0);
-            s1 = dot4((int)q.u1[i], (int)x1[i], s1);
-        }
-        const float* xd = a.xd + m * nb + q.g0;
-        const float* xs = a.aux + m * nb + q.g0;
-        return xd[0] * (q.ds0 * (float)s0 - q.dm0 * xs[0]) + xd[1] * (q.ds1 * (float)s1 - q.dm1 * xs[1]);
-    }
-};
-
-struct FmtQ6KRaw {
-    // task r: super-block r >> 3, ql chunk c = r & 7 holding values
-    // 128h + 32*ulo + l0 .. +15 (low nibbles) and quarter ulo + 2 (high nibbles)
-    struct Task { u32x4 ql, qh, sc; uint32_t d; };
-    static BQ_DEV void load(Task& t, const uint8_t* W, int row, int r, int K) {
-        const uint8_t* blk = W + ((size_t)row * (K >> 8) + (r >> 3)) * kQ6Bytes;
-        const int c = r & 7, h = c >> 2, l0 = 16 * (c & 1);
-        t.ql = ld16_a2(blk + 16 * c);
-        t.qh = ld16_a2(blk + 128 + 32 * h + l0);
-        t.sc = ld16_a2(blk + 192);
-        t.d = *(const uint16_t*)(blk + 208);
-    }
-    struct Prep { uint32_t qa[4], qb[4]; float sA, sB; int kA; };
-    static BQ_DEV void prep(Prep& q, const Task& t, int r) {
-        const int sb = r >> 3, c = r & 7, h = c >> 2, ulo = (c >> 1) & 1, l0 = 16 * (c & 1);
-        const int gA = 8 * h + 2 * ulo + (c & 1);  // 16-value group in the block; B = gA + 4
-        const float d = h2f(t.d);
-        const int bA = (int)(int8_t)(t.sc[gA >> 2] >> (8 * (gA & 3)));
-        const int bB = (int)(int8_t)(t.sc[(gA + 4) >> 2] >> (8 * (gA & 3)));
-        q.sA = d * (float)bA;
-        q.sB = d * (float)bB;
+        for (int m = 0; m < MR; ++m) {
+            const int8_t* xp = act.x + m * K + 32 * g0;
+            const u32x4 x0 = *(const u32x4*)(xp), x1 = *(const u32x4*)(xp + 16);
+            const u32x4 x2 = *(const u32x4*)(xp + 32), x3 = *(const u32x4*)(xp + 48);
+            int s0 = 0, s1 = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            q.qa[i] = (t.ql[i] & 0x0F0F0F0Fu) | (((t.qh[i] >> (2 * ulo)) & 0x03030303u) << 4);
-            q.qb[i] = ((t.ql[i] >> 4) & 0x0F0F0F0Fu) | (((t.qh[i] >> (2 * ulo + 4)) & 0x03030303u) << 4);
+            for (int i = 0; i < 4; ++i) {
+                s0 = dot4((int)u0[i], (int)x0[i], s0);
+                s0 = dot4((int)u0[i + 4], (int)x1[i], s0);
+                s1 = dot4((int)u1[i], (int)x2[i], s1);
+                s1 = dot4((int)u1[i + 4], (int)x3[i], s1);
+            }
+            const float2 xdv = *(const float2*)(act.xd + m * nb + g0);
+            const int2 xsv = *(const int2*)(act.xs + m * nb + g0);
+            acc[m] += xdv.x * (ds0 * (float)s0 - dm0 * (float)xsv.x) + xdv.y * (ds1 * (float)s1 - dm1 * (float)xsv.y);
         }
-        q.kA = sb * 256 + 128 * h + 32 * ulo + l0;
-    }
-    // codes are q in 0..63: dot(q - 32, x) = dot(q, x) - 32 * sum16(x)
-    static BQ_DEV float dot(const Prep& q, const ActLds& a, int m, int K) {
-        const int nb = K >> 5, n16 = K >> 4;
-        const u32x4 x0 = *(const u32x4*)(a.x + m * K + q.kA);
-        const u32x4 x1 = *(const u32x4*)(a.x + m * K + q.kA + 64);
-        const int* s16 = (const int*)a.aux + m * n16 + (q.kA >> 4);
-        int s0 = -s16[0], s1 = -s16[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            s0 = dot4((int)q.qa[i], (int)x0[i], s0);
-            s1 = dot4((int)q.qb[i], (int)x1[i], s1);
-        }
-        const float* xd = a.xd + m * nb + (q.kA >> 5);
-        return xd[0] * q.sA * (float)s0 + xd[2] * q.sB * (float)s1;
     }
 };
 
 struct FmtQ6KRep {
-    // task r: stage r >> 2, 32 values at 32*(r & 3) (two 16-value scale groups)
-    struct Task { u32x4 wa, wb; float2 sc; };
-    static BQ_DEV void load(Task& t, const uint8_t* W, int row, int r, int K) {
-        const uint8_t* st = W + ((size_t)row * (K >> 7) + (r >> 2)) * kW160;
-        const int c4 = r & 3;
-        t.wa = ld16(st + 32 * c4);
-        t.wb = ld16(st + 32 * c4 + 16);
-        t.sc = *(const float2*)(st + 128 + 8 * c4);
-    }
-    struct Prep { u32x4 wa, wb; float2 sc; int k; };
-    static BQ_DEV void prep(Prep& q, const Task& t, int r) {
-        q.wa = t.wa;
-        q.wb = t.wb;
-        q.sc = t.sc;
-        q.k = (r >> 2) * 128 + 32 * (r & 3);
-    }
-    static BQ_DEV float dot(const Prep& q, const ActLds& a, int m, int K) {
-        const u32x4 x0 = *(const u32x4*)(a.x + m * K + q.k);
-        const u32x4 x1 = *(const u32x4*)(a.x + m * K + q.k + 16);
-        int s0 = 0, s1 = 0;
+    static constexpr int kLoads = 5;
+    struct Task { u32x4 c[4]; f32x4 sc; };
+    // task t: stage t >> 1, half t & 1 (64 codes + the 4 scales of their 16-value groups)
+    static BQ_DEV void load(Task& a, const uint8_t* row, int t) {
+        const uint8_t* st = row + (t >> 1) * kW160;
+        const int hf = t & 1;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            s0 = dot4((int)q.wa[i], (int)x0[i], s0);
-            s1 = dot4((int)q.wb[i], (int)x1[i], s1);
+        for (int i = 0; i < 4; ++i) a.c[i] = ld16(st + 64 * hf + 16 * i);
+        a.sc = *(const f32x4*)(st + 128 + 16 * hf);
+    }
+    template <int MR>
+    static BQ_DEV void dot(const Task& a, const uint8_t*, int t, const ActLds& act, int K, float (&acc)[MR]) {
+        const int k0 = 64 * t, nb = K >> 5;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            int s[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const u32x4 x = *(const u32x4*)(act.x + m * K + k0 + 16 * g);
+                int v = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v = dot4((int)a.c[g][i], (int)x[i], v);
+                s[g] = v;
+            }
+            const float2 xdv = *(const float2*)(act.xd + m * nb + (k0 >> 5));
+            acc[m] += xdv.x * (a.sc.x * (float)s[0] + a.sc.y * (float)s[1]) +
+                      xdv.y * (a.sc.z * (float)s[2] + a.sc.w * (float)s[3]);
         }
-        return a.xd[m * (K >> 5) + (q.k >> 5)] * (q.sc.x * (float)s0 + q.sc.y * (float)s1);
     }
 };
 
-// LDS bytes for MR staged activation rows
-template <class F>
-constexpr size_t act_lds_bytes(int rows, int K);
+// round a pointer down to 4 bytes, keeping it a (global) pointer
+BQ_DEV const uint8_t* align4(const uint8_t* p) { return p - ((uintptr_t)p & 3); }
 
-template <> constexpr size_t act_lds_bytes<FmtQ5K>(int rows, int K) {
-    return (size_t)rows * K + (size_t)rows * (K / 32) * 8;
-}
-template <> constexpr size_t act_lds_bytes<FmtQ6KRaw>(int rows, int K) {
-    return (size_t)rows * K + (size_t)rows * (K / 32) * 4 + (size_t)rows * (K / 16) * 4;
-}
-template <> constexpr size_t act_lds_bytes<FmtQ6KRep>(int rows, int K) {
-    return (size_t)rows * K + (size_t)rows * (K / 32) * 4;
-}
-
-// ---------------------------------------------------------------------------
-// The GEMV kernel: WAVES waves per workgroup, one tile of T weight rows per
-// wave, MR activation rows, S steps (64 tasks each) of loads kept in flight.
-//   1. every wave issues the loads of its first S steps,
-//   2. the workgroup stages the activations in LDS while those are in flight,
-//   3. steps are computed S at a time, the next S steps' loads issued first.
-// ---------------------------------------------------------------------------
-template <class F, int T, int MR, int S, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES)
-k_gemv(PartTable pt, int K, const int8_t* __restrict__ xq, const float* __restrict__ xd,
-       const int32_t* __restrict__ xsum) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int lane = threadIdx.x & 63;
-    const int tile = blockIdx.x * WAVES + (threadIdx.x >> 6);
-    const bool valid = tile < pt.ntiles;
-    const int p = valid ? find_part(pt, tile) : 0;
-    const uint8_t* __restrict__ W = (const uint8_t*)pt.W[p];
-    const int Nloc = pt.N[p];
-    const int row0 = valid ? (tile - pt.tile0[p]) * T : 0;
-    const int tpr = K >> 5;                 // tasks per weight row
-    const int total = T * tpr;
-    const int nchunks = (total + 64 * S - 1) / (64 * S);
-
-    // task f -> (tile row t, task in row r); rows past N are skipped
-    auto locate = [&](int f, int& t, int& r) -> bool {
-        t = 0;
-        r = f;
-#pragma unroll
-        for (int i = 1; i < T; ++i)
-            if (r >= tpr) { r -= tpr; ++t; }
-        return f < total && row0 + t < Nloc;
-    };
-    typename F::Task cur[S];
-    auto load_chunk = [&](int ch, typename F::Task (&buf)[S]) {
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            int t, r;
-            if (locate((ch * S + s) * 64 + lane, t, r)) F::load(buf[s], W, row0 + t, r, K);
-        }
-    };
-    if (valid) load_chunk(0, cur);
-
-    // ---- stage activations
-    const int nb = K >> 5;
-    ActLds a;
-    a.x = (const int8_t*)smem;
-    a.xd = (const float*)(smem + MR * K);
-    a.aux = a.xd + MR * nb;
-    for (int i = threadIdx.x; i < MR * K / 16; i += 64 * WAVES) {
-        const u32x4 v = ((const u32x4*)xq)[i];
-        ((u32x4*)smem)[i] = v;
-        if constexpr (std::is_same<F, FmtQ6KRaw>::value) {
-            int s = 0;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) s = dot4((int)v[k], 0x01010101, s);
-            ((int*)a.aux)[i] = 32 * s;
-        }
+struct FmtQ6KRaw {
+    // task t: super-block t >> 2, half h = (t >> 1) & 1, positions l0 = 16*(t & 1):
+    // values 128h + 32u + l0 .. +15 of the four quarters u (both ql nibbles used).
+    // Blocks are 2-byte aligned: every field is read as whole dwords from a
+    // 4-byte aligned window inside the block and funnel-shifted into place.
+    static constexpr int kLoads = 8;  // VMEM instructions per task
+    struct Task { u32x4 qlA, qlB, qh; uint32_t qlA4, qlB4, qh4, d; uint32_t sc[3]; };
+    static BQ_DEV void load(Task& a, const uint8_t* row, int t) {
+        const uint8_t* blk = row + (t >> 2) * kQ6Bytes;
+        const int h = (t >> 1) & 1, l0 = 16 * (t & 1);
+        const uint8_t* pa = align4(blk + 64 * h + l0);
+        const uint8_t* pb = align4(blk + 64 * h + 32 + l0);
+        const uint8_t* ph = align4(blk + 128 + 32 * h + l0);
+        // scales 192 + 8h .. +7: 12-byte window ending at most at byte 210
+        const uint8_t* ps = align4(blk + 192 + 8 * h - 2);
+        a.qlA = *(const u32x4*)pa;
+        a.qlA4 = *(const uint32_t*)(pa + 16);
+        a.qlB = *(const u32x4*)pb;
+        a.qlB4 = *(const uint32_t*)(pb + 16);
+        a.qh = *(const u32x4*)ph;
+        a.qh4 = *(const uint32_t*)(ph + 16);
+        __builtin_memcpy(a.sc, ps, 12);
+        a.d = *(const uint16_t*)(blk + 208);
     }
-    for (int i = threadIdx.x; i < MR * nb; i += 64 * WAVES) {
-        ((float*)a.xd)[i] = xd[i];
-        if constexpr (std::is_same<F, FmtQ5K>::value) ((float*)a.aux)[i] = (float)xsum[i];
+    static BQ_DEV u32x4 shift16(const u32x4& v, uint32_t v4, uint32_t sh) {
+        u32x4 r;
+        r.x = __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+        r.y = __builtin_amdgcn_alignbyte(v.z, v.y, sh);
+        r.z = __builtin_amdgcn_alignbyte(v.w, v.z, sh);
+        r.w = __builtin_amdgcn_alignbyte(v4, v.w, sh);
+        return r;
     }
-    __syncthreads();
-    if (!valid) return;
-
-    float acc[T][MR];
+    template <int MR>
+    static BQ_DEV void dot(const Task& a, const uint8_t* row, int t, const ActLds& act, int K, float (&acc)[MR]) {
+        const int h = (t >> 1) & 1, l0 = 16 * (t & 1);
+        const uint8_t* blk = row + (t >> 2) * kQ6Bytes;
+        const uint32_t sh = (uint32_t)(uintptr_t)blk & 2;  // 0 or 2 bytes
+        const u32x4 qlA = shift16(a.qlA, a.qlA4, sh), qlB = shift16(a.qlB, a.qlB4, sh);
+        const u32x4 qh = shift16(a.qh, a.qh4, sh);
+        // the scale window starts 4 (aligned block) or 2 bytes before byte 192 + 8h
+        const uint32_t s0 = sh ? __builtin_amdgcn_alignbyte(a.sc[1], a.sc[0], 2) : a.sc[1];
+        const uint32_t s1 = sh ? __builtin_amdgcn_alignbyte(a.sc[2], a.sc[1], 2) : a.sc[2];
+        const float d = h2f(a.d);
+        float sc[4];
+        uint32_t q[4][4];
 #pragma unroll
-    for (int t = 0; t < T; ++t)
+        for (int u = 0; u < 4; ++u) {
+            const int gi = 2 * u + (l0 >> 4);  // byte of the 8 scale bytes of this half
+            const uint32_t w = gi < 4 ? s0 : s1;
+            sc[u] = d * (float)(int8_t)(w >> (8 * (gi & 3)));
 #pragma unroll
-        for (int m = 0; m < MR; ++m) acc[t][m] = 0.f;
-
-    for (int ch = 0; ch < nchunks; ++ch) {
-        typename F::Task nxt[S];
-        if (ch + 1 < nchunks) load_chunk(ch + 1, nxt);
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            int t, r;
-            if (!locate((ch * S + s) * 64 + lane, t, r)) continue;
-            typename F::Prep q;
-            F::prep(q, cur[s], r);
-#pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const float v = F::dot(q, a, m, K);
-#pragma unroll
-                for (int i = 0; i < T; ++i) acc[i][m] += (t == i) ? v : 0.f;
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ql = (u & 1) ? qlB[i] : qlA[i];
+                const uint32_t nib = ((u >= 2) ? (ql >> 4) : ql) & 0x0F0F0F0Fu;
+                q[u][i] = nib | (((qh[i] >> (2 * u)) & 0x03030303u) << 4);
             }
         }
-#pragma unroll
-        for (int s = 0; s < S; ++s) cur[s] = nxt[s];
-    }
-
-    float* __restrict__ Y = pt.Y[p];
-#pragma unroll
-    for (int t = 0; t < T; ++t)
+        const int kb = (t >> 2) * 256 + 128 * h + l0, nb = K >> 5;
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            const float v = wave_sum(acc[t][m]);
-            if (lane == 0 && row0 + t < Nloc) Y[(size_t)m * Nloc + row0 + t] = v;
+            float v = 0.f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int k = kb + 32 * u;
+                const u32x4 x = *(const u32x4*)(act.x + m * K + k);
+                int s = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    s = dot4((int)q[u][i], (int)x[i], s);
+                    s = dot4((int)0xE0E0E0E0u, (int)x[i], s);  // codes are q in 0..63: add -32*x
+                }
+                v += act.xd[m * nb + (k >> 5)] * sc[u] * (float)s;
+            }
+            acc[m] += v;
         }
+    }
+};
+
+template <class F> struct RowBytes;
+template <> struct RowBytes<FmtQ5K> { static BQ_DEV size_t of(int K) { return (size_t)(K / 256) * kQ5Bytes; } };
+template <> struct RowBytes<FmtQ6KRaw> { static BQ_DEV size_t of(int K) { return (size_t)(K / 256) * kQ6Bytes; } };
+template <> struct RowBytes<FmtQ6KRep> { static BQ_DEV size_t of(int K) { return (size_t)(K / 128) * kW160; } };
+
+// LDS bytes: MR staged activation rows + the K-slice partial sums
+template <class F>
+__host__ __device__ inline size_t act_lds_bytes(int rows, int K) {
+    size_t b = (size_t)rows * K + (size_t)rows * (K / 32) * 4;
+    if (std::is_same<F, FmtQ5K>::value) b += (size_t)rows * (K / 32) * 4;
+    return b;
+}
+
+// s_waitcnt vmcnt(N) with lgkmcnt/expcnt left unconstrained (gfx9 encoding)
+#define BQ_WAIT_VMCNT(n) \
+    __builtin_amdgcn_s_waitcnt(((n) & 0xF) | ((((n) >> 4) & 3) << 14) | 0x70 | 0xF00)
+
+// Copy `bytes` (multiple of 16) from global to LDS with direct-to-LDS loads:
+// one 64-lane instruction moves 1 KiB into consecutive LDS.
+template <int WAVES>
+BQ_DEV void dma_to_lds(uint8_t* lds, const void* src, int bytes, int wave, int lane) {
+    const int n = bytes >> 4;
+    for (int b = wave * 64; b < n; b += 64 * WAVES) {
+        if (b + lane < n)
+            __builtin_amdgcn_global_load_lds((const uint8_t*)src + 16 * (b + lane),
+                                             (__attribute__((address_space(3))) void*)(lds + 16 * b), 16, 0, 0);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The kernel: WAVES waves per workgroup, a wave owns (tile of 4 rows, K slice
+// ks of KS), SPS steps of 16 tasks per row; MR activation rows.
+// ---------------------------------------------------------------------------
+template <class F, int MR, int SPS, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES)
+k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+       const int32_t* __restrict__ xsum) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+    const int nb = K >> 5;
+    // ---- 1. activations -> LDS (asynchronous)
+    ActLds act;
+    act.x = (const int8_t*)smem;
+    act.xd = (const float*)(smem + MR * K);
+    act.xs = (const int32_t*)(act.xd + MR * nb);
+    float* part_sums = (float*)(smem + act_lds_bytes<F>(MR, K));  // [WAVES][MR][4]
+    dma_to_lds<WAVES>(smem, xq, MR * K, wave, lane);
+    dma_to_lds<WAVES>(smem + MR * K, xd, MR * nb * 4, wave, lane);
+    if constexpr (std::is_same<F, FmtQ5K>::value)
+        dma_to_lds<WAVES>(smem + MR * K + MR * nb * 4, xsum, MR * nb * 4, wave, lane);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 2. this wave's weight loads, all issued now (addresses clamped so the
+    //         instruction count is fixed; results of clamped lanes are unused)
+    const int RT = WAVES / KS;
+    const int tile = blockIdx.x * RT + wave / KS, ks = wave % KS;
+    const bool active = wave < RT * KS && tile < pt.ntiles;
+    const int tl = active ? tile : 0;
+    const int p = find_part(pt, tl);
+    const int Nloc = pt.N[p];
+    const int row = (tl - pt.tile0[p]) * kRowsPerTile + g;
+    const int tpr = K >> 6;
+    const uint8_t* rowp = (const uint8_t*)pt.W[p] + (size_t)min(row, Nloc - 1) * RowBytes<F>::of(K);
+    typename F::Task w[SPS];
+#pragma unroll
+    for (int s = 0; s < SPS; ++s) {
+        const int t = (ks * SPS + s) * kTasksPerStep + li;
+        F::load(w[s], rowp, min(t, tpr - 1));
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 3. own DMA done (only the weight loads may still be outstanding)
+    BQ_WAIT_VMCNT(F::kLoads * SPS);
+    __builtin_amdgcn_s_barrier();
+
+    // ---- 4. compute, step by step as the loads return
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+    const bool rowok = active && row < Nloc;
+#pragma unroll
+    for (int s = 0; s < SPS; ++s) {
+        const int t = (ks * SPS + s) * kTasksPerStep + li;
+#ifdef BQ_EXP_NOCOMPUTE
+        if (rowok && t < tpr) acc[0] += as_float(((const uint32_t*)&w[s])[0] & 0x3F800000u);
+#else
+        if (rowok && t < tpr) F::template dot<MR>(w[s], rowp, t, act, K, acc);
+#endif
+    }
+    // ---- 5. row sums; K slices combined through LDS
+    float* Y = pt.Y[p];
+    if (KS == 1) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const float v = row16_sum(acc[m]);
+            if (li == 15 && rowok) Y[(size_t)m * Nloc + row] = v;
+        }
+        return;
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const float v = row16_sum(acc[m]);
+        if (li == 15) part_sums[(wave * MR + m) * 4 + g] = v;
+    }
+    __syncthreads();
+    if (ks == 0 && rowok && li == 15) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float v = 0.f;
+            for (int k = 0; k < KS; ++k) v += part_sums[((wave + k) * MR + m) * 4 + g];
+            Y[(size_t)m * Nloc + row] = v;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
-static void build_tiles(PartTable& pt, int T) {
+void gemv_set_cus(int) {}
+
+static void build_tiles(PartTable& pt) {
     int acc = 0;
     for (int p = 0; p < pt.nparts; ++p) {
         pt.tile0[p] = acc;
-        acc += (pt.N[p] + T - 1) / T;
+        acc += (pt.N[p] + kRowsPerTile - 1) / kRowsPerTile;
     }
     for (int p = pt.nparts; p < kMaxParts; ++p) pt.tile0[p] = acc;
     pt.ntiles = acc;
 }
 
-// steps in flight per wave: 3 for one or two rows (load-latency bound),
-// 2 for more rows (VALU heavier, registers scarcer)
-template <int MR> constexpr int steps_for() { return MR <= 2 ? 3 : 2; }
+// K split: ceil(K/1024) steps per row, at most 3 per wave (BQ_GEMV_SPS=1|2
+// lowers the cap: a dev A/B switch, read once)
+static void k_split(int K, int& KS, int& SPS) {
+    static int cap = -1;
+    if (cap < 0) {
+        const char* e = getenv("BQ_GEMV_SPS");
+        cap = e ? std::max(1, std::min(3, atoi(e))) : 3;
+    }
+    const int spt = (K / 64 + kTasksPerStep - 1) / kTasksPerStep;
+    KS = (spt + cap - 1) / cap;
+    SPS = (spt + KS - 1) / KS;
+}
 
-template <class F, int T, int MR, int WAVES>
-static hipError_t launch_fmt(const PartTable& pt, int K, const int8_t* xq, const float* xd,
-                             const int32_t* xsum, size_t lds, hipStream_t st) {
-    const dim3 grid((pt.ntiles + WAVES - 1) / WAVES), block(64 * WAVES);
-    hipLaunchKernelGGL((k_gemv<F, T, MR, steps_for<MR>(), WAVES>), grid, block, lds, st, pt, K, xq, xd, xsum);
+template <class F, int MR, int SPS, int WAVES>
+static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* xq, const float* xd,
+                             const int32_t* xsum, hipStream_t st) {
+    const size_t lds = act_lds_bytes<F>(MR, K) + (size_t)WAVES * MR * 4 * sizeof(float);
+    const int RT = WAVES / KS;
+    const int blocks = (pt.ntiles + RT - 1) / RT;
+    hipLaunchKernelGGL((k_gemv<F, MR, SPS, WAVES>), dim3(blocks), dim3(64 * WAVES), lds, st, pt, K, KS,
+                       xq, xd, xsum);
     return hipGetLastError();
 }
 
 template <class F, int MR>
-static hipError_t dispatch_t(int T, const PartTable& pt, int K, const int8_t* xq, const float* xd,
-                             const int32_t* xsum, hipStream_t st) {
-    const size_t lds = act_lds_bytes<F>(MR, K);
-    const bool big = lds > 32 * 1024;  // one LDS copy shared by 16 waves
-#define BQ_LT(TT) return big ? launch_fmt<F, TT, MR, 16>(pt, K, xq, xd, xsum, lds, st) \
-                             : launch_fmt<F, TT, MR, 4>(pt, K, xq, xd, xsum, lds, st)
-    switch (T) {
-        case 1: BQ_LT(1);
-        case 2: BQ_LT(2);
-        default: BQ_LT(4);
+static hipError_t dispatch_mr(const PartTable& pt, int K, const int8_t* xq, const float* xd,
+                              const int32_t* xsum, hipStream_t st) {
+    int KS, SPS;
+    k_split(K, KS, SPS);
+    if (KS <= 4) {
+        switch (SPS) {
+            case 1: return launch_fmt<F, MR, 1, 4>(pt, K, KS, xq, xd, xsum, st);
+            case 2: return launch_fmt<F, MR, 2, 4>(pt, K, KS, xq, xd, xsum, st);
+            default: return launch_fmt<F, MR, 3, 4>(pt, K, KS, xq, xd, xsum, st);
+        }
     }
-#undef BQ_LT
+    if (KS <= 16) return launch_fmt<F, MR, 3, 16>(pt, K, KS, xq, xd, xsum, st);
+    return hipErrorInvalidValue;  // K > 49152
 }
 
 template <class F>
-static hipError_t dispatch_rows(int rows, int T, const PartTable& pt, int K, const int8_t* xq,
-                                const float* xd, const int32_t* xsum, hipStream_t st) {
+static hipError_t dispatch_rows(int rows, const PartTable& pt, int K, const int8_t* xq, const float* xd,
+                                const int32_t* xsum, hipStream_t st) {
     switch (rows) {
-        case 1: return dispatch_t<F, 1>(T, pt, K, xq, xd, xsum, st);
-        case 2: return dispatch_t<F, 2>(T, pt, K, xq, xd, xsum, st);
-        case 3: return dispatch_t<F, 3>(T, pt, K, xq, xd, xsum, st);
-        case 4: return dispatch_t<F, 4>(T, pt, K, xq, xd, xsum, st);
-        case 5: return dispatch_t<F, 5>(T, pt, K, xq, xd, xsum, st);
-        case 6: return dispatch_t<F, 6>(T, pt, K, xq, xd, xsum, st);
-        case 7: return dispatch_t<F, 7>(T, pt, K, xq, xd, xsum, st);
-        case 8: return dispatch_t<F, 8>(T, pt, K, xq, xd, xsum, st);
+        case 1: return dispatch_mr<F, 1>(pt, K, xq, xd, xsum, st);
+        case 2: return dispatch_mr<F, 2>(pt, K, xq, xd, xsum, st);
+        case 3: return dispatch_mr<F, 3>(pt, K, xq, xd, xsum, st);
+        case 4: return dispatch_mr<F, 4>(pt, K, xq, xd, xsum, st);
+        case 5: return dispatch_mr<F, 5>(pt, K, xq, xd, xsum, st);
+        case 6: return dispatch_mr<F, 6>(pt, K, xq, xd, xsum, st);
+        case 7: return dispatch_mr<F, 7>(pt, K, xq, xd, xsum, st);
+        case 8: return dispatch_mr<F, 8>(pt, K, xq, xd, xsum, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 size_t gemv_lds_bytes(GemvKind kind, int rows, int K) {
+    const size_t partials = (size_t)16 * rows * 4 * sizeof(float);
     switch (kind) {
-        case GemvKind::Q5K: return act_lds_bytes<FmtQ5K>(rows, K);
-        case GemvKind::Q6KRaw: return act_lds_bytes<FmtQ6KRaw>(rows, K);
-        default: return act_lds_bytes<FmtQ6KRep>(rows, K);
+        case GemvKind::Q5K: return act_lds_bytes<FmtQ5K>(rows, K) + partials;
+        case GemvKind::Q6KRaw: return act_lds_bytes<FmtQ6KRaw>(rows, K) + partials;
+        default: return act_lds_bytes<FmtQ6KRep>(rows, K) + partials;
     }
 }
 
 // rows 1..8 activation rows starting at xq/xd/xsum (already offset)
 hipError_t launch_gemv(GemvKind kind, PartTable pt, int rows, int K, const int8_t* xq,
                        const float* xd, const int32_t* xsum, hipStream_t st) {
-    const int T = tile_rows(K);
-    build_tiles(pt, T);
+    build_tiles(pt);
     if (pt.ntiles == 0) return hipSuccess;
     switch (kind) {
-        case GemvKind::Q5K: return dispatch_rows<FmtQ5K>(rows, T, pt, K, xq, xd, xsum, st);
-        case GemvKind::Q6KRaw: return dispatch_rows<FmtQ6KRaw>(rows, T, pt, K, xq, xd, xsum, st);
-        default: return dispatch_rows<FmtQ6KRep>(rows, T, pt, K, xq, xd, xsum, st);
+        case GemvKind::Q5K: return dispatch_rows<FmtQ5K>(rows, pt, K, xq, xd, xsum, st);
+        case GemvKind::Q6KRaw: return dispatch_rows<FmtQ6KRaw>(rows, pt, K, xq, xd, xsum, st);
+        default: return dispatch_rows<FmtQ6KRep>(rows, pt, K, xq, xd, xsum, st);
     }
 }
 

@@ -27,6 +27,7 @@ hipError_t launch_quant_q8(const float* x, int rows, int K, int8_t* xq, float* x
                            uint16_t* xdh, hipStream_t st);
 hipError_t launch_fill_xdh(const float* xd, const int32_t* xsum, int n, uint16_t* xdh, hipStream_t st);
 
+void gemv_set_cus(int cus);
 size_t gemv_lds_bytes(GemvKind kind, int rows, int K);
 hipError_t launch_gemv(GemvKind kind, PartTable pt, int rows, int K, const int8_t* xq,
                        const float* xd, const int32_t* xsum, hipStream_t st);
