@@ -1,0 +1,241 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X k-quant matmul path (libbq) on one GPU.
+
+Headline (BASELINE metric "GEMV GB/s (% HBM peak) at batch 1"): the decode FFN
+GEMV set of BASELINE config 2 -- per step, quantize the block input (q8),
+fused gate+up Q5_K GEMV 2 x (9216 x 3072), quantize the down-projection input,
+down Q6_K GEMV 3072 x 9216 -- batch 1, synthetic Gaussian data, weight sets
+rotated so the working set exceeds the 256 MB last-level cache.  `value` is
+algorithmic bytes (GGUF weight bytes + q8 activations + fp32 outputs) per
+step x steps / timed region.
+
+Also reported: the prefill GEMM of config 4 (M = 2048, int8 MFMA, TOPS and
+fraction of the dense int8 peak), the multi-row GEMV of config 3, config 1,
+and the reference's scalar host loop timed on this machine's CPU.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu]
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "bruce-engine_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
+METRIC = "GEMV GB/s (% HBM peak) at batch 1; prefill GEMM int8 TOPS (% MFMA peak)"
+SEED = 0xB5CE
+K, FF = 3072, 9216
+LLC_BYTES = 256e6
+
+
+def q8_bytes(rows, k):
+    return rows * (k + (k // 32) * 8)
+
+
+def gbs(nbytes, ms):
+    return nbytes / (ms * 1e-3) / 1e9
+
+
+def traffic_for(name):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    calibrated on a copy kernel), committed in profiles/traffic.json; None if absent."""
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(p) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(gate, up, down, x, t, budget_s=12.0):
+    """The reference's scalar host loop (restated in oracle/bq_oracle.c), one
+    thread, on full decode FFN steps of the same inputs."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    xq, xd, xs = O.q8_rows(x)
+    tq, td, ts = O.q8_rows(t)
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        O.gemm_q5k_f32(gate, xq, xd, xs)
+        O.gemm_q5k_f32(up, xq, xd, xs)
+        O.gemm_q6k_f32(down, tq, td)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or steps >= 50:
+            break
+    return steps, el
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the k-quant matmul path has no multi-GPU mode in this "
+              "build (it would shard weight rows N across GPUs); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import bq
+    import synth
+
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    bq.load()
+    B = ctypes.CDLL(os.path.join(ROOT, "bruce-engine_amd", "libbq_bench.so"))
+    P, I = ctypes.c_void_p, ctypes.c_int
+    WP = ctypes.POINTER(bq.Weight)
+    D4 = ctypes.c_double * 4
+    B.bqb_decode_ffn.argtypes = [I, I, I, I, WP, WP, WP, P, P, P, P, P, P, P, P, P, P, P, P, P]
+    B.bqb_gemm.argtypes = [I, I, WP, I, P, P, P, P, P, P, P]
+    B.bqb_gemv_rows.argtypes = [I, I, I, WP, I, P, P, P, P, P, P]
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    # ---------------------------------------------------------------- data
+    w_gate = synth.quantize_q5k(synth.gaussian(SEED + 1, (FF, K), 0.02))
+    w_up = synth.quantize_q5k(synth.gaussian(SEED + 2, (FF, K), 0.02))
+    w_down = synth.quantize_q6k(synth.gaussian(SEED + 3, (K, FF), 0.02))
+    x = synth.gaussian(SEED + 4, (1, K))
+    t = synth.gaussian(SEED + 5, (1, FF))
+    wbytes = w_gate.nbytes + w_up.nbytes + w_down.nbytes
+    nsets = max(2, math.ceil(3 * LLC_BYTES / wbytes))
+    g_gate = torch.from_numpy(w_gate).cuda()
+    g_up = torch.from_numpy(w_up).cuda()
+    g_down = torch.from_numpy(w_down).cuda()
+    keep = []
+    gates, ups, downs = (bq.Weight * nsets)(), (bq.Weight * nsets)(), (bq.Weight * nsets)()
+    for s in range(nsets):
+        a, b, c = g_gate.clone(), g_up.clone(), g_down.clone()
+        keep += [a, b, c]
+        gates[s] = bq.make_weight(a, bq.TYPE_Q5_K, K, FF)
+        ups[s] = bq.make_weight(b, bq.TYPE_Q5_K, K, FF)
+        downs[s] = bq.make_weight(c, bq.TYPE_Q6_K, FF, K)
+    dx, dt = torch.from_numpy(x).cuda(), torch.from_numpy(t).cuda()
+    xq = torch.empty((1, K), dtype=torch.int8, device="cuda")
+    xd = torch.empty((1, K // 32), device="cuda")
+    xs = torch.empty((1, K // 32), dtype=torch.int32, device="cuda")
+    tq = torch.empty((1, FF), dtype=torch.int8, device="cuda")
+    td = torch.empty((1, FF // 32), device="cuda")
+    ts = torch.empty((1, FF // 32), dtype=torch.int32, device="cuda")
+    yg, yu, yd = (torch.empty(FF, device="cuda"), torch.empty(FF, device="cuda"),
+                  torch.empty(K, device="cuda"))
+    torch.cuda.synchronize()
+
+    # ---------------------------------------------------------------- decode FFN step
+    out = D4()
+    # timed region: K graph-replayed steps (the headline value)
+    r = B.bqb_decode_ffn(0, args.steps, args.warmup, nsets, gates, ups, downs, ptr(dx), ptr(dt), ptr(xq),
+                         ptr(xd), ptr(xs), ptr(tq), ptr(td), ptr(ts), ptr(yg), ptr(yu), ptr(yd), sp, out)
+    if r != 0:
+        raise RuntimeError(f"bqb_decode_ffn failed: {r} {bq.strerror(r)}")
+    step_bytes = wbytes + q8_bytes(1, K) + q8_bytes(1, FF) + 4 * (2 * FF + K)
+    total_ms = out[0]
+    # second timed region, same K steps launched directly: the GEMV kernels'
+    # own durations from dispatch start/end events
+    r = B.bqb_decode_ffn(1, args.steps, 0, nsets, gates, ups, downs, ptr(dx), ptr(dt), ptr(xq),
+                         ptr(xd), ptr(xs), ptr(tq), ptr(td), ptr(ts), ptr(yg), ptr(yu), ptr(yd), sp, out)
+    if r != 0:
+        raise RuntimeError(f"bqb_decode_ffn (kernel timing) failed: {r} {bq.strerror(r)}")
+    value = gbs(step_bytes * args.steps, total_ms)
+    gu_bytes = w_gate.nbytes + w_up.nbytes + q8_bytes(1, K) + 4 * 2 * FF
+    gu_ms = out[1] / args.steps
+    dn_bytes = w_down.nbytes + q8_bytes(1, FF) + 4 * K
+    dn_ms = out[2] / args.steps
+    achieved = gbs(gu_bytes, gu_ms)
+
+    # ---------------------------------------------------------------- prefill GEMM (config 4)
+    gemm = {}
+    gw144, gdm = bq.repack_q5k(g_gate, K, FF)
+    for M in (2048, 512, 8192):
+        xm = torch.from_numpy(synth.gaussian(SEED + 6, (M, K))).cuda()
+        mq, md, ms_, mh = bq.quantize_q8(xm, with_xdh=True)
+        ym = torch.empty((M, FF), device="cuda")
+        res = {}
+        for name, w in (("w144", bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF, rep=gw144, rep_min=gdm)),
+                        ("raw", bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF))):
+            gsteps = 20 if M == 8192 else 50
+            r = B.bqb_gemm(gsteps, 5, ctypes.byref(w), M, ptr(mq), ptr(md), ptr(ms_), ptr(mh), ptr(ym), sp, out)
+            if r != 0:
+                raise RuntimeError(f"bqb_gemm failed: {r}")
+            kms = out[1] / gsteps
+            tops = 2.0 * M * FF * K / (kms * 1e-3) / 1e12
+            res[name] = {"ms": round(kms, 4), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)}
+        gemm[f"M{M}"] = res
+        del xm, mq, md, ms_, mh, ym
+    g = gemm["M2048"]["w144"]
+    gemm_obj = {
+        "config": "prefill GEMM Q5_K 9216x3072 (W144 repack, fp16 min term), M=2048 q8 tokens, fp32 out",
+        "value": g["tops"], "unit": "TOPS", "ms": g["ms"],
+        "roofline": {"bound": "mfma", "achieved": g["tops"], "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                     "frac": g["frac"], "traffic": traffic_for("mmq_q5k_144_M2048"),
+                     "kernel": "k_mmq_q5k<Q5W144>", "ops_per_launch": 2 * 2048 * FF * K},
+        "shapes": gemm,
+    }
+
+    # ---------------------------------------------------------------- config 3 / config 1 GEMV
+    rows_res = {}
+    xr = torch.from_numpy(synth.gaussian(SEED + 7, (8, K))).cuda()
+    rq, rd, rs = bq.quantize_q8(xr)
+    yr = torch.empty((8, FF), device="cuda")
+    gsets = (bq.Weight * nsets)(*[gates[s] for s in range(nsets)])
+    for rows in (1, 2, 4, 8):
+        r = B.bqb_gemv_rows(100, 10, nsets, gsets, rows, ptr(rq), ptr(rd), ptr(rs), ptr(yr), sp, out)
+        kms = out[1] / 100
+        rows_res[f"rows{rows}"] = {"us": round(kms * 1e3, 2),
+                                   "GBps": round(gbs(w_gate.nbytes + q8_bytes(rows, K) + 4 * rows * FF, kms), 1)}
+    c1 = synth.quantize_q5k(synth.gaussian(SEED + 8, (K, K), 0.02))
+    n1 = max(2, math.ceil(3 * LLC_BYTES / c1.nbytes))
+    c1g = [torch.from_numpy(c1).cuda() for _ in range(n1)]
+    c1w = (bq.Weight * n1)(*[bq.make_weight(a, bq.TYPE_Q5_K, K, K) for a in c1g])
+    r = B.bqb_gemv_rows(200, 10, n1, c1w, 1, ptr(rq), ptr(rd), ptr(rs), ptr(yr), sp, out)
+    c1ms = out[1] / 200
+    del c1g
+
+    # ---------------------------------------------------------------- CPU baseline
+    cpu = None
+    if not args.no_cpu:
+        steps_cpu, el = cpu_baseline(w_gate, w_up, w_down, x, t)
+        cpu = {"value": round(gbs(step_bytes * steps_cpu, el * 1e3), 3), "unit": "GB/s", "cores": 1,
+               "kind": "port",
+               "sample": f"{steps_cpu} full decode FFN steps (gate+up Q5_K + down Q6_K, batch 1, same "
+                         "inputs) through the scalar fp32 restatement of the reference host loop "
+                         "(tools/mmq_test.cu:269-294), single thread",
+               "seconds": round(el, 2), "host_threads_available": os.cpu_count()}
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "BASELINE config 2: decode FFN GEMV set, batch 1 -- q8 quantize, fused "
+                               "gate+up Q5_K 2x(9216x3072), q8 quantize, down Q6_K 3072x9216 (raw GGUF)",
+                   "K": K, "FF": FF, "weight_sets_rotated": nsets, "bytes_per_step": step_bytes,
+                   "hbm_frac_of_step": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for("gemv_q5k_gateup"),
+                     "kernel": "k_gemv<FmtQ5K,1,3,4> (fused gate+up)", "bytes_per_launch": gu_bytes,
+                     "avg_launch_us": round(gu_ms * 1e3, 3)},
+        "down_gemv": {"kernel": "k_gemv<FmtQ6KRaw,1,3,4>", "avg_launch_us": round(dn_ms * 1e3, 3),
+                      "GBps": round(gbs(dn_bytes, dn_ms), 1)},
+        "gemv_config1_3072x3072": {"us": round(c1ms * 1e3, 2),
+                                   "GBps": round(gbs(c1.nbytes + q8_bytes(1, K) + 4 * K, c1ms), 1)},
+        "gemv_config3_9216x3072": rows_res,
+        "gemm": gemm_obj,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

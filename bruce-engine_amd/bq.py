@@ -30,6 +30,7 @@ EXPORTS = [
     "bq_verify_fused", "bq_q6_verify_fused", "bq_gemm_q6k_dp", "bq_gemm_q6k_raw", "bq_try_mmq",
     "bq_gemm_q6k_mma", "bq_gemm_b", "bq_gemm_b_fused", "bq_repack_q5k", "bq_repack_q5k_bytes",
     "bq_repack_q5k_min_bytes", "bq_repack_q6k", "bq_repack_q6k_host", "bq_repack_q6k_bytes",
+    "bq_time_next_launch",
 ]
 
 
@@ -81,6 +82,7 @@ def load(path=LIB_PATH):
         "bq_repack_q6k": (I, [P, I, I, P, P]),
         "bq_repack_q6k_host": (I, [P, I, I, P]),
         "bq_repack_q6k_bytes": (S, [I, I]),
+        "bq_time_next_launch": (I, [P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

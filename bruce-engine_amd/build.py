@@ -13,6 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libbq.so")
+BENCH_LIB = os.path.join(HERE, "libbq_bench.so")
 SOURCES = ["bq_quant.hip", "bq_gemv.hip", "bq_repack.hip", "bq_gemm.hip", "bq_api.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -46,8 +47,17 @@ def build(verbose=False):
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    # timing driver for bench.py, linked against libbq.so
+    bobj = _compile("bq_bench.hip")
+    tmp = BENCH_LIB + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, bobj, "-L" + HERE, "-lbq",
+           "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, BENCH_LIB)
     if verbose:
-        print("built", LIB)
+        print("built", LIB, "and", BENCH_LIB)
     return LIB
 
 

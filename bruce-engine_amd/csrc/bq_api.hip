@@ -76,7 +76,21 @@ PartTable one_part(float* y, const void* W, int N) {
 
 }  // namespace
 
+namespace bq {
+LaunchTiming& next_launch_timing() {
+    static thread_local LaunchTiming t;
+    return t;
+}
+}  // namespace bq
+
 extern "C" {
+
+int bq_time_next_launch(void* start_event, void* stop_event) {
+    if (!start_event || !stop_event) return BQ_EINVAL;
+    next_launch_timing().start = (hipEvent_t)start_event;
+    next_launch_timing().stop = (hipEvent_t)stop_event;
+    return BQ_OK;
+}
 
 int bq_init(void) { return ensure_init(); }
 

@@ -1,0 +1,172 @@
+// bq_bench.hip -- native timing driver for bench.py (libbq_bench.so).
+//
+// Runs the decode / prefill steps through libbq's public C ABI in a tight host
+// loop on one stream and times them with HIP events: the whole timed region
+// (start/end events after a device synchronisation) and, per step, the
+// dominant kernels' own durations (bq_time_next_launch: events recorded at the
+// dispatch's start and end, the same interval a kernel trace reports).
+// The same launch sequence is what the reference's decode loop issues per
+// token for one FFN block (bruce.cu:7992-8011): quantize the block input,
+// fused gate+up GEMV, quantize the down-projection input, down GEMV.
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "../../include/bq.h"
+
+namespace {
+
+struct EventPool {
+    std::vector<hipEvent_t> ev;
+    explicit EventPool(size_t n) : ev(n, nullptr) {
+        for (auto& e : ev) hipEventCreate(&e);
+    }
+    ~EventPool() {
+        for (auto& e : ev)
+            if (e) hipEventDestroy(e);
+    }
+};
+
+float elapsed(hipEvent_t a, hipEvent_t b) {
+    float ms = 0.f;
+    hipEventElapsedTime(&ms, a, b);
+    return ms;
+}
+
+}  // namespace
+
+extern "C" {
+
+// One decode FFN step per iteration, weight set s = i % nsets (sets rotate so
+// that the working set exceeds the 256 MB last-level cache).
+// mode 0: each set's step is captured once into a HIP graph and the timed
+//         region replays graph[i % nsets] -- the reference replays a captured
+//         CUDA graph per decoded token (bruce.cu:8246-8252).
+//         out[0] = timed region (ms, `steps` steps).
+// mode 1: direct launches, the two GEMV kernels timed with dispatch events.
+//         out[0] = timed region, out[1] / out[2] = summed gate+up / down
+//         kernel durations (ms).
+int bqb_decode_ffn(int mode, int steps, int warmup, int nsets, const bq_weight* gate, const bq_weight* up,
+                   const bq_weight* down, const float* x, const float* t, int8_t* xq, float* xd,
+                   int32_t* xs, int8_t* tq, float* td, int32_t* ts, float* yg, float* yu, float* yd,
+                   bq_stream_t st, double* out) {
+    const int K = gate[0].K, KD = down[0].K;
+    auto step = [&](int i, hipEvent_t g0, hipEvent_t g1, hipEvent_t d0, hipEvent_t d1,
+                    bq_stream_t s_) -> int {
+        const int s = i % nsets;
+        int r = bq_quantize_q8(x, 1, K, xq, xd, xs, nullptr, s_);
+        if (r) return r;
+        float* ys[2] = {yg, yu};
+        const bq_weight* ws[2] = {&gate[s], &up[s]};
+        if (g0) bq_time_next_launch(g0, g1);
+        r = bq_verify_fused(ys, ws, 2, 1, xq, xd, xs, 0, s_);
+        if (r) return r;
+        r = bq_quantize_q8(t, 1, KD, tq, td, ts, nullptr, s_);
+        if (r) return r;
+        if (d0) bq_time_next_launch(d0, d1);
+        return bq_gemv(yd, &down[s], tq, td, ts, s_);
+    };
+    for (int i = 0; i < warmup; ++i)
+        if (int r = step(i, nullptr, nullptr, nullptr, nullptr, st)) return r;
+    out[0] = out[1] = out[2] = 0.0;
+    if (mode == 0) {
+        hipStream_t cs;
+        if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) return -1;
+        std::vector<hipGraphExec_t> ex(nsets, nullptr);
+        for (int s = 0; s < nsets; ++s) {
+            hipGraph_t g;
+            hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+            const int r = step(s, nullptr, nullptr, nullptr, nullptr, (bq_stream_t)cs);
+            if (hipStreamEndCapture(cs, &g) != hipSuccess || r) return r ? r : -1;
+            if (hipGraphInstantiate(&ex[s], g, nullptr, nullptr, 0) != hipSuccess) return -1;
+            hipGraphDestroy(g);
+        }
+        for (int i = 0; i < nsets; ++i) hipGraphLaunch(ex[i], (hipStream_t)st);  // warm the graphs
+        EventPool pool(2);
+        hipDeviceSynchronize();
+        hipEventRecord(pool.ev[0], (hipStream_t)st);
+        for (int i = 0; i < steps; ++i) hipGraphLaunch(ex[i % nsets], (hipStream_t)st);
+        hipEventRecord(pool.ev[1], (hipStream_t)st);
+        hipDeviceSynchronize();
+        out[0] = elapsed(pool.ev[0], pool.ev[1]);
+        for (auto e : ex) hipGraphExecDestroy(e);
+        hipStreamDestroy(cs);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    EventPool pool((size_t)steps * 4 + 2);
+    hipDeviceSynchronize();
+    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    for (int i = 0; i < steps; ++i) {
+        hipEvent_t* e = &pool.ev[2 + 4 * (size_t)i];
+        if (int r = step(i, e[0], e[1], e[2], e[3], st)) return r;
+    }
+    hipEventRecord(pool.ev[1], (hipStream_t)st);
+    hipDeviceSynchronize();
+    out[0] = elapsed(pool.ev[0], pool.ev[1]);
+    double g = 0, d = 0;
+    for (int i = 0; i < steps; ++i) {
+        hipEvent_t* e = &pool.ev[2 + 4 * (size_t)i];
+        g += elapsed(e[0], e[1]);
+        d += elapsed(e[2], e[3]);
+    }
+    out[1] = g;
+    out[2] = d;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// Prefill GEMM: `steps` launches of try_launch_mmq over the same inputs.
+//   out[0] = timed region (ms), out[1] = sum of per-launch event times (ms).
+int bqb_gemm(int steps, int warmup, const bq_weight* w, int M, const int8_t* xq, const float* xd,
+             const int32_t* xs, uint16_t* xdh, float* y, bq_stream_t st, double* out) {
+    float* ys[1] = {y};
+    const bq_weight* ws[1] = {w};
+    for (int i = 0; i < warmup; ++i)
+        if (int r = bq_try_mmq(ys, ws, 1, M, xq, xd, xs, xdh, st)) return r;
+    EventPool pool((size_t)steps * 2 + 2);
+    hipDeviceSynchronize();
+    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    for (int i = 0; i < steps; ++i) {
+        // the fill_xdh pre-pass of the W144 path is not timed: the event pair
+        // brackets the GEMM kernel itself
+        bq_time_next_launch(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
+        if (int r = bq_try_mmq(ys, ws, 1, M, xq, xd, xs, xdh, st)) return r;
+    }
+    hipEventRecord(pool.ev[1], (hipStream_t)st);
+    hipDeviceSynchronize();
+    out[0] = elapsed(pool.ev[0], pool.ev[1]);
+    double k = 0;
+    for (int i = 0; i < steps; ++i) k += elapsed(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
+    out[1] = k;
+    return 0;
+}
+
+// Single-kernel timing helper: `steps` launches of one GEMV entry point with
+// rotating weights (gemv over nsets weights, rows activation rows).
+int bqb_gemv_rows(int steps, int warmup, int nsets, const bq_weight* w, int rows, const int8_t* xq,
+                  const float* xd, const int32_t* xs, float* y, bq_stream_t st, double* out) {
+    auto launch = [&](int i) -> int {
+        float* ys[1] = {y};
+        const bq_weight* wp[1] = {&w[i % nsets]};
+        if (w[0].ggml_type == BQ_TYPE_Q5_K) return bq_verify_fused(ys, wp, 1, rows, xq, xd, xs, 0, st);
+        if (w[0].rep) return bq_gemm_q6k_dp(y, wp[0], rows, xq, xd, 0, st);
+        return bq_gemm_q6k_raw(y, wp[0], rows, xq, xd, 0, st);
+    };
+    for (int i = 0; i < warmup; ++i)
+        if (int r = launch(i)) return r;
+    EventPool pool((size_t)steps * 2 + 2);
+    hipDeviceSynchronize();
+    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    for (int i = 0; i < steps; ++i) {
+        bq_time_next_launch(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
+        if (int r = launch(i)) return r;
+    }
+    hipEventRecord(pool.ev[1], (hipStream_t)st);
+    hipDeviceSynchronize();
+    out[0] = elapsed(pool.ev[0], pool.ev[1]);
+    double k = 0;
+    for (int i = 0; i < steps; ++i) k += elapsed(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
+    out[1] = k;
+    return 0;
+}
+
+}  // extern "C"

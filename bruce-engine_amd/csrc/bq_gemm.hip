@@ -474,7 +474,7 @@ hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, c
                               const uint16_t* xdh, hipStream_t st) {
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_mmq_q5k<MmqMode::Q5W144>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
+    launch_kernel((k_mmq_q5k<MmqMode::Q5W144>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
                        rows, K, xq, xd, (const int32_t*)nullptr, xdh);
     return hipGetLastError();
 }
@@ -483,7 +483,7 @@ hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, c
                               const int32_t* xsum, hipStream_t st) {
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    hipLaunchKernelGGL((k_mmq_q5k<MmqMode::Q5Raw>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
+    launch_kernel((k_mmq_q5k<MmqMode::Q5Raw>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
                        rows, K, xq, xd, xsum, (const uint16_t*)nullptr);
     return hipGetLastError();
 }
@@ -492,7 +492,7 @@ hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const
                           hipStream_t st) {
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_mmq_q6k, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd);
+    launch_kernel(k_mmq_q6k, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd);
     return hipGetLastError();
 }
 

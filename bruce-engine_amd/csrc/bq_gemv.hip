@@ -402,7 +402,7 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     const size_t lds = act_lds_bytes<F>(MR, K) + (size_t)WAVES * MR * 4 * sizeof(float);
     const int RT = WAVES / KS;
     const int blocks = (pt.ntiles + RT - 1) / RT;
-    hipLaunchKernelGGL((k_gemv<F, MR, SPS, WAVES>), dim3(blocks), dim3(64 * WAVES), lds, st, pt, K, KS,
+    launch_kernel((k_gemv<F, MR, SPS, WAVES>), dim3(blocks), dim3(64 * WAVES), lds, st, pt, K, KS,
                        xq, xd, xsum);
     return hipGetLastError();
 }

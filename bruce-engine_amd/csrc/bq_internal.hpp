@@ -1,5 +1,6 @@
 // bq_internal.hpp -- host-side declarations shared by the libbq translation units.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -22,6 +23,25 @@ struct PartTable {
 };
 
 enum class GemvKind { Q5K, Q6KRaw, Q6KRep };
+
+// Optional per-launch timing (bq_time_next_launch): when set, the next GEMV /
+// GEMM kernel of the calling thread is launched with hipExtLaunchKernelGGL,
+// which records the two events at the dispatch's start and end.
+struct LaunchTiming {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchTiming& next_launch_timing();
+
+template <typename F, typename... Args>
+inline void launch_kernel(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
+    LaunchTiming& t = next_launch_timing();
+    if (t.start) {
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, st, t.start, t.stop, 0, args...);
+        t = LaunchTiming();
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+    }
+}
 
 hipError_t launch_quant_q8(const float* x, int rows, int K, int8_t* xq, float* xd, int32_t* xsum,
                            uint16_t* xdh, hipStream_t st);

@@ -140,6 +140,14 @@ int bq_repack_q6k(const void* raw, int K, int N, void* w160, bq_stream_t st);
 int bq_repack_q6k_host(const void* raw, int K, int N, void* w160);
 size_t bq_repack_q6k_bytes(int K, int N);     /* N*(K/128)*160 */
 
+/* ---- tooling ---------------------------------------------------------------
+ * No counterpart in the reference (its harnesses bracket launches with
+ * cudaEventRecord, tools/gemvbench.cu:360-371).  Times the calling thread's
+ * next GEMV/GEMM kernel dispatch: the two hipEvent_t handles are recorded at
+ * the dispatch's start and end (hipExtLaunchKernelGGL), so their elapsed time
+ * is the kernel's own duration.  Used by the benchmark driver. */
+int bq_time_next_launch(void* start_event, void* stop_event);
+
 #ifdef __cplusplus
 }
 #endif
