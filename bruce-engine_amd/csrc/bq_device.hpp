@@ -17,6 +17,7 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
 
 BQ_DEV float h2f(uint32_t bits16) {
     // v_cvt_f32_f16: exact, fp16 denormals included
@@ -70,6 +71,11 @@ BQ_DEV u32x4 ld16_a2(const uint8_t* p) {
     r.w = __builtin_amdgcn_alignbyte(v[4], v[3], 2);
     return r;
 }
+
+// s_waitcnt vmcnt(N) leaving lgkmcnt / expcnt unconstrained (gfx9 encoding:
+// vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
+#define BQ_WAIT_VM(n) \
+    __builtin_amdgcn_s_waitcnt(((n) & 0xF) | ((((n) >> 4) & 3) << 14) | 0x70 | 0xF00)
 
 // Wave64 sum.  Butterfly over the 64 lanes; every lane ends with the total.
 BQ_DEV float wave_sum(float v) {

@@ -243,38 +243,43 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
 #endif
         if (s + 1 < nst) load_stage(s + 1);
 
+        // Per group pair (q0, q0+1) and tile: the scale products ds[n] * xd[m]
+        // of both groups come from one fp32 outer-product MFMA (32x32x1, two
+        // blocks: lanes 0-31 feed group q0, lanes 32-63 group q0+1), so the
+        // VALU epilogue is one convert and one FMA per output and group.
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            i32x4 a[2], b[2];
+        for (int qp = 0; qp < 2; ++qp) {
+            i32x4 a[2][2], b[2][2];  // [tile][group of the pair]
+            float wsv[2], xsv[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int q = 2 * qp + e;
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    a[nt][e] = *(const i32x4*)(sm.w + (wn * 64 + nt * 32 + l32) * kRS + 32 * q + 16 * lh);
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+                    b[mt][e] = *(const i32x4*)(sm.x + (wm * 64 + mt * 32 + l32) * kRS + 32 * q + 16 * lh);
+            }
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) wsv[nt] = sm.ws[(2 * qp + lh) * kTN + wn * 64 + nt * 32 + l32];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) xsv[mt] = sm.xs[(2 * qp + lh) * kTM + wm * 64 + mt * 32 + l32];
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt)
-                a[nt] = *(const i32x4*)(sm.w + (wn * 64 + nt * 32 + l32) * kRS + 32 * q + 16 * lh);
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-                b[mt] = *(const i32x4*)(sm.x + (wm * 64 + mt * 32 + l32) * kRS + 32 * q + 16 * lh);
-            float xs[2];
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) xs[mt] = sm.xs[q * kTM + wm * 64 + mt * 32 + l32];
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                float ws[16];
-#pragma unroll
-                for (int rg = 0; rg < 4; ++rg) {
-                    const f32x4 v = *(const f32x4*)(sm.ws + q * kTN + wn * 64 + nt * 32 + 8 * rg + 4 * lh);
-                    ws[4 * rg + 0] = v.x;
-                    ws[4 * rg + 1] = v.y;
-                    ws[4 * rg + 2] = v.z;
-                    ws[4 * rg + 3] = v.w;
-                }
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt) {
-                    const i32x16 zero = {0};
-                    const i32x16 dd = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[nt], b[mt], zero, 0, 0, 0);
+                    const f32x32 zero32 = {0.f};
+                    const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(wsv[nt], xsv[mt], zero32, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        acc[nt][mt][r] = __builtin_fmaf(ws[r] * xs[mt], (float)dd[r], acc[nt][mt][r]);
+                    for (int e = 0; e < 2; ++e) {
+                        const i32x16 zero = {0};
+                        const i32x16 dd = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[nt][e], b[mt][e], zero, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            acc[nt][mt][r] = __builtin_fmaf(sc[16 * e + r], (float)dd[r], acc[nt][mt][r]);
+                    }
                 }
-            }
         }
         if constexpr (MODE == MmqMode::Q5Raw) {
             // exact fp32 min term of the stage's four groups: two K=2 MFMAs per tile
@@ -409,34 +414,28 @@ k_mmq_q6k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
                 for (int mt = 0; mt < 2; ++mt)
                     b[mt][h] = *(const long*)(sm.x + (wm * 64 + mt * 32 + l32) * kRS + 32 * q + 16 * h + 8 * lh);
             }
-            float xs[2];
+            // scale products of the two 16-value groups (2q, 2q+1) of this
+            // 32-group: one two-block fp32 outer-product MFMA per tile
+            float wsv[2], xsv[2];
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) xs[mt] = sm.xs[q * kTM + wm * 64 + mt * 32 + l32];
+            for (int nt = 0; nt < 2; ++nt) wsv[nt] = sm.ws[(2 * q + lh) * kTN + wn * 64 + nt * 32 + l32];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                float w0[16], w1[16];
+            for (int mt = 0; mt < 2; ++mt) xsv[mt] = sm.xs[q * kTM + wm * 64 + mt * 32 + l32];
 #pragma unroll
-                for (int rg = 0; rg < 4; ++rg) {
-                    const int r0 = wn * 64 + nt * 32 + 8 * rg + 4 * lh;
-                    const f32x4 v0 = *(const f32x4*)(sm.ws + (2 * q) * kTN + r0);
-                    const f32x4 v1 = *(const f32x4*)(sm.ws + (2 * q + 1) * kTN + r0);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        w0[4 * rg + e] = v0[e];
-                        w1[4 * rg + e] = v1[e];
-                    }
-                }
+            for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt) {
+                    const f32x32 zero32 = {0.f};
+                    const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(wsv[nt], xsv[mt], zero32, 0, 0, 0);
                     const i32x16 zero = {0};
                     const i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a[nt][0], b[mt][0], zero, 0, 0, 0);
                     const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a[nt][1], b[mt][1], zero, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        acc[nt][mt][r] = __builtin_fmaf(xs[mt], w0[r] * (float)d0[r] + w1[r] * (float)d1[r],
-                                                        acc[nt][mt][r]);
+                    for (int r = 0; r < 16; ++r) {
+                        acc[nt][mt][r] = __builtin_fmaf(sc[r], (float)d0[r], acc[nt][mt][r]);
+                        acc[nt][mt][r] = __builtin_fmaf(sc[16 + r], (float)d1[r], acc[nt][mt][r]);
+                    }
                 }
-            }
         }
     }
 
@@ -475,7 +474,7 @@ hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, c
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
     launch_kernel((k_mmq_q5k<MmqMode::Q5W144>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
-                       rows, K, xq, xd, (const int32_t*)nullptr, xdh);
+                  rows, K, xq, xd, (const int32_t*)nullptr, xdh);
     return hipGetLastError();
 }
 

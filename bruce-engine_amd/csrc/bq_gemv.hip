@@ -263,9 +263,6 @@ __host__ __device__ inline size_t act_lds_bytes(int rows, int K) {
     return b;
 }
 
-// s_waitcnt vmcnt(N) with lgkmcnt/expcnt left unconstrained (gfx9 encoding)
-#define BQ_WAIT_VMCNT(n) \
-    __builtin_amdgcn_s_waitcnt(((n) & 0xF) | ((((n) >> 4) & 3) << 14) | 0x70 | 0xF00)
 
 // Copy `bytes` (multiple of 16) from global to LDS with direct-to-LDS loads:
 // one 64-lane instruction moves 1 KiB into consecutive LDS.
@@ -325,7 +322,7 @@ k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* 
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 3. own DMA done (only the weight loads may still be outstanding)
-    BQ_WAIT_VMCNT(F::kLoads * SPS);
+    BQ_WAIT_VM(F::kLoads * SPS);
     __builtin_amdgcn_s_barrier();
 
     // ---- 4. compute, step by step as the loads return
