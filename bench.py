@@ -131,6 +131,12 @@ def main():
     ts = torch.empty((1, FF // 32), dtype=torch.int32, device="cuda")
     yg, yu, yd = (torch.empty(FF, device="cuda"), torch.empty(FF, device="cuda"),
                   torch.empty(K, device="cuda"))
+    # a plain 64 MiB device copy: the reference point that scales rocprofv3's
+    # FETCH_SIZE / WRITE_SIZE counters to bytes (profiles/traffic.json)
+    calib_src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    calib_dst = torch.empty_like(calib_src)
+    calib_dst.copy_(calib_src)
+    del calib_src, calib_dst
     torch.cuda.synchronize()
 
     # ---------------------------------------------------------------- decode FFN step
