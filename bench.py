@@ -155,10 +155,22 @@ def main():
     if r != 0:
         raise RuntimeError(f"bqb_decode_ffn (kernel timing) failed: {r} {bq.strerror(r)}")
     value = gbs(step_bytes * args.steps, total_ms)
+    gu_ms, dn_ms = out[1] / args.steps, out[2] / args.steps
+    # the same step through bq_gemv_q8_fused (quantizer inside each GEMV)
+    r = B.bqb_decode_ffn(2, args.steps, args.warmup, nsets, gates, ups, downs, ptr(dx), ptr(dt), ptr(xq),
+                         ptr(xd), ptr(xs), ptr(tq), ptr(td), ptr(ts), ptr(yg), ptr(yu), ptr(yd), sp, out)
+    if r != 0:
+        raise RuntimeError(f"bqb_decode_ffn (fused) failed: {r} {bq.strerror(r)}")
+    fused_ms = out[0]
+    r = B.bqb_decode_ffn(3, args.steps, 0, nsets, gates, ups, downs, ptr(dx), ptr(dt), ptr(xq),
+                         ptr(xd), ptr(xs), ptr(tq), ptr(td), ptr(ts), ptr(yg), ptr(yu), ptr(yd), sp, out)
+    if r != 0:
+        raise RuntimeError(f"bqb_decode_ffn (fused, kernel timing) failed: {r} {bq.strerror(r)}")
+    fused = {"ms_per_step": round(fused_ms / args.steps, 5),
+             "GBps": round(gbs(step_bytes * args.steps, fused_ms), 1),
+             "gateup_us": round(out[1] / args.steps * 1e3, 3), "down_us": round(out[2] / args.steps * 1e3, 3)}
     gu_bytes = w_gate.nbytes + w_up.nbytes + q8_bytes(1, K) + 4 * 2 * FF
-    gu_ms = out[1] / args.steps
     dn_bytes = w_down.nbytes + q8_bytes(1, FF) + 4 * K
-    dn_ms = out[2] / args.steps
     achieved = gbs(gu_bytes, gu_ms)
 
     # ---------------------------------------------------------------- prefill GEMM (config 4)
@@ -234,6 +246,7 @@ def main():
                      "avg_launch_us": round(gu_ms * 1e3, 3)},
         "down_gemv": {"kernel": "k_gemv<FmtQ6KRaw,1,3,4>", "avg_launch_us": round(dn_ms * 1e3, 3),
                       "GBps": round(gbs(dn_bytes, dn_ms), 1)},
+        "decode_ffn_fused_quantizer": fused,
         "gemv_config1_3072x3072": {"us": round(c1ms * 1e3, 2),
                                    "GBps": round(gbs(c1.nbytes + q8_bytes(1, K) + 4 * K, c1ms), 1)},
         "gemv_config3_9216x3072": rows_res,

@@ -30,7 +30,7 @@ EXPORTS = [
     "bq_verify_fused", "bq_q6_verify_fused", "bq_gemm_q6k_dp", "bq_gemm_q6k_raw", "bq_try_mmq",
     "bq_gemm_q6k_mma", "bq_gemm_b", "bq_gemm_b_fused", "bq_repack_q5k", "bq_repack_q5k_bytes",
     "bq_repack_q5k_min_bytes", "bq_repack_q6k", "bq_repack_q6k_host", "bq_repack_q6k_bytes",
-    "bq_time_next_launch",
+    "bq_time_next_launch", "bq_gemv_q8_fused",
 ]
 
 
@@ -83,6 +83,7 @@ def load(path=LIB_PATH):
         "bq_repack_q6k_host": (I, [P, I, I, P]),
         "bq_repack_q6k_bytes": (S, [I, I]),
         "bq_time_next_launch": (I, [P, P]),
+        "bq_gemv_q8_fused": (I, [P, P, I, P, P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -169,6 +170,16 @@ def verify_fused(ys, ws, rows, xq, xd, xsum, xoff=0):
     r = load().bq_verify_fused(yarr, warr, len(ws), rows, _ptr(xq), _ptr(xd), _ptr(xsum), xoff, _stream())
     if r not in (BQ_OK, BQ_UNSUPPORTED):
         raise BqError(r, "bq_verify_fused")
+    return r
+
+
+def gemv_q8_fused(ys, ws, x, xq=None, xd=None, xsum=None):
+    """Quantize the fp32 row x and run the GEMV over every part in one launch;
+    xq/xd/xsum (all or none) receive the q8 row."""
+    yarr, warr = _arrays(ys, ws)
+    r = load().bq_gemv_q8_fused(yarr, warr, len(ws), _ptr(x), _ptr(xq), _ptr(xd), _ptr(xsum), _stream())
+    if r not in (BQ_OK, BQ_UNSUPPORTED):
+        raise BqError(r, "bq_gemv_q8_fused")
     return r
 
 

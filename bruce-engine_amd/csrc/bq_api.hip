@@ -201,6 +201,44 @@ int bq_q6_verify_fused(float* const* ys, const bq_weight* const* ws, int nparts,
                      nullptr, (hipStream_t)st);
 }
 
+int bq_gemv_q8_fused(float* const* ys, const bq_weight* const* ws, int nparts, const float* x,
+                     int8_t* xq, float* xd, int32_t* xsum, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (nparts < 1 || nparts > BQ_MAX_PARTS) return BQ_UNSUPPORTED;
+    if (!ys || !ws || !ws[0] || !x) return BQ_EINVAL;
+    if ((xq != nullptr) != (xd != nullptr) || (xq != nullptr) != (xsum != nullptr)) return BQ_EINVAL;
+    const int K = ws[0]->K;
+    const uint32_t type = ws[0]->ggml_type;
+    const bool q6rep = type == BQ_TYPE_Q6_K && ws[0]->rep;
+    PartTable pt;
+    memset(&pt, 0, sizeof(pt));
+    for (int p = 0; p < nparts; ++p) {
+        const bq_weight* w = ws[p];
+        if (!weight_ok(w) || !ys[p]) return BQ_EINVAL;
+        if (w->K != K || w->ggml_type != type) return BQ_UNSUPPORTED;
+        if (type == BQ_TYPE_Q5_K) {
+            if (!w->raw) return BQ_UNSUPPORTED;
+            pt.W[p] = w->raw;
+        } else if (type == BQ_TYPE_Q6_K) {
+            if ((w->rep != nullptr) != q6rep || (!q6rep && !w->raw)) return BQ_UNSUPPORTED;
+            pt.W[p] = q6rep ? w->rep : w->raw;
+        } else {
+            return BQ_UNSUPPORTED;
+        }
+        pt.Y[p] = ys[p];
+        pt.N[p] = w->N;
+    }
+    pt.nparts = nparts;
+    const GemvKind kind = type == BQ_TYPE_Q5_K ? GemvKind::Q5K : (q6rep ? GemvKind::Q6KRep : GemvKind::Q6KRaw);
+    hipStream_t s = (hipStream_t)st;
+    if (gemv_fused_supported(K)) return from_hip(launch_gemv_fused_q8(kind, pt, K, x, xq, xd, xsum, s));
+    // longer rows: quantizer launch, then the GEMV (needs the q8 buffers)
+    if (!xq) return BQ_UNSUPPORTED;
+    hipError_t e = launch_quant_q8(x, 1, K, xq, xd, xsum, nullptr, s);
+    if (e != hipSuccess) return from_hip(e);
+    return gemv_rows(kind, pt, 1, K, xq, xd, type == BQ_TYPE_Q5_K ? xsum : nullptr, s);
+}
+
 int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
                const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
                bq_stream_t st) {

@@ -39,25 +39,40 @@ extern "C" {
 
 // One decode FFN step per iteration, weight set s = i % nsets (sets rotate so
 // that the working set exceeds the 256 MB last-level cache).
-// mode 0: each set's step is captured once into a HIP graph and the timed
-//         region replays graph[i % nsets] -- the reference replays a captured
-//         CUDA graph per decoded token (bruce.cu:8246-8252).
+// mode 0: nsets consecutive steps (sets 0..nsets-1) are captured into one
+//         HIP graph and the timed region replays it -- the reference replays
+//         one captured CUDA graph per decoded token, i.e. per layer stack
+//         (bruce.cu:8246-8252).
 //         out[0] = timed region (ms, `steps` steps).
 // mode 1: direct launches, the two GEMV kernels timed with dispatch events.
 //         out[0] = timed region, out[1] / out[2] = summed gate+up / down
 //         kernel durations (ms).
+// mode | 2: the same step with bq_gemv_q8_fused (each GEMV quantizes its own
+//         fp32 input: two launches per step instead of four); the q8 rows are
+//         still written out.
 int bqb_decode_ffn(int mode, int steps, int warmup, int nsets, const bq_weight* gate, const bq_weight* up,
                    const bq_weight* down, const float* x, const float* t, int8_t* xq, float* xd,
                    int32_t* xs, int8_t* tq, float* td, int32_t* ts, float* yg, float* yu, float* yd,
                    bq_stream_t st, double* out) {
     const int K = gate[0].K, KD = down[0].K;
+    const bool fused = (mode & 2) != 0;
+    mode &= 1;
     auto step = [&](int i, hipEvent_t g0, hipEvent_t g1, hipEvent_t d0, hipEvent_t d1,
                     bq_stream_t s_) -> int {
         const int s = i % nsets;
-        int r = bq_quantize_q8(x, 1, K, xq, xd, xs, nullptr, s_);
-        if (r) return r;
         float* ys[2] = {yg, yu};
         const bq_weight* ws[2] = {&gate[s], &up[s]};
+        if (fused) {
+            if (g0) bq_time_next_launch(g0, g1);
+            int r = bq_gemv_q8_fused(ys, ws, 2, x, xq, xd, xs, s_);
+            if (r) return r;
+            float* yd_[1] = {yd};
+            const bq_weight* wd[1] = {&down[s]};
+            if (d0) bq_time_next_launch(d0, d1);
+            return bq_gemv_q8_fused(yd_, wd, 1, t, tq, td, ts, s_);
+        }
+        int r = bq_quantize_q8(x, 1, K, xq, xd, xs, nullptr, s_);
+        if (r) return r;
         if (g0) bq_time_next_launch(g0, g1);
         r = bq_verify_fused(ys, ws, 2, 1, xq, xd, xs, 0, s_);
         if (r) return r;
@@ -70,26 +85,36 @@ int bqb_decode_ffn(int mode, int steps, int warmup, int nsets, const bq_weight* 
         if (int r = step(i, nullptr, nullptr, nullptr, nullptr, st)) return r;
     out[0] = out[1] = out[2] = 0.0;
     if (mode == 0) {
+        // one graph holds nsets consecutive steps (one per weight set, like a
+        // token's layer stack); a second graph holds the steps % nsets tail
         hipStream_t cs;
         if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) return -1;
-        std::vector<hipGraphExec_t> ex(nsets, nullptr);
-        for (int s = 0; s < nsets; ++s) {
+        auto capture = [&](int n, hipGraphExec_t* ex) -> int {
+            *ex = nullptr;
+            if (n == 0) return 0;
             hipGraph_t g;
             hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
-            const int r = step(s, nullptr, nullptr, nullptr, nullptr, (bq_stream_t)cs);
+            int r = 0;
+            for (int i = 0; i < n && !r; ++i) r = step(i, nullptr, nullptr, nullptr, nullptr, (bq_stream_t)cs);
             if (hipStreamEndCapture(cs, &g) != hipSuccess || r) return r ? r : -1;
-            if (hipGraphInstantiate(&ex[s], g, nullptr, nullptr, 0) != hipSuccess) return -1;
+            const hipError_t e = hipGraphInstantiate(ex, g, nullptr, nullptr, 0);
             hipGraphDestroy(g);
-        }
-        for (int i = 0; i < nsets; ++i) hipGraphLaunch(ex[i], (hipStream_t)st);  // warm the graphs
+            return e == hipSuccess ? 0 : -1;
+        };
+        hipGraphExec_t full, tail;
+        if (int r = capture(nsets, &full)) return r;
+        if (int r = capture(steps % nsets, &tail)) return r;
+        hipGraphLaunch(full, (hipStream_t)st);  // warm the graph
         EventPool pool(2);
         hipDeviceSynchronize();
         hipEventRecord(pool.ev[0], (hipStream_t)st);
-        for (int i = 0; i < steps; ++i) hipGraphLaunch(ex[i % nsets], (hipStream_t)st);
+        for (int i = 0; i < steps / nsets; ++i) hipGraphLaunch(full, (hipStream_t)st);
+        if (tail) hipGraphLaunch(tail, (hipStream_t)st);
         hipEventRecord(pool.ev[1], (hipStream_t)st);
         hipDeviceSynchronize();
         out[0] = elapsed(pool.ev[0], pool.ev[1]);
-        for (auto e : ex) hipGraphExecDestroy(e);
+        hipGraphExecDestroy(full);
+        if (tail) hipGraphExecDestroy(tail);
         hipStreamDestroy(cs);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }

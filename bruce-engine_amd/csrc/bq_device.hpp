@@ -76,6 +76,8 @@ BQ_DEV u32x4 ld16_a2(const uint8_t* p) {
 // vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
 #define BQ_WAIT_VM(n) \
     __builtin_amdgcn_s_waitcnt(((n) & 0xF) | ((((n) >> 4) & 3) << 14) | 0x70 | 0xF00)
+// s_waitcnt lgkmcnt(0) only (LDS writes done; vector loads may stay in flight)
+#define BQ_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
 
 // Wave64 sum.  Butterfly over the 64 lanes; every lane ends with the total.
 BQ_DEV float wave_sum(float v) {
@@ -87,6 +89,29 @@ BQ_DEV int wave_sum_i(int v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
+}
+
+// Per-32 q8 quantization of 4 values per lane, 8 consecutive lanes per group
+// (bruce.cu:518-539 semantics: d = amax*(1/127), id = d > 0 ? 1/d : 0,
+// q = clamp(rint(v*id), -127, 127), sum = sum q).  All 8 lanes of a group must
+// execute it together.  Returns the 4 codes packed little-endian.
+BQ_DEV uint32_t q8_quant4(const f32x4& v, float& d, int& s) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    d = amax * (1.f / 127.f);
+    const float id = d > 0.f ? 1.f / d : 0.f;
+    const int q0 = max(-127, min(127, (int)__builtin_rintf(v.x * id)));
+    const int q1 = max(-127, min(127, (int)__builtin_rintf(v.y * id)));
+    const int q2 = max(-127, min(127, (int)__builtin_rintf(v.z * id)));
+    const int q3 = max(-127, min(127, (int)__builtin_rintf(v.w * id)));
+    s = q0 + q1 + q2 + q3;
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 4, 64);
+    return (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+           ((uint32_t)(q3 & 0xFF) << 24);
 }
 
 // 6-bit scale and min of Q5_K sub-block j from the three scale words

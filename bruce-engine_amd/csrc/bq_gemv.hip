@@ -276,28 +276,54 @@ BQ_DEV void dma_to_lds(uint8_t* lds, const void* src, int bytes, int wave, int l
     }
 }
 
+// Fused-quantizer arguments: the fp32 activation row and optional q8 outputs
+// (written by workgroup 0 only; NULL = not written).
+struct FusedQ8 {
+    const float* x;
+    int8_t* xq;
+    float* xd;
+    int32_t* xsum;
+};
+constexpr int kFusedWaves = 4;
+constexpr int kFusedMaxK = 12288;  // = 4 K slices x 3 steps x 16 tasks x 64 values
+constexpr int kFusedQ = kFusedMaxK / 4 / (64 * kFusedWaves);  // float4 loads per lane
+
 // ---------------------------------------------------------------------------
 // The kernel: WAVES waves per workgroup, a wave owns (tile of 4 rows, K slice
 // ks of KS), SPS steps of 16 tasks per row; MR activation rows.
+// FQ: the workgroup quantizes one fp32 activation row itself (bit-exact with
+// k_quant_q8) instead of copying q8 activations: the fp32 loads are issued
+// before the weight loads, the codes go from registers into LDS.
 // ---------------------------------------------------------------------------
-template <class F, int MR, int SPS, int WAVES>
+template <class F, int MR, int SPS, int WAVES, bool FQ = false>
 __global__ void __launch_bounds__(64 * WAVES)
 k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* __restrict__ xd,
-       const int32_t* __restrict__ xsum) {
+       const int32_t* __restrict__ xsum, FusedQ8 fq) {
+    static_assert(!FQ || (MR == 1 && WAVES == kFusedWaves), "fused quantizer: one row, 4 waves");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
     const int nb = K >> 5;
-    // ---- 1. activations -> LDS (asynchronous)
+    // ---- 1. activations -> LDS (asynchronous), or fp32 row -> registers
     ActLds act;
     act.x = (const int8_t*)smem;
     act.xd = (const float*)(smem + MR * K);
     act.xs = (const int32_t*)(act.xd + MR * nb);
     float* part_sums = (float*)(smem + act_lds_bytes<F>(MR, K));  // [WAVES][MR][4]
-    dma_to_lds<WAVES>(smem, xq, MR * K, wave, lane);
-    dma_to_lds<WAVES>(smem + MR * K, xd, MR * nb * 4, wave, lane);
-    if constexpr (std::is_same<F, FmtQ5K>::value)
-        dma_to_lds<WAVES>(smem + MR * K + MR * nb * 4, xsum, MR * nb * 4, wave, lane);
+    constexpr int QN = FQ ? kFusedQ : 1;
+    f32x4 xv[QN];
+    if constexpr (FQ) {
+        // float4 f = threadIdx.x + 256*i; K % 256 == 0 makes liveness wave-uniform
+#pragma unroll
+        for (int i = 0; i < QN; ++i)
+            if (64 * (WAVES * i + wave) < (K >> 2))
+                xv[i] = *(const f32x4*)(fq.x + 4 * (threadIdx.x + 64 * WAVES * i));
+    } else {
+        dma_to_lds<WAVES>(smem, xq, MR * K, wave, lane);
+        dma_to_lds<WAVES>(smem + MR * K, xd, MR * nb * 4, wave, lane);
+        if constexpr (std::is_same<F, FmtQ5K>::value)
+            dma_to_lds<WAVES>(smem + MR * K + MR * nb * 4, xsum, MR * nb * 4, wave, lane);
+    }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 
@@ -321,9 +347,39 @@ k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* 
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- 3. own DMA done (only the weight loads may still be outstanding)
+    // ---- 3. own DMA / fp32 loads done (only the weight loads may still be outstanding)
     BQ_WAIT_VM(F::kLoads * SPS);
+    if constexpr (FQ) {
+        uint8_t* lx = smem;
+        float* lxd = (float*)(smem + K);
+        int32_t* lxs = (int32_t*)(lxd + nb);
+        const bool out = blockIdx.x == 0 && fq.xq;
+#pragma unroll
+        for (int i = 0; i < QN; ++i) {
+            if (64 * (WAVES * i + wave) < (K >> 2)) {
+                float d;
+                int s;
+                const uint32_t pk = q8_quant4(xv[i], d, s);
+                const int f = threadIdx.x + 64 * WAVES * i, gi = f >> 3;
+                *(uint32_t*)(lx + 4 * f) = pk;
+                if ((lane & 7) == 0) {
+                    lxd[gi] = d;
+                    if constexpr (std::is_same<F, FmtQ5K>::value) lxs[gi] = s;
+                }
+                if (out) {
+                    *(uint32_t*)(fq.xq + 4 * f) = pk;
+                    if ((lane & 7) == 0) {
+                        fq.xd[gi] = d;
+                        fq.xsum[gi] = s;
+                    }
+                }
+            }
+        }
+        asm volatile("" ::: "memory");
+        BQ_WAIT_LGKM0();
+    }
     __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 
     // ---- 4. compute, step by step as the loads return
     float acc[MR];
@@ -393,14 +449,14 @@ static void k_split(int K, int& KS, int& SPS) {
     SPS = (spt + KS - 1) / KS;
 }
 
-template <class F, int MR, int SPS, int WAVES>
+template <class F, int MR, int SPS, int WAVES, bool FQ = false>
 static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* xq, const float* xd,
-                             const int32_t* xsum, hipStream_t st) {
+                             const int32_t* xsum, hipStream_t st, FusedQ8 fq = {}) {
     const size_t lds = act_lds_bytes<F>(MR, K) + (size_t)WAVES * MR * 4 * sizeof(float);
     const int RT = WAVES / KS;
     const int blocks = (pt.ntiles + RT - 1) / RT;
-    launch_kernel((k_gemv<F, MR, SPS, WAVES>), dim3(blocks), dim3(64 * WAVES), lds, st, pt, K, KS,
-                       xq, xd, xsum);
+    launch_kernel((k_gemv<F, MR, SPS, WAVES, FQ>), dim3(blocks), dim3(64 * WAVES), lds, st, pt, K, KS,
+                  xq, xd, xsum, fq);
     return hipGetLastError();
 }
 
@@ -454,6 +510,37 @@ hipError_t launch_gemv(GemvKind kind, PartTable pt, int rows, int K, const int8_
         case GemvKind::Q5K: return dispatch_rows<FmtQ5K>(rows, pt, K, xq, xd, xsum, st);
         case GemvKind::Q6KRaw: return dispatch_rows<FmtQ6KRaw>(rows, pt, K, xq, xd, xsum, st);
         default: return dispatch_rows<FmtQ6KRep>(rows, pt, K, xq, xd, xsum, st);
+    }
+}
+
+template <class F>
+static hipError_t dispatch_fused(const PartTable& pt, int K, const FusedQ8& fq, hipStream_t st) {
+    int KS, SPS;
+    k_split(K, KS, SPS);
+    if (K > kFusedMaxK || KS > 4) return hipErrorInvalidValue;
+    switch (SPS) {
+        case 1: return launch_fmt<F, 1, 1, kFusedWaves, true>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
+        case 2: return launch_fmt<F, 1, 2, kFusedWaves, true>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
+        default: return launch_fmt<F, 1, 3, kFusedWaves, true>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
+    }
+}
+
+bool gemv_fused_supported(int K) { return K > 0 && K % 256 == 0 && K <= kFusedMaxK; }
+
+// one fp32 activation row x[K], quantized inside the GEMV; q8 outputs optional
+hipError_t launch_gemv_fused_q8(GemvKind kind, PartTable pt, int K, const float* x, int8_t* xq,
+                                float* xd, int32_t* xsum, hipStream_t st) {
+    if (!gemv_fused_supported(K)) return hipErrorInvalidValue;
+    build_tiles(pt);
+    const FusedQ8 fq{x, xq, xd, xsum};
+    if (pt.ntiles == 0) {
+        // no weight rows: the q8 outputs are still produced
+        return xq ? launch_quant_q8(x, 1, K, xq, xd, xsum, nullptr, st) : hipSuccess;
+    }
+    switch (kind) {
+        case GemvKind::Q5K: return dispatch_fused<FmtQ5K>(pt, K, fq, st);
+        case GemvKind::Q6KRaw: return dispatch_fused<FmtQ6KRaw>(pt, K, fq, st);
+        default: return dispatch_fused<FmtQ6KRep>(pt, K, fq, st);
     }
 }
 

@@ -48,6 +48,11 @@ hipError_t launch_quant_q8(const float* x, int rows, int K, int8_t* xq, float* x
 hipError_t launch_fill_xdh(const float* xd, const int32_t* xsum, int n, uint16_t* xdh, hipStream_t st);
 
 void gemv_set_cus(int cus);
+// Fused quantize + GEMV of one fp32 activation row (K % 256 == 0, K <= 12288);
+// xq/xd/xsum receive the q8 row when xq != NULL.
+bool gemv_fused_supported(int K);
+hipError_t launch_gemv_fused_q8(GemvKind kind, PartTable pt, int K, const float* x, int8_t* xq,
+                                float* xd, int32_t* xsum, hipStream_t st);
 size_t gemv_lds_bytes(GemvKind kind, int rows, int K);
 hipError_t launch_gemv(GemvKind kind, PartTable pt, int rows, int K, const int8_t* xq,
                        const float* xd, const int32_t* xsum, hipStream_t st);

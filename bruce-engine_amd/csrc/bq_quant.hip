@@ -24,27 +24,10 @@ __global__ void __launch_bounds__(256) k_quant_q8(const float* __restrict__ x, i
     const bool live = g < ngroups;
     f32x4 v = {0.f, 0.f, 0.f, 0.f};
     if (live) v = *(const f32x4*)(x + (size_t)tid * 4);
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-    const float d = amax * (1.f / 127.f);
-    const float id = d > 0.f ? 1.f / d : 0.f;
-    int q0 = (int)__builtin_rintf(v.x * id);
-    int q1 = (int)__builtin_rintf(v.y * id);
-    int q2 = (int)__builtin_rintf(v.z * id);
-    int q3 = (int)__builtin_rintf(v.w * id);
-    q0 = max(-127, min(127, q0));
-    q1 = max(-127, min(127, q1));
-    q2 = max(-127, min(127, q2));
-    q3 = max(-127, min(127, q3));
-    int s = q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
+    float d;
+    int s;
+    const uint32_t packed = q8_quant4(v, d, s);
     if (!live) return;
-    const uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) |
-                            ((uint32_t)(q2 & 0xFF) << 16) | ((uint32_t)(q3 & 0xFF) << 24);
     *(uint32_t*)(xq + (size_t)tid * 4) = packed;
     if ((tid & 7) == 0) {
         xd[g] = d;

@@ -99,6 +99,18 @@ int bq_gemm_q6k_dp(float* y, const bq_weight* w, int rows, const int8_t* xq, con
 int bq_gemm_q6k_raw(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
                     int xoff, bq_stream_t st);
 
+/* Fused quantize + GEMV of one fp32 activation row x[K] against nparts (1..4)
+ * matrices of one type sharing K (all Q5_K raw, or all Q6_K: W160 repacks if
+ * part 0 has one, else raw blocks).  Replaces the decode pair "quantize, then
+ * GEMV" -- k_q8_quant (bruce.cu:518-539) followed by launch_verify_fused rows==1
+ * (:7141-7229) or launch_gemv (:5624-5640) -- with one launch: every workgroup
+ * quantizes x itself, bit-exactly as bq_quantize_q8.  xq/xd/xsum (all three or
+ * none) receive the q8 row for later consumers.  K % 256 == 0; K > 12288 runs
+ * bq_quantize_q8 then the GEMV and needs the q8 buffers (else BQ_UNSUPPORTED).
+ * An extension of this library: the reference has no single-launch form. */
+int bq_gemv_q8_fused(float* const* ys, const bq_weight* const* ws, int nparts, const float* x,
+                     int8_t* xq, float* xd, int32_t* xsum, bq_stream_t st);
+
 /* ---- prefill GEMM ----------------------------------------------------------
  * Y_p[M][N_p] for nparts (1..4) Q5_K matrices, 128x128 tiles on int8 MFMA.
  * Replaces try_launch_mmq (bruce.cu:7366-7419).  rows >= 96 (the reference's

@@ -215,6 +215,74 @@ def test_q6_verify_fused(bq, oracle):
         assert oracle.normwise_err(host(y), oracle.gemm_q6k(r, xq, xd)) < TOL
 
 
+# ---------------------------------------------------------------- fused quantize + GEMV
+@pytest.mark.parametrize("qtype,K,Ns,rep", [
+    ("q5k", 3072, [512, 1024], False),     # config-2 gate+up shape class
+    ("q5k", 256, [48], False),
+    ("q5k", 12288, [64, 32, 16, 80], False),  # largest fused K, 4 parts
+    ("q5k", 12800, [32], False),           # K > 12288: quantizer launch + GEMV
+    ("q6k", 9216, [3072], False),          # config-2 down projection
+    ("q6k", 1024, [130], True),
+])
+def test_gemv_q8_fused(bq, oracle, qtype, K, Ns, rep):
+    """One launch quantizes x and runs the GEMV: q8 outputs bit-exact with the
+    oracle quantizer, y within TOL of the oracle and bit-identical to the
+    unfused pair (same kernel arithmetic once the codes are in LDS)."""
+    import torch
+    x, _ = acts(1000 + K, 1, K)
+    x[0, :32] = 0.0                                  # an all-zero group
+    xq, xd, xs = oracle.q8_rows(x)
+    raws = [weights(1010 + i, n, K, qtype) for i, n in enumerate(Ns)]
+    tp = bq.TYPE_Q5_K if qtype == "q5k" else bq.TYPE_Q6_K
+    ws = []
+    for r, n in zip(raws, Ns):
+        g = dev(r)
+        ws.append(bq.make_weight(g, tp, K, n, rep=bq.repack_q6k(g, K, n) if rep else None))
+    ys = [torch.full((n,), float("nan"), device="cuda") for n in Ns]
+    gx = dev(x)
+    gq = torch.full((1, K), 99, dtype=torch.int8, device="cuda")
+    gd = torch.full((1, K // 32), float("nan"), device="cuda")
+    gs = torch.full((1, K // 32), -7, dtype=torch.int32, device="cuda")
+    assert bq.gemv_q8_fused(ys, ws, gx, gq, gd, gs) == bq.BQ_OK
+    torch.cuda.synchronize()
+    assert np.array_equal(host(gq), xq)
+    assert np.array_equal(host(gd).view(np.uint32), xd.view(np.uint32))
+    assert np.array_equal(host(gs), xs)
+    for r, y, w in zip(raws, ys, ws):
+        ref = oracle.gemm_q5k(r, xq, xd, xs) if qtype == "q5k" else oracle.gemm_q6k(r, xq, xd)
+        assert oracle.normwise_err(host(y)[None], ref) < TOL
+        y2 = torch.full_like(y, float("nan"))
+        bq.gemv(y2, w, gq, gd, gs)
+        torch.cuda.synchronize()
+        assert np.array_equal(host(y2).view(np.uint32), host(y).view(np.uint32))
+    if K <= 12288:                                   # fused kernel without q8 outputs
+        ys3 = [torch.full((n,), float("nan"), device="cuda") for n in Ns]
+        assert bq.gemv_q8_fused(ys3, ws, gx) == bq.BQ_OK
+        torch.cuda.synchronize()
+        for y, y3 in zip(ys, ys3):
+            assert np.array_equal(host(y3).view(np.uint32), host(y).view(np.uint32))
+    else:
+        assert bq.gemv_q8_fused(ys, ws, gx) == bq.BQ_UNSUPPORTED
+
+
+def test_gemv_q8_fused_rejects(bq):
+    import torch
+    K = 512
+    raw5 = torch.zeros((16, K // 256 * 176), dtype=torch.uint8, device="cuda")
+    raw6 = torch.zeros((16, K // 256 * 210), dtype=torch.uint8, device="cuda")
+    w5 = bq.make_weight(raw5, bq.TYPE_Q5_K, K, 16)
+    w6 = bq.make_weight(raw6, bq.TYPE_Q6_K, K, 16)
+    w5b = bq.make_weight(raw5, bq.TYPE_Q5_K, 256, 32)
+    y = torch.zeros(16, device="cuda")
+    x = torch.zeros(K, device="cuda")
+    assert bq.gemv_q8_fused([y, y], [w5, w6], x) == bq.BQ_UNSUPPORTED   # mixed types
+    assert bq.gemv_q8_fused([y, y], [w5, w5b], x) == bq.BQ_UNSUPPORTED  # mismatched K
+    assert bq.gemv_q8_fused([y] * 5, [w5] * 5, x) == bq.BQ_UNSUPPORTED  # > 4 parts
+    xq = torch.zeros(K, dtype=torch.int8, device="cuda")
+    with pytest.raises(bq.BqError):                                    # xq without xd/xsum
+        bq.gemv_q8_fused([y], [w5], x, xq)
+
+
 # ---------------------------------------------------------------- prefill GEMM
 def _mmq_case(bq, oracle, seed, M, Ns, K, prepacked):
     import torch
