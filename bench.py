@@ -2,18 +2,21 @@
 """Benchmark of the MI355X k-quant matmul path (libbq) on one GPU.
 
 Headline (BASELINE metric "GEMV GB/s (% HBM peak) at batch 1"): the decode FFN
-GEMV set of BASELINE config 2 -- per step, quantize the block input (q8),
-fused gate+up Q5_K GEMV 2 x (9216 x 3072), quantize the down-projection input,
-down Q6_K GEMV 3072 x 9216 -- batch 1, synthetic Gaussian data, weight sets
-rotated so the working set exceeds the 256 MB last-level cache.  `value` is
-algorithmic bytes (GGUF weight bytes + q8 activations + fp32 outputs) per
-step x steps / timed region.
+GEMV set of BASELINE config 2 -- per step, quantize the block input (q8) and
+run the fused gate+up Q5_K GEMV 2 x (9216 x 3072), then quantize the
+down-projection input and run the down Q6_K GEMV 3072 x 9216 -- batch 1,
+synthetic Gaussian data, weight sets rotated so the working set exceeds the
+256 MB last-level cache.  Each quantize+GEMV pair is one bq_gemv_q8_fused
+launch; the reference's four-launch form (bq_quantize_q8 + GEMV, twice) is
+reported beside it.  Steps are replayed from a HIP graph holding one step per
+weight set.  `value` is algorithmic bytes (GGUF weight bytes + q8 activations
++ fp32 outputs) per step x steps / timed region.
 
 Also reported: the prefill GEMM of config 4 (M = 2048, int8 MFMA, TOPS and
 fraction of the dense int8 peak), the multi-row GEMV of config 3, config 1,
 and the reference's scalar host loop timed on this machine's CPU.
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--decode-only]
 """
 import argparse
 import ctypes
@@ -78,6 +81,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode FFN step (for kernel traces); implies --no-cpu")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the k-quant matmul path has no multi-GPU mode in this "
@@ -141,89 +146,86 @@ def main():
 
     # ---------------------------------------------------------------- decode FFN step
     out = D4()
-    # timed region: K graph-replayed steps (the headline value)
-    r = B.bqb_decode_ffn(0, args.steps, args.warmup, nsets, gates, ups, downs, ptr(dx), ptr(dt), ptr(xq),
-                         ptr(xd), ptr(xs), ptr(tq), ptr(td), ptr(ts), ptr(yg), ptr(yu), ptr(yd), sp, out)
-    if r != 0:
-        raise RuntimeError(f"bqb_decode_ffn failed: {r} {bq.strerror(r)}")
     step_bytes = wbytes + q8_bytes(1, K) + q8_bytes(1, FF) + 4 * (2 * FF + K)
-    total_ms = out[0]
+
+    def decode(mode, warmup):
+        r = B.bqb_decode_ffn(mode, args.steps, warmup, nsets, gates, ups, downs, ptr(dx), ptr(dt), ptr(xq),
+                             ptr(xd), ptr(xs), ptr(tq), ptr(td), ptr(ts), ptr(yg), ptr(yu), ptr(yd), sp, out)
+        if r != 0:
+            raise RuntimeError(f"bqb_decode_ffn(mode {mode}) failed: {r} {bq.strerror(r)}")
+        return out[0], out[1] / args.steps, out[2] / args.steps
+
+    # headline: K steps of the fused form (bq_gemv_q8_fused: each GEMV quantizes
+    # its fp32 input), replayed from HIP graphs -- the timed region
+    total_ms, _, _ = decode(2, args.warmup)
     # second timed region, same K steps launched directly: the GEMV kernels'
     # own durations from dispatch start/end events
-    r = B.bqb_decode_ffn(1, args.steps, 0, nsets, gates, ups, downs, ptr(dx), ptr(dt), ptr(xq),
-                         ptr(xd), ptr(xs), ptr(tq), ptr(td), ptr(ts), ptr(yg), ptr(yu), ptr(yd), sp, out)
-    if r != 0:
-        raise RuntimeError(f"bqb_decode_ffn (kernel timing) failed: {r} {bq.strerror(r)}")
+    _, gu_ms, dn_ms = decode(3, 0)
     value = gbs(step_bytes * args.steps, total_ms)
-    gu_ms, dn_ms = out[1] / args.steps, out[2] / args.steps
-    # the same step through bq_gemv_q8_fused (quantizer inside each GEMV)
-    r = B.bqb_decode_ffn(2, args.steps, args.warmup, nsets, gates, ups, downs, ptr(dx), ptr(dt), ptr(xq),
-                         ptr(xd), ptr(xs), ptr(tq), ptr(td), ptr(ts), ptr(yg), ptr(yu), ptr(yd), sp, out)
-    if r != 0:
-        raise RuntimeError(f"bqb_decode_ffn (fused) failed: {r} {bq.strerror(r)}")
-    fused_ms = out[0]
-    r = B.bqb_decode_ffn(3, args.steps, 0, nsets, gates, ups, downs, ptr(dx), ptr(dt), ptr(xq),
-                         ptr(xd), ptr(xs), ptr(tq), ptr(td), ptr(ts), ptr(yg), ptr(yu), ptr(yd), sp, out)
-    if r != 0:
-        raise RuntimeError(f"bqb_decode_ffn (fused, kernel timing) failed: {r} {bq.strerror(r)}")
-    fused = {"ms_per_step": round(fused_ms / args.steps, 5),
-             "GBps": round(gbs(step_bytes * args.steps, fused_ms), 1),
-             "gateup_us": round(out[1] / args.steps * 1e3, 3), "down_us": round(out[2] / args.steps * 1e3, 3)}
-    gu_bytes = w_gate.nbytes + w_up.nbytes + q8_bytes(1, K) + 4 * 2 * FF
-    dn_bytes = w_down.nbytes + q8_bytes(1, FF) + 4 * K
+    # the same step as the reference issues it: quantize, GEMV, quantize, GEMV
+    un_ms, un_gu, un_dn = decode(0, args.warmup)
+    _, un_gu, un_dn = decode(1, 0)
+    unfused = {"ms_per_step": round(un_ms / args.steps, 5), "GBps": round(gbs(step_bytes * args.steps, un_ms), 1),
+               "gateup_us": round(un_gu * 1e3, 3), "down_us": round(un_dn * 1e3, 3)}
+    # fused gate+up launch: fp32 x in, q8 x out, both weight matrices, two fp32 outputs
+    gu_bytes = w_gate.nbytes + w_up.nbytes + 4 * K + q8_bytes(1, K) + 4 * 2 * FF
+    dn_bytes = w_down.nbytes + 4 * FF + q8_bytes(1, FF) + 4 * K
     achieved = gbs(gu_bytes, gu_ms)
 
-    # ---------------------------------------------------------------- prefill GEMM (config 4)
-    gemm = {}
-    gw144, gdm = bq.repack_q5k(g_gate, K, FF)
-    for M in (2048, 512, 8192):
-        xm = torch.from_numpy(synth.gaussian(SEED + 6, (M, K))).cuda()
-        mq, md, ms_, mh = bq.quantize_q8(xm, with_xdh=True)
-        ym = torch.empty((M, FF), device="cuda")
-        res = {}
-        for name, w in (("w144", bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF, rep=gw144, rep_min=gdm)),
-                        ("raw", bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF))):
-            gsteps = 20 if M == 8192 else 50
-            r = B.bqb_gemm(gsteps, 5, ctypes.byref(w), M, ptr(mq), ptr(md), ptr(ms_), ptr(mh), ptr(ym), sp, out)
-            if r != 0:
-                raise RuntimeError(f"bqb_gemm failed: {r}")
-            kms = out[1] / gsteps
-            tops = 2.0 * M * FF * K / (kms * 1e-3) / 1e12
-            res[name] = {"ms": round(kms, 4), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)}
-        gemm[f"M{M}"] = res
-        del xm, mq, md, ms_, mh, ym
-    g = gemm["M2048"]["w144"]
-    gemm_obj = {
-        "config": "prefill GEMM Q5_K 9216x3072 (W144 repack, fp16 min term), M=2048 q8 tokens, fp32 out",
-        "value": g["tops"], "unit": "TOPS", "ms": g["ms"],
-        "roofline": {"bound": "mfma", "achieved": g["tops"], "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": g["frac"], "traffic": traffic_for("mmq_q5k_144_M2048"),
-                     "kernel": "k_mmq_q5k<Q5W144>", "ops_per_launch": 2 * 2048 * FF * K},
-        "shapes": gemm,
-    }
+    gemm_obj, rows_res, c1_obj = None, None, None
+    if not args.decode_only:
+        # ---------------------------------------------------------------- prefill GEMM (config 4)
+        gemm = {}
+        gw144, gdm = bq.repack_q5k(g_gate, K, FF)
+        for M in (2048, 512, 8192):
+            xm = torch.from_numpy(synth.gaussian(SEED + 6, (M, K))).cuda()
+            mq, md, ms_, mh = bq.quantize_q8(xm, with_xdh=True)
+            ym = torch.empty((M, FF), device="cuda")
+            res = {}
+            for name, w in (("w144", bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF, rep=gw144, rep_min=gdm)),
+                            ("raw", bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF))):
+                gsteps = 20 if M == 8192 else 50
+                r = B.bqb_gemm(gsteps, 5, ctypes.byref(w), M, ptr(mq), ptr(md), ptr(ms_), ptr(mh), ptr(ym), sp, out)
+                if r != 0:
+                    raise RuntimeError(f"bqb_gemm failed: {r}")
+                kms = out[1] / gsteps
+                tops = 2.0 * M * FF * K / (kms * 1e-3) / 1e12
+                res[name] = {"ms": round(kms, 4), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)}
+            gemm[f"M{M}"] = res
+            del xm, mq, md, ms_, mh, ym
+        g = gemm["M2048"]["w144"]
+        gemm_obj = {
+            "config": "prefill GEMM Q5_K 9216x3072 (W144 repack, fp16 min term), M=2048 q8 tokens, fp32 out",
+            "value": g["tops"], "unit": "TOPS", "ms": g["ms"],
+            "roofline": {"bound": "mfma", "achieved": g["tops"], "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                         "frac": g["frac"], "traffic": traffic_for("mmq_q5k_144_M2048"),
+                         "kernel": "k_mmq_q5k<Q5W144>", "ops_per_launch": 2 * 2048 * FF * K},
+            "shapes": gemm,
+        }
 
-    # ---------------------------------------------------------------- config 3 / config 1 GEMV
-    rows_res = {}
-    xr = torch.from_numpy(synth.gaussian(SEED + 7, (8, K))).cuda()
-    rq, rd, rs = bq.quantize_q8(xr)
-    yr = torch.empty((8, FF), device="cuda")
-    gsets = (bq.Weight * nsets)(*[gates[s] for s in range(nsets)])
-    for rows in (1, 2, 4, 8):
-        r = B.bqb_gemv_rows(100, 10, nsets, gsets, rows, ptr(rq), ptr(rd), ptr(rs), ptr(yr), sp, out)
-        kms = out[1] / 100
-        rows_res[f"rows{rows}"] = {"us": round(kms * 1e3, 2),
-                                   "GBps": round(gbs(w_gate.nbytes + q8_bytes(rows, K) + 4 * rows * FF, kms), 1)}
-    c1 = synth.quantize_q5k(synth.gaussian(SEED + 8, (K, K), 0.02))
-    n1 = max(2, math.ceil(3 * LLC_BYTES / c1.nbytes))
-    c1g = [torch.from_numpy(c1).cuda() for _ in range(n1)]
-    c1w = (bq.Weight * n1)(*[bq.make_weight(a, bq.TYPE_Q5_K, K, K) for a in c1g])
-    r = B.bqb_gemv_rows(200, 10, n1, c1w, 1, ptr(rq), ptr(rd), ptr(rs), ptr(yr), sp, out)
-    c1ms = out[1] / 200
-    del c1g
+        # ---------------------------------------------------------------- config 3 / config 1 GEMV
+        rows_res = {}
+        xr = torch.from_numpy(synth.gaussian(SEED + 7, (8, K))).cuda()
+        rq, rd, rs = bq.quantize_q8(xr)
+        yr = torch.empty((8, FF), device="cuda")
+        gsets = (bq.Weight * nsets)(*[gates[s] for s in range(nsets)])
+        for rows in (1, 2, 4, 8):
+            r = B.bqb_gemv_rows(100, 10, nsets, gsets, rows, ptr(rq), ptr(rd), ptr(rs), ptr(yr), sp, out)
+            kms = out[1] / 100
+            rows_res[f"rows{rows}"] = {"us": round(kms * 1e3, 2),
+                                       "GBps": round(gbs(w_gate.nbytes + q8_bytes(rows, K) + 4 * rows * FF, kms), 1)}
+        c1 = synth.quantize_q5k(synth.gaussian(SEED + 8, (K, K), 0.02))
+        n1 = max(2, math.ceil(3 * LLC_BYTES / c1.nbytes))
+        c1g = [torch.from_numpy(c1).cuda() for _ in range(n1)]
+        c1w = (bq.Weight * n1)(*[bq.make_weight(a, bq.TYPE_Q5_K, K, K) for a in c1g])
+        r = B.bqb_gemv_rows(200, 10, n1, c1w, 1, ptr(rq), ptr(rd), ptr(rs), ptr(yr), sp, out)
+        c1ms = out[1] / 200
+        del c1g
+        c1_obj = {"us": round(c1ms * 1e3, 2), "GBps": round(gbs(c1.nbytes + q8_bytes(1, K) + 4 * K, c1ms), 1)}
 
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
-    if not args.no_cpu:
+    if not (args.no_cpu or args.decode_only):
         steps_cpu, el = cpu_baseline(w_gate, w_up, w_down, x, t)
         cpu = {"value": round(gbs(step_bytes * steps_cpu, el * 1e3), 3), "unit": "GB/s", "cores": 1,
                "kind": "port",
@@ -236,19 +238,19 @@ def main():
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
-        "config": {"workload": "BASELINE config 2: decode FFN GEMV set, batch 1 -- q8 quantize, fused "
-                               "gate+up Q5_K 2x(9216x3072), q8 quantize, down Q6_K 3072x9216 (raw GGUF)",
+        "config": {"workload": "BASELINE config 2: decode FFN GEMV set, batch 1 -- q8-quantize x + fused "
+                               "gate+up Q5_K 2x(9216x3072) in one launch, q8-quantize t + down Q6_K "
+                               "3072x9216 (raw GGUF) in one launch (bq_gemv_q8_fused)",
                    "K": K, "FF": FF, "weight_sets_rotated": nsets, "bytes_per_step": step_bytes,
                    "hbm_frac_of_step": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for("gemv_q5k_gateup"),
-                     "kernel": "k_gemv<FmtQ5K,1,3,4> (fused gate+up)", "bytes_per_launch": gu_bytes,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for("gemv_q5k_gateup_fused"),
+                     "kernel": "k_gemv<FmtQ5K,1,3,4,1> (quantize x + gate+up)", "bytes_per_launch": gu_bytes,
                      "avg_launch_us": round(gu_ms * 1e3, 3)},
-        "down_gemv": {"kernel": "k_gemv<FmtQ6KRaw,1,3,4>", "avg_launch_us": round(dn_ms * 1e3, 3),
+        "down_gemv": {"kernel": "k_gemv<FmtQ6KRaw,1,3,4,3> (quantize t + down)", "avg_launch_us": round(dn_ms * 1e3, 3),
                       "GBps": round(gbs(dn_bytes, dn_ms), 1)},
-        "decode_ffn_fused_quantizer": fused,
-        "gemv_config1_3072x3072": {"us": round(c1ms * 1e3, 2),
-                                   "GBps": round(gbs(c1.nbytes + q8_bytes(1, K) + 4 * K, c1ms), 1)},
+        "decode_ffn_unfused": unfused,
+        "gemv_config1_3072x3072": c1_obj,
         "gemv_config3_9216x3072": rows_res,
         "gemm": gemm_obj,
         "cpu_baseline": cpu,

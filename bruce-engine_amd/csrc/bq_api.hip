@@ -48,6 +48,7 @@ bool weight_ok(const bq_weight* w) { return w && w->K > 0 && w->N > 0 && (w->K %
 // Run a multi-row GEMV in row chunks that fit the per-block LDS limit.
 int gemv_rows(GemvKind kind, PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
               const int32_t* xsum, hipStream_t st) {
+    if (K > kGemvMaxK) return BQ_UNSUPPORTED;
     int r0 = 0;
     while (r0 < rows) {
         int c = std::min(rows - r0, (int)BQ_MAX_ROWS);
@@ -231,12 +232,8 @@ int bq_gemv_q8_fused(float* const* ys, const bq_weight* const* ws, int nparts, c
     pt.nparts = nparts;
     const GemvKind kind = type == BQ_TYPE_Q5_K ? GemvKind::Q5K : (q6rep ? GemvKind::Q6KRep : GemvKind::Q6KRaw);
     hipStream_t s = (hipStream_t)st;
-    if (gemv_fused_supported(K)) return from_hip(launch_gemv_fused_q8(kind, pt, K, x, xq, xd, xsum, s));
-    // longer rows: quantizer launch, then the GEMV (needs the q8 buffers)
-    if (!xq) return BQ_UNSUPPORTED;
-    hipError_t e = launch_quant_q8(x, 1, K, xq, xd, xsum, nullptr, s);
-    if (e != hipSuccess) return from_hip(e);
-    return gemv_rows(kind, pt, 1, K, xq, xd, type == BQ_TYPE_Q5_K ? xsum : nullptr, s);
+    if (!gemv_fused_supported(K)) return BQ_UNSUPPORTED;
+    return from_hip(launch_gemv_fused_q8(kind, pt, K, x, xq, xd, xsum, s));
 }
 
 int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int rows,

@@ -91,27 +91,39 @@ BQ_DEV int wave_sum_i(int v) {
     return v;
 }
 
-// Per-32 q8 quantization of 4 values per lane, 8 consecutive lanes per group
-// (bruce.cu:518-539 semantics: d = amax*(1/127), id = d > 0 ? 1/d : 0,
-// q = clamp(rint(v*id), -127, 127), sum = sum q).  All 8 lanes of a group must
-// execute it together.  Returns the 4 codes packed little-endian.
-BQ_DEV uint32_t q8_quant4(const f32x4& v, float& d, int& s) {
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+// q8 quantization of one 32-value group held by a lane pair (lanes 2i, 2i+1,
+// 16 consecutive values each; both lanes of the pair must execute it).
+// Semantics of k_q8_quant (bruce.cu:518-539): d = amax*(1/127),
+// id = d > 0 ? 1/d : 0 (IEEE division), q = clamp(rint(v*id), -127, 127),
+// s = sum q.  The rounding is exact: c = clamp(v*id) is in [-127, 127] and
+// c + 1.5*2^23 lands in [2^23, 2^24) where the float spacing is 1, so the
+// addition rounds c to the nearest integer (ties to even, 1.5*2^23 being
+// even) and the low byte of the sum's bit pattern is that integer in two's
+// complement.  The codes of the lane's 16 values are returned in q[0..3]
+// (little-endian bytes, value order).
+BQ_DEV void q8_quant16(const f32x4 (&v)[4], uint32_t (&q)[4], float& d, int& s) {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    // partner lane (xor 1) via DPP quad_perm [1,0,3,2]
+    amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, amax), 0xB1, 0xF, 0xF, false)));
     d = amax * (1.f / 127.f);
     const float id = d > 0.f ? 1.f / d : 0.f;
-    const int q0 = max(-127, min(127, (int)__builtin_rintf(v.x * id)));
-    const int q1 = max(-127, min(127, (int)__builtin_rintf(v.y * id)));
-    const int q2 = max(-127, min(127, (int)__builtin_rintf(v.z * id)));
-    const int q3 = max(-127, min(127, (int)__builtin_rintf(v.w * id)));
-    s = q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    s += __shfl_xor(s, 4, 64);
-    return (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
-           ((uint32_t)(q3 & 0xFF) << 24);
+    constexpr float kMagic = 12582912.f;  // 1.5 * 2^23
+    int acc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float c0 = __builtin_amdgcn_fmed3f(v[i].x * id, -127.f, 127.f) + kMagic;
+        const float c1 = __builtin_amdgcn_fmed3f(v[i].y * id, -127.f, 127.f) + kMagic;
+        const float c2 = __builtin_amdgcn_fmed3f(v[i].z * id, -127.f, 127.f) + kMagic;
+        const float c3 = __builtin_amdgcn_fmed3f(v[i].w * id, -127.f, 127.f) + kMagic;
+        const uint32_t lo = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, c1), __builtin_bit_cast(uint32_t, c0), 0x0C0C0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, c3), __builtin_bit_cast(uint32_t, c2), 0x0C0C0400u);
+        q[i] = lo | (hi << 16);
+        acc = __builtin_amdgcn_sdot4((int)q[i], 0x01010101, acc, false);
+    }
+    s = acc + __builtin_amdgcn_mov_dpp(acc, 0xB1, 0xF, 0xF, false);
 }
 
 // 6-bit scale and min of Q5_K sub-block j from the three scale words

@@ -266,10 +266,9 @@ __host__ __device__ inline size_t act_lds_bytes(int rows, int K) {
 
 // Copy `bytes` (multiple of 16) from global to LDS with direct-to-LDS loads:
 // one 64-lane instruction moves 1 KiB into consecutive LDS.
-template <int WAVES>
-BQ_DEV void dma_to_lds(uint8_t* lds, const void* src, int bytes, int wave, int lane) {
+BQ_DEV void dma_to_lds(uint8_t* lds, const void* src, int bytes, int wave, int waves, int lane) {
     const int n = bytes >> 4;
-    for (int b = wave * 64; b < n; b += 64 * WAVES) {
+    for (int b = wave * 64; b < n; b += 64 * waves) {
         if (b + lane < n)
             __builtin_amdgcn_global_load_lds((const uint8_t*)src + 16 * (b + lane),
                                              (__attribute__((address_space(3))) void*)(lds + 16 * b), 16, 0, 0);
@@ -284,52 +283,108 @@ struct FusedQ8 {
     float* xd;
     int32_t* xsum;
 };
-constexpr int kFusedWaves = 4;
-constexpr int kFusedMaxK = 12288;  // = 4 K slices x 3 steps x 16 tasks x 64 values
-constexpr int kFusedQ = kFusedMaxK / 4 / (64 * kFusedWaves);  // float4 loads per lane
+// fused quantizer limit: 16 waves x 3 chunks of 1024 values in registers
+constexpr int kFusedMaxK = kGemvMaxK;
+constexpr int kChunk = 1024;       // values one wave quantizes at a time (16 per lane)
+
+// Fused quantizer, part 1: issue the fp32 loads of this wave's chunks (chunk c
+// of the row belongs to wave c % waves).  K % 256 == 0 keeps lane pairs whole.
+template <int QN>
+BQ_DEV void fq_load(f32x4 (&xv)[QN][4], const float* x, int K, int wave, int waves, int lane) {
+#pragma unroll
+    for (int c = 0; c < QN; ++c) {
+        const int v0 = (wave + waves * c) * kChunk + 16 * lane;
+        if (v0 < K) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xv[c][i] = *(const f32x4*)(x + v0 + 4 * i);
+        }
+    }
+}
+
+// Fused quantizer, part 2 (after the loads have returned): q8_quant16 per lane
+// pair, codes / xd / (XS) xsum into the LDS activation row, and the q8 row to
+// global memory from workgroup 0 when requested.  Ends with the LDS writes
+// complete (lgkmcnt 0); the caller's barrier publishes them.
+template <int QN, bool XS>
+BQ_DEV void fq_quantize(const f32x4 (&xv)[QN][4], uint8_t* smem, int K, int wave, int waves, int lane,
+                        const FusedQ8& fq) {
+    uint8_t* lx = smem;
+    float* lxd = (float*)(smem + K);
+    int32_t* lxs = (int32_t*)(lxd + (K >> 5));
+    const bool out = blockIdx.x == 0 && fq.xq;
+#pragma unroll
+    for (int c = 0; c < QN; ++c) {
+        const int v0 = (wave + waves * c) * kChunk + 16 * lane;
+        if (v0 < K) {
+            uint32_t q[4];
+            float d;
+            int s;
+            q8_quant16(xv[c], q, d, s);
+            const int gi = v0 >> 5;
+            *(u32x4*)(lx + v0) = u32x4{q[0], q[1], q[2], q[3]};
+            if ((lane & 1) == 0) {
+                lxd[gi] = d;
+                if constexpr (XS) lxs[gi] = s;
+            }
+            if (out) {
+                *(u32x4*)(fq.xq + v0) = u32x4{q[0], q[1], q[2], q[3]};
+                if ((lane & 1) == 0) {
+                    fq.xd[gi] = d;
+                    fq.xsum[gi] = s;
+                }
+            }
+        }
+    }
+    asm volatile("" ::: "memory");
+    BQ_WAIT_LGKM0();
+}
 
 // ---------------------------------------------------------------------------
-// The kernel: WAVES waves per workgroup, a wave owns (tile of 4 rows, K slice
-// ks of KS), SPS steps of 16 tasks per row; MR activation rows.
-// FQ: the workgroup quantizes one fp32 activation row itself (bit-exact with
-// k_quant_q8) instead of copying q8 activations: the fp32 loads are issued
-// before the weight loads, the codes go from registers into LDS.
+// The kernel: blockDim.x / 64 = KS * RT waves per workgroup, a wave owns (tile
+// of 4 rows, K slice ks of KS), SPS steps of 16 tasks per row; MR activation
+// rows.
+// QN > 0: the workgroup quantizes one fp32 activation row itself (q8_quant16,
+// bit-exact with k_quant_q8) instead of copying q8 activations.  The row is cut
+// into 1024-value chunks, chunk c belongs to wave c % waves (QN = most chunks
+// of one wave); the fp32 loads are issued before the weight loads and the
+// codes go from registers into LDS.
 // ---------------------------------------------------------------------------
-template <class F, int MR, int SPS, int WAVES, bool FQ = false>
-__global__ void __launch_bounds__(64 * WAVES)
+template <class F, int MR, int SPS, int QN, int LB>
+__global__ void __launch_bounds__(LB)
 k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* __restrict__ xd,
        const int32_t* __restrict__ xsum, FusedQ8 fq) {
-    static_assert(!FQ || (MR == 1 && WAVES == kFusedWaves), "fused quantizer: one row, 4 waves");
+    static_assert(QN == 0 || MR == 1, "fused quantizer: one activation row");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+    const int waves = blockDim.x >> 6;
     const int nb = K >> 5;
-    // ---- 1. activations -> LDS (asynchronous), or fp32 row -> registers
+    // ---- 1. activations -> LDS (asynchronous), or this wave's fp32 chunks -> registers
     ActLds act;
     act.x = (const int8_t*)smem;
     act.xd = (const float*)(smem + MR * K);
     act.xs = (const int32_t*)(act.xd + MR * nb);
-    float* part_sums = (float*)(smem + act_lds_bytes<F>(MR, K));  // [WAVES][MR][4]
-    constexpr int QN = FQ ? kFusedQ : 1;
-    f32x4 xv[QN];
-    if constexpr (FQ) {
-        // float4 f = threadIdx.x + 256*i; K % 256 == 0 makes liveness wave-uniform
-#pragma unroll
-        for (int i = 0; i < QN; ++i)
-            if (64 * (WAVES * i + wave) < (K >> 2))
-                xv[i] = *(const f32x4*)(fq.x + 4 * (threadIdx.x + 64 * WAVES * i));
+    float* part_sums = (float*)(smem + act_lds_bytes<F>(MR, K));  // [waves][MR][4]
+    constexpr int QA = QN > 0 ? QN : 1;
+    f32x4 xv[QA][4];
+    // (BQ_EXP_NOSTAGE / BQ_EXP_NOCOMPUTE: timing experiments that skip the
+    // activation staging / the dot products; results are meaningless)
+#ifndef BQ_EXP_NOSTAGE
+    if constexpr (QN > 0) {
+        fq_load<QA>(xv, fq.x, K, wave, waves, lane);
     } else {
-        dma_to_lds<WAVES>(smem, xq, MR * K, wave, lane);
-        dma_to_lds<WAVES>(smem + MR * K, xd, MR * nb * 4, wave, lane);
+        dma_to_lds(smem, xq, MR * K, wave, waves, lane);
+        dma_to_lds(smem + MR * K, xd, MR * nb * 4, wave, waves, lane);
         if constexpr (std::is_same<F, FmtQ5K>::value)
-            dma_to_lds<WAVES>(smem + MR * K + MR * nb * 4, xsum, MR * nb * 4, wave, lane);
+            dma_to_lds(smem + MR * K + MR * nb * 4, xsum, MR * nb * 4, wave, waves, lane);
     }
+#endif
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 2. this wave's weight loads, all issued now (addresses clamped so the
     //         instruction count is fixed; results of clamped lanes are unused)
-    const int RT = WAVES / KS;
+    const int RT = waves / KS;  // waves beyond RT * KS only help with the staging
     const int tile = blockIdx.x * RT + wave / KS, ks = wave % KS;
     const bool active = wave < RT * KS && tile < pt.ntiles;
     const int tl = active ? tile : 0;
@@ -349,35 +404,9 @@ k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* 
 
     // ---- 3. own DMA / fp32 loads done (only the weight loads may still be outstanding)
     BQ_WAIT_VM(F::kLoads * SPS);
-    if constexpr (FQ) {
-        uint8_t* lx = smem;
-        float* lxd = (float*)(smem + K);
-        int32_t* lxs = (int32_t*)(lxd + nb);
-        const bool out = blockIdx.x == 0 && fq.xq;
-#pragma unroll
-        for (int i = 0; i < QN; ++i) {
-            if (64 * (WAVES * i + wave) < (K >> 2)) {
-                float d;
-                int s;
-                const uint32_t pk = q8_quant4(xv[i], d, s);
-                const int f = threadIdx.x + 64 * WAVES * i, gi = f >> 3;
-                *(uint32_t*)(lx + 4 * f) = pk;
-                if ((lane & 7) == 0) {
-                    lxd[gi] = d;
-                    if constexpr (std::is_same<F, FmtQ5K>::value) lxs[gi] = s;
-                }
-                if (out) {
-                    *(uint32_t*)(fq.xq + 4 * f) = pk;
-                    if ((lane & 7) == 0) {
-                        fq.xd[gi] = d;
-                        fq.xsum[gi] = s;
-                    }
-                }
-            }
-        }
-        asm volatile("" ::: "memory");
-        BQ_WAIT_LGKM0();
-    }
+#ifndef BQ_EXP_NOSTAGE
+    if constexpr (QN > 0) fq_quantize<QA, std::is_same<F, FmtQ5K>::value>(xv, smem, K, wave, waves, lane, fq);
+#endif
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 
@@ -426,11 +455,11 @@ k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* 
 // ---------------------------------------------------------------------------
 void gemv_set_cus(int) {}
 
-static void build_tiles(PartTable& pt) {
+static void build_tiles(PartTable& pt, int rows_per_tile = kRowsPerTile) {
     int acc = 0;
     for (int p = 0; p < pt.nparts; ++p) {
         pt.tile0[p] = acc;
-        acc += (pt.N[p] + kRowsPerTile - 1) / kRowsPerTile;
+        acc += (pt.N[p] + rows_per_tile - 1) / rows_per_tile;
     }
     for (int p = pt.nparts; p < kMaxParts; ++p) pt.tile0[p] = acc;
     pt.ntiles = acc;
@@ -449,14 +478,35 @@ static void k_split(int K, int& KS, int& SPS) {
     SPS = (spt + KS - 1) / KS;
 }
 
-template <class F, int MR, int SPS, int WAVES, bool FQ = false>
+// Workgroup size: 4 waves while K needs at most 4 slices, else 16; the
+// workgroup holds RT = waves / KS row tiles and any remaining waves only share
+// the activation staging (BQ_GEMV_WAVES sets the wave count instead, 0 = exactly
+// KS * RT with RT from the default: a dev A/B switch, read once).
+static int gemv_waves(int KS) {
+    static int w = -1;
+    if (w < 0) {
+        const char* e = getenv("BQ_GEMV_WAVES");
+        w = e ? std::max(0, std::min(16, atoi(e))) : -2;
+    }
+    const int def = KS <= 4 ? 4 : 16;
+    if (w == -2) return def;
+    if (w == 0) return KS * (def / KS);
+    return std::max(w, KS);
+}
+
+template <class F, int MR, int SPS, int QN = 0>
 static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* xq, const float* xd,
                              const int32_t* xsum, hipStream_t st, FusedQ8 fq = {}) {
-    const size_t lds = act_lds_bytes<F>(MR, K) + (size_t)WAVES * MR * 4 * sizeof(float);
-    const int RT = WAVES / KS;
+    const int waves = gemv_waves(KS), RT = waves / KS;
+    const size_t lds = act_lds_bytes<F>(MR, K) + (size_t)waves * MR * 4 * sizeof(float);
     const int blocks = (pt.ntiles + RT - 1) / RT;
-    launch_kernel((k_gemv<F, MR, SPS, WAVES, FQ>), dim3(blocks), dim3(64 * WAVES), lds, st, pt, K, KS,
-                  xq, xd, xsum, fq);
+    // the launch-bounds class sets the compiler's occupancy target
+    if (waves <= 4)
+        launch_kernel((k_gemv<F, MR, SPS, QN, 256>), dim3(blocks), dim3(64 * waves), lds, st, pt, K, KS,
+                      xq, xd, xsum, fq);
+    else
+        launch_kernel((k_gemv<F, MR, SPS, QN, 1024>), dim3(blocks), dim3(64 * waves), lds, st, pt, K, KS,
+                      xq, xd, xsum, fq);
     return hipGetLastError();
 }
 
@@ -465,15 +515,12 @@ static hipError_t dispatch_mr(const PartTable& pt, int K, const int8_t* xq, cons
                               const int32_t* xsum, hipStream_t st) {
     int KS, SPS;
     k_split(K, KS, SPS);
-    if (KS <= 4) {
-        switch (SPS) {
-            case 1: return launch_fmt<F, MR, 1, 4>(pt, K, KS, xq, xd, xsum, st);
-            case 2: return launch_fmt<F, MR, 2, 4>(pt, K, KS, xq, xd, xsum, st);
-            default: return launch_fmt<F, MR, 3, 4>(pt, K, KS, xq, xd, xsum, st);
-        }
+    if (KS > 16) return hipErrorInvalidValue;  // K > 49152
+    switch (SPS) {
+        case 1: return launch_fmt<F, MR, 1>(pt, K, KS, xq, xd, xsum, st);
+        case 2: return launch_fmt<F, MR, 2>(pt, K, KS, xq, xd, xsum, st);
+        default: return launch_fmt<F, MR, 3>(pt, K, KS, xq, xd, xsum, st);
     }
-    if (KS <= 16) return launch_fmt<F, MR, 3, 16>(pt, K, KS, xq, xd, xsum, st);
-    return hipErrorInvalidValue;  // K > 49152
 }
 
 template <class F>
@@ -513,15 +560,29 @@ hipError_t launch_gemv(GemvKind kind, PartTable pt, int rows, int K, const int8_
     }
 }
 
+// fused quantizer: QN = most 1024-value chunks one wave quantizes (<= 3: the
+// K split gives KS >= chunks / 3 and waves >= KS)
+template <class F, int SPS>
+static hipError_t dispatch_fused_qn(const PartTable& pt, int K, int KS, const FusedQ8& fq, hipStream_t st) {
+    const int waves = gemv_waves(KS);
+    const int qn = (K / kChunk + waves - 1) / waves;
+    switch (qn) {
+        case 0:
+        case 1: return launch_fmt<F, 1, SPS, 1>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
+        case 2: return launch_fmt<F, 1, SPS, 2>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
+        default: return launch_fmt<F, 1, SPS, 3>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
+    }
+}
+
 template <class F>
 static hipError_t dispatch_fused(const PartTable& pt, int K, const FusedQ8& fq, hipStream_t st) {
     int KS, SPS;
     k_split(K, KS, SPS);
-    if (K > kFusedMaxK || KS > 4) return hipErrorInvalidValue;
+    if (K > kFusedMaxK || KS > 16) return hipErrorInvalidValue;
     switch (SPS) {
-        case 1: return launch_fmt<F, 1, 1, kFusedWaves, true>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
-        case 2: return launch_fmt<F, 1, 2, kFusedWaves, true>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
-        default: return launch_fmt<F, 1, 3, kFusedWaves, true>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
+        case 1: return dispatch_fused_qn<F, 1>(pt, K, KS, fq, st);
+        case 2: return dispatch_fused_qn<F, 2>(pt, K, KS, fq, st);
+        default: return dispatch_fused_qn<F, 3>(pt, K, KS, fq, st);
     }
 }
 

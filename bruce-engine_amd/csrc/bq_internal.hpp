@@ -8,6 +8,7 @@
 namespace bq {
 
 constexpr int kMaxParts = 4;
+constexpr int kGemvMaxK = 49152;  // GEMV / multi-row kernels: 16 K slices x 3 steps x 1024
 
 // Up to four matrices that share K and the activation rows, concatenated along
 // N (the reference's W0..W3 / Y0..Y3 / N0..N3 kernel arguments, bruce.cu:5815).
@@ -48,7 +49,7 @@ hipError_t launch_quant_q8(const float* x, int rows, int K, int8_t* xq, float* x
 hipError_t launch_fill_xdh(const float* xd, const int32_t* xsum, int n, uint16_t* xdh, hipStream_t st);
 
 void gemv_set_cus(int cus);
-// Fused quantize + GEMV of one fp32 activation row (K % 256 == 0, K <= 12288);
+// Fused quantize + GEMV of one fp32 activation row (K % 256 == 0, K <= 49152);
 // xq/xd/xsum receive the q8 row when xq != NULL.
 bool gemv_fused_supported(int K);
 hipError_t launch_gemv_fused_q8(GemvKind kind, PartTable pt, int K, const float* x, int8_t* xq,

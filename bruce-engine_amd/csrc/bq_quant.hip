@@ -7,10 +7,11 @@
 //
 // Layout on gfx950: x[rows][K] is contiguous and K % 32 == 0, so group g of the
 // flattened array is exactly xd[g] -- the kernel ignores row boundaries.  Each
-// lane owns 4 consecutive values (one 16-byte load), 8 lanes own a group, a
-// wave64 covers 8 groups (1 KiB of fp32 in, 256 B of int8 out, coalesced).
-// amax and sum are reduced across the 8 lanes with xor shuffles; max and
-// integer sums are order-independent, so the result is bit-exact.
+// lane owns 16 consecutive values (four 16-byte loads), a lane pair owns a
+// group, a wave64 covers 32 groups (4 KiB of fp32 in, 1 KiB of int8 out).
+// amax and sum are combined across the pair with one DPP move each; max and
+// integer sums are order-independent, so the result is bit-exact.  The same
+// q8_quant16 runs inside the fused quantize+GEMV kernel.
 #include "bq_device.hpp"
 
 namespace bq {
@@ -20,16 +21,21 @@ __global__ void __launch_bounds__(256) k_quant_q8(const float* __restrict__ x, i
                                                   int32_t* __restrict__ xsum,
                                                   uint16_t* __restrict__ xdh) {
     const int tid = blockIdx.x * 256 + threadIdx.x;
-    const int g = tid >> 3;
+    const int g = tid >> 1;
     const bool live = g < ngroups;
-    f32x4 v = {0.f, 0.f, 0.f, 0.f};
-    if (live) v = *(const f32x4*)(x + (size_t)tid * 4);
+    f32x4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (live) v[i] = *(const f32x4*)(x + (size_t)tid * 16 + 4 * i);
+    }
+    uint32_t q[4];
     float d;
     int s;
-    const uint32_t packed = q8_quant4(v, d, s);
+    q8_quant16(v, q, d, s);
     if (!live) return;
-    *(uint32_t*)(xq + (size_t)tid * 4) = packed;
-    if ((tid & 7) == 0) {
+    *(u32x4*)(xq + (size_t)tid * 16) = u32x4{q[0], q[1], q[2], q[3]};
+    if ((tid & 1) == 0) {
         xd[g] = d;
         xsum[g] = s;
         if (xdh) xdh[g] = f2h_rn(d * (float)s);
@@ -47,7 +53,7 @@ hipError_t launch_quant_q8(const float* x, int rows, int K, int8_t* xq, float* x
                            uint16_t* xdh, hipStream_t st) {
     const long long ngroups = (long long)rows * (K / 32);
     if (ngroups == 0) return hipSuccess;
-    const long long threads = ngroups * 8;
+    const long long threads = ngroups * 2;
     const int blocks = (int)((threads + 255) / 256);
     hipLaunchKernelGGL(k_quant_q8, dim3(blocks), dim3(256), 0, st, x, (int)ngroups, xq, xd, xsum, xdh);
     return hipGetLastError();

@@ -68,6 +68,7 @@ int bq_quantize_q8(const float* x, int rows, int K, int8_t* xq, float* xd, int32
 int bq_fill_xdh(const float* xd, const int32_t* xsum, int n, uint16_t* xdh, bq_stream_t st);
 
 /* ---- decode GEMV ----------------------------------------------------------
+ * The GEMV / multi-row entry points take K <= 49152 (BQ_UNSUPPORTED above). 
  * y[N] = W x for one activation row.  Replaces launch_gemv(y, w, x, st)
  * (bruce.cu:5624-5640): Q5_K raw -> k_gemv_q5k (:384-440); Q6_K with a W160
  * repack -> k_gemv_q6k_dp (:4452-4513), else raw Q6_K -> k_gemm_q6k (:4282). */
@@ -105,8 +106,8 @@ int bq_gemm_q6k_raw(float* y, const bq_weight* w, int rows, const int8_t* xq, co
  * GEMV" -- k_q8_quant (bruce.cu:518-539) followed by launch_verify_fused rows==1
  * (:7141-7229) or launch_gemv (:5624-5640) -- with one launch: every workgroup
  * quantizes x itself, bit-exactly as bq_quantize_q8.  xq/xd/xsum (all three or
- * none) receive the q8 row for later consumers.  K % 256 == 0; K > 12288 runs
- * bq_quantize_q8 then the GEMV and needs the q8 buffers (else BQ_UNSUPPORTED).
+ * none) receive the q8 row for later consumers.  K % 256 == 0 and
+ * K <= 49152 (the GEMV kernels' limit), else BQ_UNSUPPORTED.
  * An extension of this library: the reference has no single-launch form. */
 int bq_gemv_q8_fused(float* const* ys, const bq_weight* const* ws, int nparts, const float* x,
                      int8_t* xq, float* xd, int32_t* xsum, bq_stream_t st);

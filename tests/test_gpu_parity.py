@@ -219,10 +219,14 @@ def test_q6_verify_fused(bq, oracle):
 @pytest.mark.parametrize("qtype,K,Ns,rep", [
     ("q5k", 3072, [512, 1024], False),     # config-2 gate+up shape class
     ("q5k", 256, [48], False),
-    ("q5k", 12288, [64, 32, 16, 80], False),  # largest fused K, 4 parts
-    ("q5k", 12800, [32], False),           # K > 12288: quantizer launch + GEMV
+    ("q5k", 12288, [64, 32, 16, 80], False),  # 4 parts
+    ("q5k", 49152, [32], False),           # largest fused K (16 waves, 3 chunks each)
     ("q6k", 9216, [3072], False),          # config-2 down projection
     ("q6k", 1024, [130], True),
+    ("q5k", 2560, [40, 24], False),        # partial last chunk / block group
+    ("q5k", 5120, [40], False),            # 5 K slices
+    ("q6k", 20480, [64], False),           # 16-wave workgroups, 2 chunks per wave
+    ("q6k", 12288, [48], True),
 ])
 def test_gemv_q8_fused(bq, oracle, qtype, K, Ns, rep):
     """One launch quantizes x and runs the GEMV: q8 outputs bit-exact with the
@@ -255,14 +259,11 @@ def test_gemv_q8_fused(bq, oracle, qtype, K, Ns, rep):
         bq.gemv(y2, w, gq, gd, gs)
         torch.cuda.synchronize()
         assert np.array_equal(host(y2).view(np.uint32), host(y).view(np.uint32))
-    if K <= 12288:                                   # fused kernel without q8 outputs
-        ys3 = [torch.full((n,), float("nan"), device="cuda") for n in Ns]
-        assert bq.gemv_q8_fused(ys3, ws, gx) == bq.BQ_OK
-        torch.cuda.synchronize()
-        for y, y3 in zip(ys, ys3):
-            assert np.array_equal(host(y3).view(np.uint32), host(y).view(np.uint32))
-    else:
-        assert bq.gemv_q8_fused(ys, ws, gx) == bq.BQ_UNSUPPORTED
+    ys3 = [torch.full((n,), float("nan"), device="cuda") for n in Ns]   # without q8 outputs
+    assert bq.gemv_q8_fused(ys3, ws, gx) == bq.BQ_OK
+    torch.cuda.synchronize()
+    for y, y3 in zip(ys, ys3):
+        assert np.array_equal(host(y3).view(np.uint32), host(y).view(np.uint32))
 
 
 def test_gemv_q8_fused_rejects(bq):
@@ -278,6 +279,14 @@ def test_gemv_q8_fused_rejects(bq):
     assert bq.gemv_q8_fused([y, y], [w5, w6], x) == bq.BQ_UNSUPPORTED   # mixed types
     assert bq.gemv_q8_fused([y, y], [w5, w5b], x) == bq.BQ_UNSUPPORTED  # mismatched K
     assert bq.gemv_q8_fused([y] * 5, [w5] * 5, x) == bq.BQ_UNSUPPORTED  # > 4 parts
+    Kbig = 49408                                                       # above the GEMV K limit
+    rawb = torch.zeros((16, Kbig // 256 * 176), dtype=torch.uint8, device="cuda")
+    wb = bq.make_weight(rawb, bq.TYPE_Q5_K, Kbig, 16)
+    xb = torch.zeros(Kbig, device="cuda")
+    assert bq.gemv_q8_fused([y], [wb], xb) == bq.BQ_UNSUPPORTED
+    assert bq.verify_fused([y.view(1, 16)], [wb], 1, xb.to(torch.int8).view(1, -1),
+                           torch.zeros(1, Kbig // 32, device="cuda"),
+                           torch.zeros(1, Kbig // 32, dtype=torch.int32, device="cuda")) == bq.BQ_UNSUPPORTED
     xq = torch.zeros(K, dtype=torch.int8, device="cuda")
     with pytest.raises(bq.BqError):                                    # xq without xd/xsum
         bq.gemv_q8_fused([y], [w5], x, xq)
