@@ -26,6 +26,8 @@
 #include "bq_device.hpp"
 #include "bq_internal.hpp"
 
+#include <stdlib.h>
+
 namespace bq {
 
 constexpr int kTM = 128;   // tokens per tile
@@ -319,6 +321,222 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
 }
 
 // ---------------------------------------------------------------------------
+// W144 prefill GEMM (the k_gemm_mmq_q5k_144 semantics above), DMA-staged.
+//   * A stage (128 K values = 4 scale groups) is copied global -> LDS with
+//     direct-to-LDS loads (64 lanes x 16 B = 1 KB per instruction, no VGPRs):
+//     the 128 W144 rows of the tile are contiguous in global memory and land
+//     verbatim (row = 128 codes + 4 fp32 ds, 144-byte stride: conflict-free
+//     128-bit reads); token rows land 128 B apart with slot p of token t at
+//     p ^ (t & 7), so the 8 lanes of each LDS read phase hit 8 different bank
+//     groups; xd lands token-major [tok][4].
+//   * Two stage buffers (two LDS objects, the stage loop unrolled by two): the
+//     DMA of stage s+1 runs while stage s is computed, one barrier per stage.
+//   * Per group pair and 32x32 tile: two v_mfma_i32_32x32x32_i8 dots, the
+//     scale products ds[n]*xd[m] of both groups from one two-block fp32
+//     outer-product MFMA, then one convert + one FMA per output and group.
+//     (Measured on gfx950: int8 MFMAs overlap independent VALU work, fp32
+//     MFMAs do not, so the outer product costs VALU time; a one-block-per-group
+//     variant with the MFMAs of the next unit issued ahead was slower.)
+// ---------------------------------------------------------------------------
+constexpr int kXS = 128;  // token row stride in LDS (bytes)
+
+struct SmemStage {
+    uint8_t w[kTN * kW144];  // 18432 B: W144 rows verbatim
+    uint8_t x[kTM * kXS];    // 16384 B: token codes, swizzled 16-byte slots
+    float xs[kTM * 4];       //  2048 B: xd[tok][q]
+};
+
+// Direct-to-LDS 16-byte load: lane i's 16 bytes from gbase + voff land at
+// LDS address lds + 16 * i.  Issued through asm so that the compiler does not
+// treat LDS reads of the other stage buffer as dependent on it (it would wait
+// for vmcnt(0) before them); the kernel orders the copies itself (vmcnt(0) +
+// barrier before a buffer is read).  An untracked VMEM op can only make the
+// compiler's own vmcnt waits stricter, never looser.
+BQ_DEV void dma16(const void* gbase, uint32_t voff, const void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(gbase), "s"(m0)
+                 : "m0", "memory");
+}
+
+// One stage's DMA; every wave issues instructions c = wave + 4i.  Per-lane
+// offsets are loop invariant (token slot swizzle: tok & 7 == lane >> 3), the
+// rest is wave-uniform.  Token rows past `rows` are skipped (their LDS slots
+// keep stale bytes; those outputs are never stored).
+struct Mmq144Dma {
+    uint32_t w_off, x_off, xd_off;  // per lane
+    int tok_hi;                     // lane >> 3
+};
+
+BQ_DEV void mmq144_dma(SmemStage& sb, const uint8_t* wsrc, const int8_t* xq, const float* xd,
+                       const Mmq144Dma& o, int m0, int rows, int K, int nb, int s, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const int c = wave + 4 * i;
+        if (c < 18) dma16(wsrc + 1024 * c, o.w_off, sb.w + 1024 * c);
+    }
+    const int8_t* xs0 = xq + (size_t)m0 * K + 128 * s;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = wave + 4 * i;
+        if (m0 + 8 * c + o.tok_hi < rows) dma16(xs0 + (size_t)(8 * c) * K, o.x_off, sb.x + 1024 * c);
+    }
+    if (wave < 2 && m0 + 64 * wave + lane < rows)
+        dma16(xd + (size_t)(m0 + 64 * wave) * nb + 4 * s, o.xd_off, (uint8_t*)sb.xs + 1024 * wave);
+}
+
+// Operands of one group pair (2qp, 2qp+1): this lane's 16 code bytes of each
+// weight tile / token tile for both groups.
+struct Mmq144Ops {
+    i32x4 a[2][2], b[2][2];  // [nt|mt][group of the pair]
+};
+
+BQ_DEV void mmq144_ops(Mmq144Ops& o, const SmemStage& sb, int qp, int wn, int wm, int l32, int lh) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int g = 2 * qp + e;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+            o.a[nt][e] = *(const i32x4*)(sb.w + (wn * 64 + nt * 32 + l32) * kW144 + 32 * g + 16 * lh);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const int tok = wm * 64 + mt * 32 + l32;
+            o.b[mt][e] = *(const i32x4*)(sb.x + tok * kXS + 16 * ((2 * g + lh) ^ (tok & 7)));
+        }
+    }
+}
+
+// One stage.  Per group pair and tile: the scale products of both groups come
+// from one two-block fp32 outer-product MFMA (lanes 0-31 feed group 2qp,
+// lanes 32-63 group 2qp+1), the two dots from two int8 MFMAs, then one convert
+// and one FMA per output and group.  The next pair's operands are read from
+// LDS while this pair is computed.
+BQ_DEV void mmq144_stage(const SmemStage& sb, f32x16 (&acc)[2][2], int wn, int wm, int l32, int lh) {
+    f32x4 wsq[2], xsq[2];  // the stage's four scales per weight row / token: one 16-byte read each
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) wsq[nt] = *(const f32x4*)(sb.w + (wn * 64 + nt * 32 + l32) * kW144 + 128);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) xsq[mt] = *(const f32x4*)(sb.xs + 4 * (wm * 64 + mt * 32 + l32));
+    Mmq144Ops cur;
+    mmq144_ops(cur, sb, 0, wn, wm, l32, lh);
+#pragma unroll 1
+    for (int qp = 0; qp < 2; ++qp) {
+        Mmq144Ops nxt;
+        mmq144_ops(nxt, sb, 1, wn, wm, l32, lh);  // qp = 1: harmless reread
+        float wsv[2], xsv[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            wsv[t] = qp ? (lh ? wsq[t][3] : wsq[t][2]) : (lh ? wsq[t][1] : wsq[t][0]);
+            xsv[t] = qp ? (lh ? xsq[t][3] : xsq[t][2]) : (lh ? xsq[t][1] : xsq[t][0]);
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const f32x32 zf = {0.f};
+                const i32x16 zi = {0};
+                const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(wsv[nt], xsv[mt], zf, 0, 0, 0);
+                const i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[nt][0], cur.b[mt][0], zi, 0, 0, 0);
+                const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[nt][1], cur.b[mt][1], zi, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    acc[nt][mt][r] = __builtin_fmaf(sc[r], (float)d0[r], acc[nt][mt][r]);
+                    acc[nt][mt][r] = __builtin_fmaf(sc[16 + r], (float)d1[r], acc[nt][mt][r]);
+                }
+            }
+        cur = nxt;
+    }
+}
+
+__global__ void __launch_bounds__(256, 2)
+k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
+           const float* __restrict__ xd, const uint16_t* __restrict__ xdh) {
+    __shared__ __attribute__((aligned(16))) SmemStage sm0;
+    __shared__ __attribute__((aligned(16))) SmemStage sm1;
+    TileMap tm;
+    if (!map_tile(blockIdx.x, ntm, ntn, tm)) return;
+    int nbase = tm.nt * kTN;
+    const int p = part_of_ntile(pt, nbase);
+    const int Nloc = pt.N[p];
+    const uint8_t* __restrict__ W = (const uint8_t*)pt.W[p];
+    const int m0 = tm.mt * kTM;
+    const int nb = K >> 5, nst = K >> 7;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave >> 1, wm = wave & 1;
+    const int l32 = lane & 31, lh = lane >> 5;
+    auto wsrc = [&](int s) { return W + ((size_t)s * Nloc + nbase) * kW144; };
+    Mmq144Dma dof;
+    dof.tok_hi = lane >> 3;
+    dof.w_off = 16 * lane;
+    dof.x_off = (uint32_t)(lane >> 3) * (uint32_t)K + 16u * (uint32_t)((lane & 7) ^ (lane >> 3));
+    dof.xd_off = (uint32_t)lane * (uint32_t)(nb * 4);
+
+    mmq144_dma(sm0, wsrc(0), xq, xd, dof, m0, rows, K, nb, 0, wave, lane);
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+    // min term: sum_g f16(Dm[n][g]) * f16(xdh[m][g]) on fp16 MFMA, K/32 % 16 == 0
+    {
+        const uint16_t* __restrict__ Dm = (const uint16_t*)pt.aux[p];
+        for (int g0 = 0; g0 < nb; g0 += 16) {
+            f16x8 a[2], b[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int n = nbase + wn * 64 + nt * 32 + l32;
+                a[nt] = *(const f16x8*)(Dm + (size_t)n * nb + g0 + 8 * lh);
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const int m = min(m0 + wm * 64 + mt * 32 + l32, rows - 1);
+                b[mt] = *(const f16x8*)(xdh + (size_t)m * nb + g0 + 8 * lh);
+            }
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[nt], b[mt], acc[nt][mt], 0, 0, 0);
+        }
+    }
+
+    for (int s = 0; s < nst; s += 2) {
+        BQ_WAIT_VM(0);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (s + 1 < nst) mmq144_dma(sm1, wsrc(s + 1), xq, xd, dof, m0, rows, K, nb, s + 1, wave, lane);
+        mmq144_stage(sm0, acc, wn, wm, l32, lh);
+        if (s + 1 >= nst) break;
+        BQ_WAIT_VM(0);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (s + 2 < nst) mmq144_dma(sm0, wsrc(s + 2), xq, xd, dof, m0, rows, K, nb, s + 2, wave, lane);
+        mmq144_stage(sm1, acc, wn, wm, l32, lh);
+    }
+
+    float* __restrict__ Y = pt.Y[p];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int m = m0 + wm * 64 + mt * 32 + l32;
+        if (m >= rows) continue;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const int n = nbase + wn * 64 + nt * 32 + 8 * rg + 4 * lh;
+                const f32x4 v = {acc[nt][mt][4 * rg], acc[nt][mt][4 * rg + 1], acc[nt][mt][4 * rg + 2],
+                                 acc[nt][mt][4 * rg + 3]};
+                *(f32x4*)(Y + (size_t)m * Nloc + n) = v;
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Q6_K over the W160 repack: K = 16 MFMA per 16-value scale group.
 // ---------------------------------------------------------------------------
 struct SmemQ6 {
@@ -463,6 +681,15 @@ static int ntile_count(const PartTable& pt) {
     return n;
 }
 
+static int mmq_v2() {  // BQ_MMQ_V2=0 selects the register-staged W144 kernel (dev A/B switch)
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("BQ_MMQ_V2");
+        v = e ? atoi(e) : 1;
+    }
+    return v;
+}
+
 static dim3 mmq_grid(int ntm, int ntn) {
     const int ntiles = ntm * ntn;
     const int per = (ntiles + kXcds - 1) / kXcds;
@@ -473,8 +700,11 @@ hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, c
                               const uint16_t* xdh, hipStream_t st) {
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    launch_kernel((k_mmq_q5k<MmqMode::Q5W144>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
-                  rows, K, xq, xd, (const int32_t*)nullptr, xdh);
+    if (mmq_v2())
+        launch_kernel(k_mmq_w144, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xdh);
+    else
+        launch_kernel((k_mmq_q5k<MmqMode::Q5W144>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
+                      rows, K, xq, xd, (const int32_t*)nullptr, xdh);
     return hipGetLastError();
 }
 
