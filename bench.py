@@ -75,6 +75,57 @@ def cpu_baseline(gate, up, down, x, t, budget_s=12.0):
     return steps, el
 
 
+LAYERS, KO, NQKV, VOCAB = 32, 4096, 5120, 131072
+
+
+def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, warmup=3):
+    """32 x [QKV Q5_K 5120x3072, O Q5_K 3072x4096, gate/up Q5_K
+    2x(9216x3072), down Q6_K 3072x9216] + lm_head Q6_K 131072x3072 per token, every
+    layer's weights in their own device memory (2.94 GB/token, > 10x the MALL).
+    Synthetic weights: one seeded encoding per matrix shape, copied per layer; the
+    lm_head is 16 copies of a seeded 8192-row Q6_K block.  Every GEMV is one
+    bq_gemv_q8_fused launch (q8 quantization of the fp32 input inside)."""
+    w_qkv = synth.quantize_q5k(synth.gaussian(SEED + 9, (NQKV, K), 0.02))
+    w_o = synth.quantize_q5k(synth.gaussian(SEED + 10, (K, KO), 0.02))
+    w_lm = synth.quantize_q6k(synth.gaussian(SEED + 11, (VOCAB // 16, K), 0.02))
+    src = [torch.from_numpy(a).cuda() for a in (w_qkv, w_o, w_gate, w_up, w_down)]
+    shapes = [(bq.TYPE_Q5_K, K, NQKV), (bq.TYPE_Q5_K, KO, K), (bq.TYPE_Q5_K, K, FF), (bq.TYPE_Q5_K, K, FF),
+              (bq.TYPE_Q6_K, FF, K)]
+    keep, ws = [], (bq.Weight * (5 * LAYERS))()
+    for l in range(LAYERS):
+        for j, (t, k, n) in enumerate(shapes):
+            c = src[j].clone()
+            keep.append(c)
+            ws[5 * l + j] = bq.make_weight(c, t, k, n)
+    lm = torch.from_numpy(w_lm).cuda().repeat(16, 1).contiguous()
+    lmw = bq.make_weight(lm, bq.TYPE_Q6_K, K, VOCAB)
+    x = torch.from_numpy(synth.gaussian(SEED + 12, (K,))).cuda()
+    a = torch.from_numpy(synth.gaussian(SEED + 13, (KO,))).cuda()
+    t = torch.from_numpy(synth.gaussian(SEED + 14, (FF,))).cuda()
+    y0, y1 = torch.empty(VOCAB, device="cuda"), torch.empty(FF, device="cuda")
+    xq = torch.empty(FF, dtype=torch.int8, device="cuda")
+    xd = torch.empty(FF // 32, device="cuda")
+    xs = torch.empty(FF // 32, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    out = (ctypes.c_double * 4)()
+    r = B.bqb_stack(steps, warmup, LAYERS, ws, ctypes.byref(lmw), ptr(x), ptr(a), ptr(t), ptr(y0), ptr(y1),
+                    ptr(xq), ptr(xd), ptr(xs), sp, out)
+    if r != 0:
+        raise RuntimeError(f"bqb_stack failed: {r}")
+    ms = out[0] / steps
+    wbytes = LAYERS * sum(a.nbytes for a in (w_qkv, w_o, w_gate, w_up, w_down)) + lm.numel()
+    act = LAYERS * (2 * (4 * K + q8_bytes(1, K)) + (4 * KO + q8_bytes(1, KO)) + (4 * FF + q8_bytes(1, FF))) \
+        + 4 * K + q8_bytes(1, K)
+    outb = 4 * (LAYERS * (NQKV + K + 2 * FF + K) + VOCAB)
+    tot = wbytes + act + outb
+    del keep, lm
+    return {"config": "32 layers x (QKV 5120x3072, O 3072x4096, gate/up 2x9216x3072 Q5_K; down 3072x9216 "
+                      "Q6_K) + lm_head Q6_K 131072x3072, batch 1, one HIP graph per token",
+            "weight_bytes_per_token": wbytes, "bytes_per_token": tot, "ms_per_token": round(ms, 4),
+            "GBps": round(gbs(tot, ms), 1), "hbm_frac": round(gbs(tot, ms) / HBM_PEAK_GBS, 4),
+            "launches_per_token": 4 * LAYERS + 1}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,6 +155,7 @@ def main():
     B.bqb_decode_ffn.argtypes = [I, I, I, I, WP, WP, WP, P, P, P, P, P, P, P, P, P, P, P, P, P]
     B.bqb_gemm.argtypes = [I, I, WP, I, P, P, P, P, P, P, P]
     B.bqb_gemv_rows.argtypes = [I, I, I, WP, I, P, P, P, P, P, P]
+    B.bqb_stack.argtypes = [I, I, I, WP, WP, P, P, P, P, P, P, P, P, P, P]
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
     ptr = lambda t: ctypes.c_void_p(t.data_ptr())
@@ -172,7 +224,7 @@ def main():
     dn_bytes = w_down.nbytes + 4 * FF + q8_bytes(1, FF) + 4 * K
     achieved = gbs(gu_bytes, gu_ms)
 
-    gemm_obj, rows_res, c1_obj = None, None, None
+    gemm_obj, rows_res, c1_obj, stack_obj = None, None, None, None
     if not args.decode_only:
         # ---------------------------------------------------------------- prefill GEMM (config 4)
         gemm = {}
@@ -223,6 +275,9 @@ def main():
         del c1g
         c1_obj = {"us": round(c1ms * 1e3, 2), "GBps": round(gbs(c1.nbytes + q8_bytes(1, K) + 4 * K, c1ms), 1)}
 
+        # ------------------------------------------------------------ config 5: whole-stack token
+        stack_obj = whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr)
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if not (args.no_cpu or args.decode_only):
@@ -252,6 +307,7 @@ def main():
         "decode_ffn_unfused": unfused,
         "gemv_config1_3072x3072": c1_obj,
         "gemv_config3_9216x3072": rows_res,
+        "config5_whole_stack": stack_obj,
         "gemm": gemm_obj,
         "cpu_baseline": cpu,
     }

@@ -194,4 +194,57 @@ int bqb_gemv_rows(int steps, int warmup, int nsets, const bq_weight* w, int rows
     return 0;
 }
 
+// Whole-stack decode weight stream: per token, for each of
+// `nlayers` layers, QKV, O, fused gate+up and down GEMVs, then the lm_head --
+// each one a bq_gemv_q8_fused launch that quantizes its fp32 input row (the
+// q8 rows are written out, as the reference's norm kernels do).  The token's
+// launches are captured once into a HIP graph (the reference replays one graph
+// per decoded token, bruce.cu:8246-8252) and the timed region replays it
+// `steps` times.  w = [nlayers][5] weights (qkv, o, gate, up, down), inputs
+// x (K), a (KO), t (FF), outputs y (>= max N), xq/xd/xs scratch for the
+// largest K.  out[0] = timed region (ms).
+int bqb_stack(int steps, int warmup, int nlayers, const bq_weight* w, const bq_weight* lm_head, const float* x,
+              const float* a, const float* t, float* y0, float* y1, int8_t* xq, float* xd, int32_t* xs,
+              bq_stream_t st, double* out) {
+    hipStream_t cs;
+    if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) return -1;
+    auto token = [&](bq_stream_t s_) -> int {
+        for (int l = 0; l < nlayers; ++l) {
+            const bq_weight* lw = w + 5 * l;
+            float* ys[2] = {y0, y1};
+            const bq_weight* p1[1] = {&lw[0]};
+            if (int r = bq_gemv_q8_fused(ys, p1, 1, x, xq, xd, xs, s_)) return r;          // QKV
+            const bq_weight* p2[1] = {&lw[1]};
+            if (int r = bq_gemv_q8_fused(ys, p2, 1, a, xq, xd, xs, s_)) return r;          // O
+            const bq_weight* p3[2] = {&lw[2], &lw[3]};
+            if (int r = bq_gemv_q8_fused(ys, p3, 2, x, xq, xd, xs, s_)) return r;          // gate + up
+            const bq_weight* p4[1] = {&lw[4]};
+            if (int r = bq_gemv_q8_fused(ys, p4, 1, t, xq, xd, xs, s_)) return r;          // down
+        }
+        float* ys[1] = {y0};
+        const bq_weight* pl[1] = {lm_head};
+        return bq_gemv_q8_fused(ys, pl, 1, x, xq, xd, xs, s_);                             // lm_head
+    };
+    for (int i = 0; i < warmup; ++i)
+        if (int r = token(st)) return r;
+    hipGraph_t g;
+    hipGraphExec_t ex;
+    hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+    const int r = token((bq_stream_t)cs);
+    if (hipStreamEndCapture(cs, &g) != hipSuccess || r) return r ? r : -1;
+    if (hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) != hipSuccess) return -1;
+    hipGraphDestroy(g);
+    hipGraphLaunch(ex, (hipStream_t)st);
+    EventPool pool(2);
+    hipDeviceSynchronize();
+    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    for (int i = 0; i < steps; ++i) hipGraphLaunch(ex, (hipStream_t)st);
+    hipEventRecord(pool.ev[1], (hipStream_t)st);
+    hipDeviceSynchronize();
+    out[0] = elapsed(pool.ev[0], pool.ev[1]);
+    hipGraphExecDestroy(ex);
+    hipStreamDestroy(cs);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 }  // extern "C"

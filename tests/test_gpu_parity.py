@@ -266,6 +266,36 @@ def test_gemv_q8_fused(bq, oracle, qtype, K, Ns, rep):
         assert np.array_equal(host(y3).view(np.uint32), host(y).view(np.uint32))
 
 
+def test_config5_shapes(bq, oracle):
+    """BASELINE config 5 layer shapes through the fused entry: QKV Q5_K 5120x3072,
+    O Q5_K 3072x4096 (two K slices), and the Q6_K lm_head 131072x3072 built, as
+    in the benchmark, from 16 copies of one 8192-row block: rows with identical
+    bytes must give bit-identical outputs wherever they sit, and the first and
+    last 1024 rows must match the oracle."""
+    import torch
+    for qt, N, K in (("q5k", 5120, 3072), ("q5k", 3072, 4096)):
+        raw = weights(1100 + K, N, K, qt)
+        x, _ = acts(1101 + K, 1, K)
+        xq, xd, xs = oracle.q8_rows(x)
+        y = torch.full((N,), float("nan"), device="cuda")
+        assert bq.gemv_q8_fused([y], [bq.make_weight(dev(raw), bq.TYPE_Q5_K, K, N)], dev(x)) == bq.BQ_OK
+        torch.cuda.synchronize()
+        assert oracle.normwise_err(host(y)[None], oracle.gemm_q5k(raw, xq, xd, xs)) < TOL, (N, K)
+    K, blk = 3072, 8192
+    raw = weights(1200, blk, K, "q6k")
+    lm = dev(raw).repeat(16, 1).contiguous()
+    x, _ = acts(1201, 1, K)
+    xq, xd, xs = oracle.q8_rows(x)
+    y = torch.full((16 * blk,), float("nan"), device="cuda")
+    assert bq.gemv_q8_fused([y], [bq.make_weight(lm, bq.TYPE_Q6_K, K, 16 * blk)], dev(x)) == bq.BQ_OK
+    torch.cuda.synchronize()
+    yh = host(y).reshape(16, blk)
+    assert all(np.array_equal(yh[0].view(np.uint32), yh[i].view(np.uint32)) for i in range(1, 16))
+    for rows in (slice(0, 1024), slice(blk - 1024, blk)):
+        ref = oracle.gemm_q6k(np.ascontiguousarray(raw[rows]), xq, xd)
+        assert oracle.normwise_err(yh[15][rows][None], ref) < TOL
+
+
 def test_gemv_q8_fused_rejects(bq):
     import torch
     K = 512
