@@ -260,8 +260,8 @@ def main():
             "config": "prefill GEMM Q5_K 9216x3072 (W144 repack, fp16 min term), M=2048 q8 tokens, fp32 out",
             "value": g["tops"], "unit": "TOPS", "ms": g["ms"],
             "roofline": {"bound": "mfma", "achieved": g["tops"], "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                         "frac": g["frac"], "traffic": traffic_for("mmq_q5k_144_M2048"),
-                         "kernel": "k_mmq_q5k<Q5W144>", "ops_per_launch": 2 * 2048 * FF * K},
+                         "frac": g["frac"], "traffic": traffic_for("mmq_w144_M2048"),
+                         "kernel": "k_mmq_w144", "ops_per_launch": 2 * 2048 * FF * K},
             "shapes": gemm,
         }
 
