@@ -339,6 +339,23 @@ BQ_DEV void fq_quantize(const f32x4 (&xv)[QN][4], uint8_t* smem, int K, int wave
     BQ_WAIT_LGKM0();
 }
 
+#ifdef BQ_EXP_TIMING
+// timing experiment: s_memrealtime stamps per wave of the last launch
+__device__ uint64_t g_tstamp[1 << 17];
+extern "C" int bq_tstamp_copy(void* dst, size_t bytes) {
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_tstamp), bytes);
+}
+#define BQ_TS(i)                                                                       \
+    do {                                                                               \
+        const uint64_t t_ = __builtin_amdgcn_s_memrealtime();                          \
+        if (lane == 0) g_tstamp[((size_t)blockIdx.x * waves + wave) * 8 + (i)] = t_;   \
+    } while (0)
+#else
+#define BQ_TS(i) \
+    do {         \
+    } while (0)
+#endif
+
 // ---------------------------------------------------------------------------
 // The kernel: blockDim.x / 64 = KS * RT waves per workgroup, a wave owns (tile
 // of 4 rows, K slice ks of KS), SPS steps of 16 tasks per row; MR activation
@@ -359,6 +376,7 @@ k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
     const int waves = blockDim.x >> 6;
     const int nb = K >> 5;
+    BQ_TS(0);
     // ---- 1. activations -> LDS (asynchronous), or this wave's fp32 chunks -> registers
     ActLds act;
     act.x = (const int8_t*)smem;
@@ -394,21 +412,37 @@ k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* 
     const int tpr = K >> 6;
     const uint8_t* rowp = (const uint8_t*)pt.W[p] + (size_t)min(row, Nloc - 1) * RowBytes<F>::of(K);
     typename F::Task w[SPS];
+    // The fused quantizer's fp32 row comes from memory that the whole grid's
+    // weight stream is also queueing on: issued together, the row lands only
+    // after several microseconds (measured: median 3.5-4 us, p90 5-6 us, with
+    // the compute waiting for it).  So with QN > 0 every wave stages and
+    // quantizes first and issues its weight loads after the barrier: the row
+    // lands in ~1.5 us and the weight stream is overlapped with the compute.
+    // q8 staging (DMA of a row the previous kernel just wrote) stays ahead of
+    // the weight loads.
+    constexpr bool kLate = QN > 0;
+    auto issue_weights = [&]() {
 #pragma unroll
-    for (int s = 0; s < SPS; ++s) {
-        const int t = (ks * SPS + s) * kTasksPerStep + li;
-        F::load(w[s], rowp, min(t, tpr - 1));
-    }
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
+        for (int s = 0; s < SPS; ++s) {
+            const int t = (ks * SPS + s) * kTasksPerStep + li;
+            F::load(w[s], rowp, min(t, tpr - 1));
+        }
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    if constexpr (!kLate) issue_weights();
 
     // ---- 3. own DMA / fp32 loads done (only the weight loads may still be outstanding)
-    BQ_WAIT_VM(F::kLoads * SPS);
+    BQ_WAIT_VM(kLate ? 0 : F::kLoads * SPS);
+    BQ_TS(1);
 #ifndef BQ_EXP_NOSTAGE
     if constexpr (QN > 0) fq_quantize<QA, std::is_same<F, FmtQ5K>::value>(xv, smem, K, wave, waves, lane, fq);
 #endif
+    BQ_TS(2);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    BQ_TS(3);
+    if constexpr (kLate) issue_weights();
 
     // ---- 4. compute, step by step as the loads return
     float acc[MR];
@@ -423,7 +457,9 @@ k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* 
 #else
         if (rowok && t < tpr) F::template dot<MR>(w[s], rowp, t, act, K, acc);
 #endif
+        if (s == 0) BQ_TS(6);
     }
+    BQ_TS(4);
     // ---- 5. row sums; K slices combined through LDS
     float* Y = pt.Y[p];
     if (KS == 1) {
@@ -432,6 +468,7 @@ k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* 
             const float v = row16_sum(acc[m]);
             if (li == 15 && rowok) Y[(size_t)m * Nloc + row] = v;
         }
+        BQ_TS(5);
         return;
     }
 #pragma unroll
@@ -448,6 +485,7 @@ k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* 
             Y[(size_t)m * Nloc + row] = v;
         }
     }
+    BQ_TS(5);
 }
 
 // ---------------------------------------------------------------------------
@@ -480,14 +518,18 @@ static void k_split(int K, int& KS, int& SPS) {
 
 // Workgroup size: 4 waves while K needs at most 4 slices, else 16; the
 // workgroup holds RT = waves / KS row tiles and any remaining waves only share
-// the activation staging (BQ_GEMV_WAVES sets the wave count instead, 0 = exactly
-// KS * RT with RT from the default: a dev A/B switch, read once).
-static int gemv_waves(int KS) {
-    static int w = -1;
+// the activation staging.  Dev A/B switches, read once: BQ_GEMV_WAVES sets the
+// wave count (0 = exactly KS * RT with the default RT), BQ_GEMV_RT sets RT for
+// single-row launches with KS > 1.
+static int gemv_waves(int KS, int MR) {
+    static int w = -1, rt = -1;
     if (w < 0) {
         const char* e = getenv("BQ_GEMV_WAVES");
         w = e ? std::max(0, std::min(16, atoi(e))) : -2;
+        const char* r = getenv("BQ_GEMV_RT");
+        rt = r ? std::max(1, atoi(r)) : 0;
     }
+    if (rt && MR == 1 && KS > 1) return std::min(16 / KS, rt) * KS;
     const int def = KS <= 4 ? 4 : 16;
     if (w == -2) return def;
     if (w == 0) return KS * (def / KS);
@@ -497,12 +539,15 @@ static int gemv_waves(int KS) {
 template <class F, int MR, int SPS, int QN = 0>
 static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* xq, const float* xd,
                              const int32_t* xsum, hipStream_t st, FusedQ8 fq = {}) {
-    const int waves = gemv_waves(KS), RT = waves / KS;
+    const int waves = gemv_waves(KS, MR), RT = waves / KS;
     const size_t lds = act_lds_bytes<F>(MR, K) + (size_t)waves * MR * 4 * sizeof(float);
     const int blocks = (pt.ntiles + RT - 1) / RT;
     // the launch-bounds class sets the compiler's occupancy target
     if (waves <= 4)
         launch_kernel((k_gemv<F, MR, SPS, QN, 256>), dim3(blocks), dim3(64 * waves), lds, st, pt, K, KS,
+                      xq, xd, xsum, fq);
+    else if (waves <= 9 && MR == 1)
+        launch_kernel((k_gemv<F, MR, SPS, QN, 576>), dim3(blocks), dim3(64 * waves), lds, st, pt, K, KS,
                       xq, xd, xsum, fq);
     else
         launch_kernel((k_gemv<F, MR, SPS, QN, 1024>), dim3(blocks), dim3(64 * waves), lds, st, pt, K, KS,
@@ -564,7 +609,7 @@ hipError_t launch_gemv(GemvKind kind, PartTable pt, int rows, int K, const int8_
 // K split gives KS >= chunks / 3 and waves >= KS)
 template <class F, int SPS>
 static hipError_t dispatch_fused_qn(const PartTable& pt, int K, int KS, const FusedQ8& fq, hipStream_t st) {
-    const int waves = gemv_waves(KS);
+    const int waves = gemv_waves(KS, 1);
     const int qn = (K / kChunk + waves - 1) / waves;
     switch (qn) {
         case 0:
