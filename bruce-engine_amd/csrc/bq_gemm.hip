@@ -681,7 +681,9 @@ static int ntile_count(const PartTable& pt) {
     return n;
 }
 
-static int mmq_v2() {  // BQ_MMQ_V2=0 selects the register-staged W144 kernel (dev A/B switch)
+// W144 kernel choice (BQ_MMQ_V2 dev A/B switch, read once): 1 = k_mmq_w144,
+// 0 = the register-staged k_mmq_q5k<Q5W144>
+static int mmq_v2() {
     static int v = -1;
     if (v < 0) {
         const char* e = getenv("BQ_MMQ_V2");
@@ -698,7 +700,8 @@ static dim3 mmq_grid(int ntm, int ntn) {
 
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                               const uint16_t* xdh, hipStream_t st) {
-    const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
+    const int ntm = (rows + kTM - 1) / kTM;
+    const int ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
     if (mmq_v2())
         launch_kernel(k_mmq_w144, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xdh);
