@@ -421,19 +421,22 @@ k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* 
     // q8 staging (DMA of a row the previous kernel just wrote) stays ahead of
     // the weight loads.
     constexpr bool kLate = QN > 0;
-    auto issue_weights = [&]() {
+    constexpr int kEarly = kLate ? 0 : SPS;  // steps whose loads go out before the staging wait
+                                             // (issuing 1 or 2 of 3 early measured slower)
+    auto issue_weights = [&](int s0, int s1) {
 #pragma unroll
         for (int s = 0; s < SPS; ++s) {
+            if (s < s0 || s >= s1) continue;
             const int t = (ks * SPS + s) * kTasksPerStep + li;
             F::load(w[s], rowp, min(t, tpr - 1));
         }
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
     };
-    if constexpr (!kLate) issue_weights();
+    if constexpr (kEarly > 0) issue_weights(0, kEarly);
 
     // ---- 3. own DMA / fp32 loads done (only the weight loads may still be outstanding)
-    BQ_WAIT_VM(kLate ? 0 : F::kLoads * SPS);
+    BQ_WAIT_VM(F::kLoads * kEarly);
     BQ_TS(1);
 #ifndef BQ_EXP_NOSTAGE
     if constexpr (QN > 0) fq_quantize<QA, std::is_same<F, FmtQ5K>::value>(xv, smem, K, wave, waves, lane, fq);
@@ -442,7 +445,7 @@ k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* 
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     BQ_TS(3);
-    if constexpr (kLate) issue_weights();
+    if constexpr (kEarly < SPS) issue_weights(kEarly, SPS);
 
     // ---- 4. compute, step by step as the loads return
     float acc[MR];
