@@ -87,26 +87,29 @@ struct FmtQ5K {
         a.qs0 = ld16(blk + 48 + 32 * jp);
         a.qs1 = ld16(blk + 64 + 32 * jp);
     }
-    // 6-bit scale / min of sub-block j from the header words (y = scales[0..3],
-    // z = scales[4..7], w = scales[8..11]) with two 4+2-bit field extracts each:
-    // j < 4: sc = y.byte(j) & 63, m = z.byte(j) & 63; j >= 4: low nibbles of
-    // w.byte(j-4), top two bits from y.byte(j-4) / z.byte(j-4).
-    static BQ_DEV void scale_min(const u32x4& hdr, int j, uint32_t& sc, uint32_t& m) {
-        const bool lo = j < 4;
-        const uint32_t b = 8u * (uint32_t)(j & 3);
-        const uint32_t s2 = lo ? b + 4 : b + 6;
-        sc = __builtin_amdgcn_ubfe(lo ? hdr.y : hdr.w, b, 4) | (__builtin_amdgcn_ubfe(hdr.y, s2, 2) << 4);
-        m = __builtin_amdgcn_ubfe(lo ? hdr.z : hdr.w, lo ? b : b + 4, 4) | (__builtin_amdgcn_ubfe(hdr.z, s2, 2) << 4);
+    // 6-bit scales / mins of the task's sub-blocks j0 = 2jp, j1 = 2jp + 1 from
+    // the header words (y = scales[0..3], z = scales[4..7], w = scales[8..11]),
+    // packed as bytes [sc0, sc1, m0, m1]:
+    //   jp < 2:  sc = y.byte(j) & 63, m = z.byte(j) & 63
+    //   jp >= 2: sc = (w.byte(j-4) & 15) | (y.byte(j-4) >> 6) << 4,
+    //            m  = (w.byte(j-4) >> 4) | (z.byte(j-4) >> 6) << 4
+    // Bytes i0 = 2(jp & 1), i0 + 1 of y/z/w are gathered with v_perm_b32.
+    static BQ_DEV uint32_t scale_min4(const u32x4& hdr, int jp) {
+        const bool odd = jp & 1;
+        const uint32_t q = __builtin_amdgcn_perm(hdr.z, hdr.y, odd ? 0x07060302u : 0x05040100u);  // y_i0 y_i1 z_i0 z_i1
+        const uint32_t lo = q & 0x3F3F3F3Fu;
+        const uint32_t ww = __builtin_amdgcn_perm(hdr.w, hdr.w, odd ? 0x03020302u : 0x01000100u); // w_i0 w_i1 w_i0 w_i1
+        const uint32_t wn = ((ww >> 4) & 0x0F0F0000u) | (ww & 0x00000F0Fu);
+        const uint32_t hi = wn | ((q >> 2) & 0x30303030u);
+        return jp >= 2 ? hi : lo;
     }
     template <int MR>
     static BQ_DEV void dot(const Task& a, const uint8_t*, int t, const ActLds& act, int K, float (&acc)[MR]) {
         const int jp = t & 3, j0 = 2 * jp, j1 = j0 + 1;
-        uint32_t sc0, m0, sc1, m1;
-        scale_min(a.hdr, j0, sc0, m0);
-        scale_min(a.hdr, j1, sc1, m1);
+        const uint32_t sm = scale_min4(a.hdr, jp);
         const float d = h2f(a.hdr.x & 0xFFFF), dmin = h2f(a.hdr.x >> 16);
-        const float ds0 = d * (float)sc0, ds1 = d * (float)sc1;
-        const float dm0 = dmin * (float)m0, dm1 = dmin * (float)m1;
+        const float ds0 = d * (float)(sm & 0xFF), ds1 = d * (float)((sm >> 8) & 0xFF);
+        const float dm0 = dmin * (float)((sm >> 16) & 0xFF), dm1 = dmin * (float)(sm >> 24);
         uint32_t u0[8], u1[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
