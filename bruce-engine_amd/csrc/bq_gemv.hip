@@ -369,15 +369,22 @@ extern "C" int bq_tstamp_copy(void* dst, size_t bytes) {
 // of one wave); the fp32 loads are issued before the weight loads and the
 // codes go from registers into LDS.
 // ---------------------------------------------------------------------------
-template <class F, int MR, int SPS, int QN, int LB>
+// K slices of a row of K values (ceil(K/1024) steps, at most 3 per wave)
+__host__ __device__ constexpr int ks_for(int K) { return ((K + 1023) / 1024 + 2) / 3; }
+
+template <class F, int MR, int SPS, int QN, int LB, int KC = 0>
 __global__ void __launch_bounds__(LB)
-k_gemv(PartTable pt, int K, int KS, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float* __restrict__ xd,
        const int32_t* __restrict__ xsum, FusedQ8 fq) {
     static_assert(QN == 0 || MR == 1, "fused quantizer: one activation row");
+    // KC > 0: the row length (and so the K split and the 4-wave workgroup) is
+    // a compile-time constant -- the decode shapes get their own instances
+    const int K = KC ? KC : K_;
+    const int KS = KC ? ks_for(KC) : KS_;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
-    const int waves = blockDim.x >> 6;
+    const int waves = KC ? 4 : blockDim.x >> 6;
     const int nb = K >> 5;
     BQ_TS(0);
     // ---- 1. activations -> LDS (asynchronous), or this wave's fp32 chunks -> registers
@@ -548,7 +555,26 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     const int waves = gemv_waves(KS, MR), RT = waves / KS;
     const size_t lds = act_lds_bytes<F>(MR, K) + (size_t)waves * MR * 4 * sizeof(float);
     const int blocks = (pt.ntiles + RT - 1) / RT;
-    // the launch-bounds class sets the compiler's occupancy target
+    // the launch-bounds class sets the compiler's occupancy target; the
+    // single-row decode shapes run compile-time-K instances
+    if constexpr (MR == 1 && SPS == 3) {
+        if (waves == 4 && (K == 3072 || K == 9216) && KS == ks_for(K)) {
+            if (K == 3072)
+                launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072>), dim3(blocks), dim3(256), lds, st, pt, K, KS, xq,
+                              xd, xsum, fq);
+            else
+                launch_kernel((k_gemv<F, MR, SPS, QN, 256, 9216>), dim3(blocks), dim3(256), lds, st, pt, K, KS, xq,
+                              xd, xsum, fq);
+            return hipGetLastError();
+        }
+    }
+    if constexpr (MR == 1 && SPS == 2) {
+        if (waves == 4 && K == 4096 && KS == ks_for(K)) {
+            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 4096>), dim3(blocks), dim3(256), lds, st, pt, K, KS, xq, xd,
+                          xsum, fq);
+            return hipGetLastError();
+        }
+    }
     if (waves <= 4)
         launch_kernel((k_gemv<F, MR, SPS, QN, 256>), dim3(blocks), dim3(64 * waves), lds, st, pt, K, KS,
                       xq, xd, xsum, fq);
