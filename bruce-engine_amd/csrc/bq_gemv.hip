@@ -557,14 +557,17 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     const int blocks = (pt.ntiles + RT - 1) / RT;
     // the launch-bounds class sets the compiler's occupancy target; the
     // single-row decode shapes run compile-time-K instances
-    if constexpr (MR == 1 && SPS == 3) {
-        if (waves == 4 && (K == 3072 || K == 9216) && KS == ks_for(K)) {
-            if (K == 3072)
-                launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072>), dim3(blocks), dim3(256), lds, st, pt, K, KS, xq,
-                              xd, xsum, fq);
-            else
-                launch_kernel((k_gemv<F, MR, SPS, QN, 256, 9216>), dim3(blocks), dim3(256), lds, st, pt, K, KS, xq,
-                              xd, xsum, fq);
+    if constexpr (SPS == 3 && (MR == 1 || QN == 0)) {
+        if (waves == 4 && K == 3072 && KS == ks_for(K)) {
+            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072>), dim3(blocks), dim3(256), lds, st, pt, K, KS, xq, xd,
+                          xsum, fq);
+            return hipGetLastError();
+        }
+    }
+    if constexpr (SPS == 3 && MR == 1) {
+        if (waves == 4 && K == 9216 && KS == ks_for(K)) {
+            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 9216>), dim3(blocks), dim3(256), lds, st, pt, K, KS, xq, xd,
+                          xsum, fq);
             return hipGetLastError();
         }
     }
