@@ -136,6 +136,42 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
             "launches_per_token": 4 * LAYERS + 1}
 
 
+def q8s_head(B, bq, torch, sp, ptr, steps=50):
+    """Q8_0 logits head (bruce.cu:4400-4449): Q8S 131072 x K GEMV, rows 1 and 8,
+    at the BASELINE hidden size (K = 3072) and the reference model's (K = 2560).
+    Weights: device-generated N(0, 0.02) bf16, converted by bq_quantize_q8s;
+    two copies rotate so the 256 MB last-level cache cannot serve them."""
+    N = 131072
+    out = (ctypes.c_double * 4)()
+    res = {}
+    g = torch.Generator(device="cuda").manual_seed(SEED + 9)
+    for K in (3072, 2560):
+        copies = []
+        for _ in range(2):
+            wb = (torch.randn((N, K), generator=g, device="cuda") * 0.02).to(torch.bfloat16).view(torch.int16)
+            copies.append(bq.quantize_q8s(wb, K, N))
+            del wb
+        wsa = (ctypes.c_void_p * 2)(*[c.data_ptr() for c in copies])
+        x = torch.randn((8, K), generator=g, device="cuda")
+        xq, xd, _ = bq.quantize_q8(x)
+        rs = torch.rand(N, generator=g, device="cuda") + 0.5
+        y = torch.empty((8, N), device="cuda")
+        res_k = {}
+        for rows in (1, 8):
+            r = B.bqb_q8s(steps, 5, 2, wsa, K, N, rows, ptr(xq), ptr(xd), ptr(rs), ptr(y), sp, out)
+            if r != 0:
+                raise RuntimeError(f"bqb_q8s failed: {r}")
+            kms = out[1] / steps
+            nbytes = copies[0].numel() + rows * (K + K // 32 * 4) + 4 * N + 4 * rows * N
+            res_k[f"rows{rows}"] = {"us": round(kms * 1e3, 2), "GBps": round(gbs(nbytes, kms), 1),
+                                    "hbm_frac": round(gbs(nbytes, kms) / HBM_PEAK_GBS, 4)}
+        res[f"K{K}"] = dict(res_k, weight_bytes=copies[0].numel())
+        del copies, x, xq, xd, rs, y
+        torch.cuda.empty_cache()
+    return {"config": "Q8_0 logits head 131072 x K (Q8S, 272 B / 256 values) x q8 rows, fp32 out * rs",
+            "kernel": "k_gemv_q8s", **res}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,6 +202,7 @@ def main():
     B.bqb_gemm.argtypes = [I, I, WP, I, P, P, P, P, P, P, P]
     B.bqb_gemv_rows.argtypes = [I, I, I, WP, I, P, P, P, P, P, P]
     B.bqb_stack.argtypes = [I, I, I, WP, WP, P, P, P, P, P, P, P, P, P, P]
+    B.bqb_q8s.argtypes = [I, I, I, P, I, I, I, P, P, P, P, P, P]
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
     ptr = lambda t: ctypes.c_void_p(t.data_ptr())
@@ -234,7 +271,7 @@ def main():
     dn_bytes = w_down.nbytes + 4 * FF + q8_bytes(1, FF) + 4 * K
     achieved = gbs(gu_bytes, gu_ms)
 
-    gemm_obj, rows_res, c1_obj, stack_obj = None, None, None, None
+    gemm_obj, rows_res, c1_obj, stack_obj, q8s_obj = None, None, None, None, None
     if not args.decode_only:
         # ---------------------------------------------------------------- prefill GEMM (config 4)
         gemm = {}
@@ -288,6 +325,9 @@ def main():
         # ------------------------------------------------------------ config 5: whole-stack token
         stack_obj = whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr)
 
+        # ------------------------------------------------------------ Q8_0 logits head
+        q8s_obj = q8s_head(B, bq, torch, sp, ptr)
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if not (args.no_cpu or args.decode_only):
@@ -322,6 +362,7 @@ def main():
         "gemv_config1_3072x3072": c1_obj,
         "gemv_config3_9216x3072": rows_res,
         "config5_whole_stack": stack_obj,
+        "q8s_logits_head": q8s_obj,
         "gemm": gemm_obj,
         "cpu_baseline": cpu,
     }

@@ -14,6 +14,8 @@ Host-side mirror of the reference's launchers (engine/src/bruce.cu):
     repack_q5k            q5k_prepack_launch     :4832
     repack_q6k(_host)     q6k_repack_host        :4783
     quantize_q8           k_q8_quant / k_q8_rows :518, :1081
+    quantize_q8s(_host)   k_bf16_to_q8 / q8k_quant_host :5159, :4843
+    gemv_q8s              k_gemm_q8_logits       :4409 (launch_logits_b :7570)
 """
 import ctypes
 import os
@@ -24,13 +26,15 @@ LIB_PATH = os.path.join(HERE, "libbq.so")
 BQ_OK, BQ_UNSUPPORTED, BQ_EINVAL = 0, 1, 2
 TYPE_Q5_K, TYPE_Q6_K = 13, 14
 Q5K_BYTES, Q6K_BYTES = 176, 210
+Q8S_BYTES = 272  # Q8_0 logits head: 8 fp16 scales + 256 int8 per (row, 256 values)
 
 EXPORTS = [
     "bq_init", "bq_strerror", "bq_version", "bq_quantize_q8", "bq_fill_xdh", "bq_gemv",
     "bq_verify_fused", "bq_q6_verify_fused", "bq_gemm_q6k_dp", "bq_gemm_q6k_raw", "bq_try_mmq",
     "bq_gemm_q6k_mma", "bq_gemm_b", "bq_gemm_b_fused", "bq_repack_q5k", "bq_repack_q5k_bytes",
     "bq_repack_q5k_min_bytes", "bq_repack_q6k", "bq_repack_q6k_host", "bq_repack_q6k_bytes",
-    "bq_time_next_launch", "bq_gemv_q8_fused",
+    "bq_time_next_launch", "bq_gemv_q8_fused", "bq_q8s_bytes", "bq_quantize_q8s",
+    "bq_quantize_q8s_host", "bq_gemv_q8s",
 ]
 
 
@@ -84,6 +88,10 @@ def load(path=LIB_PATH):
         "bq_repack_q6k_bytes": (S, [I, I]),
         "bq_time_next_launch": (I, [P, P]),
         "bq_gemv_q8_fused": (I, [P, P, I, P, P, P, P, P]),
+        "bq_q8s_bytes": (S, [I, I]),
+        "bq_quantize_q8s": (I, [P, I, I, P, P]),
+        "bq_quantize_q8s_host": (I, [P, I, I, P]),
+        "bq_gemv_q8s": (I, [P, P, P, P, I, I, I, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -251,3 +259,32 @@ def repack_q6k_host(raw_np, K, N):
     _check(load().bq_repack_q6k_host(raw_np.ctypes.data_as(ctypes.c_void_p), K, N,
                                      out.ctypes.data_as(ctypes.c_void_p)), "bq_repack_q6k_host")
     return out
+
+
+# ---------------------------------------------------------------- Q8_0 logits head
+def quantize_q8s(w_bf16, K, N):
+    """bf16 bit patterns (int16/uint16 device tensor [N, K]) -> Q8S uint8 [N, K/256*272]."""
+    import torch
+    _need_gpu(w_bf16)
+    out = torch.empty((N, K // 256 * Q8S_BYTES), dtype=torch.uint8, device=w_bf16.device)
+    _check(load().bq_quantize_q8s(_ptr(w_bf16.contiguous()), K, N, _ptr(out), _stream()), "bq_quantize_q8s")
+    return out
+
+
+def quantize_q8s_host(w_bf16_np, K, N):
+    """Host twin on a numpy uint16 array (no device)."""
+    import numpy as np
+    w = np.ascontiguousarray(w_bf16_np, np.uint16)
+    out = np.empty((N, K // 256 * Q8S_BYTES), np.uint8)
+    _check(load().bq_quantize_q8s_host(w.ctypes.data_as(ctypes.c_void_p), K, N,
+                                       out.ctypes.data_as(ctypes.c_void_p)), "bq_quantize_q8s_host")
+    return out
+
+
+def gemv_q8s(y, w, xq, xd, K, N, rows, rs=None):
+    """y fp32 [rows, N] = Q8S w [N, K] x q8 rows (xq [rows, K], xd [rows, K/32]), times rs[N]."""
+    _need_gpu(y, w, xq, xd, rs)
+    r = load().bq_gemv_q8s(_ptr(y), _ptr(w), _ptr(xq), _ptr(xd), K, N, rows, _ptr(rs), _stream())
+    if r not in (BQ_OK, BQ_UNSUPPORTED):
+        raise BqError(r, "bq_gemv_q8s")
+    return r

@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <mutex>
 
 #include "../../include/bq.h"
@@ -39,6 +40,7 @@ int ensure_init() {
         g_dev.lds_per_block = prop.sharedMemPerBlock;
         g_dev.cus = prop.multiProcessorCount;
         gemv_set_cus(g_dev.cus);
+        q8s_set_cus(g_dev.cus);
     });
     return g_init_status;
 }
@@ -383,6 +385,87 @@ int bq_repack_q6k_host(const void* rawv, int K, int N, void* dstv) {
             }
         }
     return BQ_OK;
+}
+
+// ---- Q8_0 logits head ------------------------------------------------------
+
+size_t bq_q8s_bytes(int K, int N) { return (size_t)N * (K / 256) * 272; }
+
+int bq_quantize_q8s(const uint16_t* bf16, int K, int N, void* dst, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (K <= 0 || N < 0 || (K % 256) != 0) return BQ_EINVAL;
+    if (N == 0) return BQ_OK;
+    if (!bf16 || !dst || ((uintptr_t)bf16 & 15) || ((uintptr_t)dst & 15)) return BQ_EINVAL;
+    return from_hip(launch_quant_q8s(bf16, K, N, (uint8_t*)dst, (hipStream_t)st));
+}
+
+namespace {
+// binary32 -> binary16, round to nearest even (the reference's __float2half)
+uint16_t host_f2h_rn(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? 0x200u : 0u));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);  // rounds to >= 65520: inf
+    uint32_t mant, shift, q;
+    if (ax < 0x38800000u) {  // half denormal or zero: units of 2^-24
+        if (ax < 0x33000000u) return (uint16_t)sign;
+        mant = (ax & 0x7FFFFFu) | 0x800000u;
+        shift = 126u - (ax >> 23);
+        q = mant >> shift;
+    } else {
+        mant = ax;
+        shift = 13u;
+        q = (((ax >> 23) - 112u) << 10) | ((ax & 0x7FFFFFu) >> 13);
+    }
+    const uint32_t rem = mant & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (q & 1u))) ++q;
+    return (uint16_t)(sign | q);
+}
+}  // namespace
+
+// q8k_quant_host (bruce.cu:4843-4867): the same bytes as bq_quantize_q8s,
+// including groups with 0 < amax < 127/FLT_MAX (id = inf), where the device
+// kernels saturate to +-127.
+int bq_quantize_q8s_host(const uint16_t* bf16, int K, int N, void* dstv) {
+    if (K <= 0 || N < 0 || (K % 256) != 0) return BQ_EINVAL;
+    if (N == 0) return BQ_OK;
+    if (!bf16 || !dstv) return BQ_EINVAL;
+    uint8_t* dst = (uint8_t*)dstv;
+    const int nsb = K / 256;
+    for (int r = 0; r < N; ++r)
+        for (int s = 0; s < nsb; ++s) {
+            uint8_t* blk = dst + ((size_t)r * nsb + s) * 272;
+            for (int g = 0; g < 8; ++g) {
+                const uint16_t* p = bf16 + (size_t)r * K + (size_t)s * 256 + (size_t)g * 32;
+                float v[32], amax = 0.f;
+                for (int i = 0; i < 32; ++i) {
+                    const uint32_t bits = (uint32_t)p[i] << 16;
+                    memcpy(&v[i], &bits, 4);
+                    amax = std::max(amax, std::fabs(v[i]));
+                }
+                const float d = amax * (1.f / 127.f);
+                const float id = d > 0.f ? 1.f / d : 0.f;
+                const uint16_t h = host_f2h_rn(d);
+                memcpy(blk + 2 * g, &h, 2);
+                for (int i = 0; i < 32; ++i) {
+                    // clamp before rounding: equal to round-then-clamp for finite v*id,
+                    // and saturating like the device kernel when id overflows to inf
+                    const float t = std::min(127.f, std::max(-127.f, v[i] * id));
+                    blk[16 + 32 * g + i] = (uint8_t)(int8_t)std::lrint(t);
+                }
+            }
+        }
+    return BQ_OK;
+}
+
+int bq_gemv_q8s(float* y, const void* w, const int8_t* xq, const float* xd, int K, int N, int rows,
+                const float* rs, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (!y || !w || !xq || !xd || K <= 0 || N <= 0 || (K % 256) != 0) return BQ_EINVAL;
+    if (((uintptr_t)w & 15) || ((uintptr_t)xq & 15)) return BQ_EINVAL;
+    if (rows < 1 || rows > BQ_MAX_ROWS || K > kQ8SMaxK) return BQ_UNSUPPORTED;
+    return from_hip(launch_gemv_q8s(w, K, N, rows, xq, xd, rs, y, (hipStream_t)st));
 }
 
 }  // extern "C"

@@ -194,6 +194,28 @@ int bqb_gemv_rows(int steps, int warmup, int nsets, const bq_weight* w, int rows
     return 0;
 }
 
+// Q8_0 logits head: `steps` launches of bq_gemv_q8s, weight copy s = i % nsets.
+// out[0] = timed region (ms), out[1] = sum of the kernels' own durations (ms).
+int bqb_q8s(int steps, int warmup, int nsets, const void* const* ws, int K, int N, int rows, const int8_t* xq,
+            const float* xd, const float* rs, float* y, bq_stream_t st, double* out) {
+    for (int i = 0; i < warmup; ++i)
+        if (int r = bq_gemv_q8s(y, ws[i % nsets], xq, xd, K, N, rows, rs, st)) return r;
+    EventPool pool((size_t)steps * 2 + 2);
+    hipDeviceSynchronize();
+    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    for (int i = 0; i < steps; ++i) {
+        bq_time_next_launch(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
+        if (int r = bq_gemv_q8s(y, ws[i % nsets], xq, xd, K, N, rows, rs, st)) return r;
+    }
+    hipEventRecord(pool.ev[1], (hipStream_t)st);
+    hipDeviceSynchronize();
+    out[0] = elapsed(pool.ev[0], pool.ev[1]);
+    double k = 0;
+    for (int i = 0; i < steps; ++i) k += elapsed(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
+    out[1] = k;
+    return 0;
+}
+
 // Whole-stack decode weight stream: per token, for each of
 // `nlayers` layers, QKV, O, fused gate+up and down GEMVs, then the lm_head --
 // each one a bq_gemv_q8_fused launch that quantizes its fp32 input row (the

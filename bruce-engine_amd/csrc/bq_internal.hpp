@@ -69,4 +69,11 @@ hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, c
 hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                           hipStream_t st);
 
+// Q8_0 logits head (Q8S: 8 fp16 scales + 256 int8 per row and 256 values)
+constexpr int kQ8SMaxK = 4096;  // the GEMV keeps K/1024 activation chunks per lane in registers
+hipError_t launch_quant_q8s(const uint16_t* src, int K, int N, uint8_t* dst, hipStream_t st);
+void q8s_set_cus(int cus);
+hipError_t launch_gemv_q8s(const void* W, int K, int N, int rows, const int8_t* xq, const float* xd,
+                           const float* rs, float* y, hipStream_t st);
+
 }  // namespace bq

@@ -153,6 +153,30 @@ int bq_repack_q6k(const void* raw, int K, int N, void* w160, bq_stream_t st);
 int bq_repack_q6k_host(const void* raw, int K, int N, void* w160);
 size_t bq_repack_q6k_bytes(int K, int N);     /* N*(K/128)*160 */
 
+/* ---- Q8_0 logits head ------------------------------------------------------
+ * Q8S layout (bruce.cu:4400-4407): per (row, 256 values) 272 B = 8 fp16 group
+ * scales | 256 int8 codes; row-major [N][K/256][272].  K % 256 == 0.
+ * The BF16 output matrix is converted once at load and the decode / prompt
+ * logits read it with the q8 activations the last norm already produced. */
+size_t bq_q8s_bytes(int K, int N);            /* N*(K/256)*272 */
+/* BF16 [N][K] (bit patterns) -> Q8S on the device.  Replaces k_bf16_to_q8
+ * (bruce.cu:5159-5184).  Per 32 values d = amax*(1/127), id = d>0 ? 1/d : 0,
+ * q = clamp(rint(v*id), -127, 127), scale = half_rn(d).  Bit-exact with the
+ * reference for finite inputs (a group with 0 < amax < 127/FLT_MAX has
+ * id = inf and saturates to +-127, as __float2int_rn does; the reference's host
+ * loop leaves that case to lrintf(inf)).  bf16 and dst 16-byte aligned. */
+int bq_quantize_q8s(const uint16_t* bf16, int K, int N, void* dst, bq_stream_t st);
+/* Host version: q8k_quant_host (bruce.cu:4843-4867), same bytes. */
+int bq_quantize_q8s_host(const uint16_t* bf16, int K, int N, void* dst);
+/* y[m][n] = rs[n] * sum_g ws[n][g]*xd[m][g]*dot(codes[n][g], xq[m][g]) for
+ * m < rows (1..8); rs NULL means 1.  Replaces k_gemm_q8_logits<M,8>
+ * (bruce.cu:4409-4449) as launched by launch_logits_b (:7570-7590) and the
+ * decode / last-row calls (:8028-8032, :7831-7836).  xq [rows][K] and xd
+ * [rows][K/32] as from bq_quantize_q8 (xsum is not used); w and xq 16-byte
+ * aligned.  K <= 4096, else BQ_UNSUPPORTED. */
+int bq_gemv_q8s(float* y, const void* w, const int8_t* xq, const float* xd, int K, int N, int rows,
+                const float* rs, bq_stream_t st);
+
 /* ---- tooling ---------------------------------------------------------------
  * No counterpart in the reference (its harnesses bracket launches with
  * cudaEventRecord, tools/gemvbench.cu:360-371).  Times the calling thread's

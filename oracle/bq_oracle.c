@@ -464,3 +464,66 @@ void orc_repack_q6k_160(const uint8_t* raw, int K, int N, uint8_t* dst) {
             }
         }
 }
+
+/* ------------------------------------------------------------------------- */
+/* Q8_0 logits head                                                           */
+/* ------------------------------------------------------------------------- */
+static float bf16_to_f32(uint16_t b) {
+    const uint32_t x = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+/* bruce.cu:4843-4867 (q8k_quant_host) and :5162-5184 (k_bf16_to_q8, its device
+ * twin and the load path in use): per 32 values d = amax*(1/127),
+ * id = d>0 ? 1/d : 0, q = clamp(rint(v*id), -127, 127); the scale is stored as
+ * half_rn(d). */
+void orc_quantize_q8s(const uint16_t* bf16, int K, int N, uint8_t* dst) {
+    const int nsb = K / 256;
+    for (int r = 0; r < N; ++r)
+        for (int s = 0; s < nsb; ++s) {
+            uint8_t* blk = dst + ((size_t)r * nsb + s) * 272;
+            for (int g = 0; g < 8; ++g) {
+                const uint16_t* p = bf16 + (size_t)r * K + (size_t)s * 256 + (size_t)g * 32;
+                float amax = 0.f;
+                for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(bf16_to_f32(p[i])));
+                const float d = amax * (1.f / 127.f);
+                const float id = d > 0.f ? 1.f / d : 0.f;
+                const uint16_t h = orc_f2h_rn(d);
+                memcpy(blk + 2 * g, &h, 2);
+                for (int i = 0; i < 32; ++i) {
+                    /* clamp, then round: the same as the reference's round-then-clamp
+                     * for every finite v*id; when 0 < amax < 127/FLT_MAX, id = inf and
+                     * the device kernel's __float2int_rn saturates (+-127) where the
+                     * host loop's lrintf(inf) is undefined -- the device result is kept. */
+                    float t = bf16_to_f32(p[i]) * id;
+                    t = t < -127.f ? -127.f : (t > 127.f ? 127.f : t);
+                    blk[16 + 32 * g + i] = (uint8_t)(int8_t)lrintf(t);
+                }
+            }
+        }
+}
+
+/* bruce.cu:4409-4449: acc += ws * xd * dot per 32-value group, then * rs[row]. */
+void orc_gemv_q8s(const uint8_t* w, int K, int N, int M, const int8_t* xq, const float* xd,
+                  const float* rs, double* y) {
+    const int nsb = K / 256, nb = K / 32;
+    for (int m = 0; m < M; ++m)
+        for (int n = 0; n < N; ++n) {
+            double acc = 0.0;
+            for (int s = 0; s < nsb; ++s) {
+                const uint8_t* blk = w + ((size_t)n * nsb + s) * 272;
+                for (int g = 0; g < 8; ++g) {
+                    uint16_t h;
+                    memcpy(&h, blk + 2 * g, 2);
+                    int32_t dot = 0;
+                    for (int i = 0; i < 32; ++i)
+                        dot += (int32_t)(int8_t)blk[16 + 32 * g + i] *
+                               (int32_t)xq[(size_t)m * K + (size_t)s * 256 + 32 * g + i];
+                    acc += (double)orc_h2f(h) * (double)xd[(size_t)m * nb + s * 8 + g] * (double)dot;
+                }
+            }
+            y[(size_t)m * N + n] = rs ? acc * (double)rs[n] : acc;
+        }
+}

@@ -17,6 +17,11 @@
  *                          the mmq_test.cu "y = K" KAT, linearity in xd, dmin = 0 case
  *   orc_repack_*           index-map restatement checked against dequant round trip
  *   orc_gemm_q5k_144       equals orc_gemm_q5k up to the fp16 rounding of the min term
+ *   orc_quantize_q8s       codes and scales equal orc_q8_rows on the widened bf16 values
+ *                          (scale = half_rn(xd)); hand-built layout KAT with numpy
+ *                          float32/float16 arithmetic; round-trip bound |w - s*q| <= s/2
+ *   orc_gemv_q8s           float64 matmul of the dequantized operands (numpy, built from
+ *                          a reshape of the block layout); "y = K" KAT; exact scaling in rs
  * None of the functions is "parity unpinned".
  */
 #ifndef BQ_ORACLE_H
@@ -84,6 +89,15 @@ void orc_gemm_q5k_144(const uint8_t* w144, const uint16_t* dm, const int8_t* xq,
 void orc_repack_q5k_144(const uint8_t* raw, int K, int N, uint8_t* w144, uint16_t* dm);
 /* Q6_K -> [N][K/128][160]  (bruce.cu:4783-4811) */
 void orc_repack_q6k_160(const uint8_t* raw, int K, int N, uint8_t* dst);
+
+/* ---- Q8_0 logits head (bruce.cu:4400-4449, 4841-4867, 5159-5184) ---------- */
+/* BF16 [N][K] -> Q8S: per (row, 256 values) 8 fp16 group scales (16 B) then
+ * 256 int8 codes (256 B) = 272 B.  q8k_quant_host, bruce.cu:4843-4867. */
+void orc_quantize_q8s(const uint16_t* bf16, int K, int N, uint8_t* dst);
+/* y[m*N+n] = rs[n] * sum_g ws[n][g] * xd[m][g] * dot_g, in double (rs NULL = 1);
+ * k_gemm_q8_logits, bruce.cu:4409-4449. */
+void orc_gemv_q8s(const uint8_t* w, int K, int N, int M, const int8_t* xq, const float* xd,
+                  const float* rs, double* y);
 
 #ifdef __cplusplus
 }

@@ -56,6 +56,8 @@ def lib():
             "orc_gemm_q5k_144": (None, [P, P, P, P, P, I, I, I, P]),
             "orc_repack_q5k_144": (None, [P, I, I, P, P]),
             "orc_repack_q6k_160": (None, [P, I, I, P]),
+            "orc_quantize_q8s": (None, [P, I, I, P]),
+            "orc_gemv_q8s": (None, [P, I, I, I, P, P, P, P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -193,6 +195,41 @@ def repack_q6k_160(raw, K):
     out = np.empty((N, K // 128, 160), np.uint8)
     lib().orc_repack_q6k_160(_p(raw), K, N, _p(out))
     return out
+
+
+Q8S_BYTES = 272  # Q8_0 logits head: 8 fp16 scales + 256 int8 per (row, 256 values)
+
+
+def quantize_q8s(w_bf16):
+    """bf16 bit patterns uint16 [N, K] -> Q8S uint8 [N, K/256*272]."""
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    N, K = w.shape
+    out = np.empty((N, K // QK * Q8S_BYTES), np.uint8)
+    lib().orc_quantize_q8s(_p(w), K, N, _p(out))
+    return out
+
+
+def gemv_q8s(w, K, xq, xd, rs=None):
+    """Q8S [N, K/256*272] x q8 rows -> float64 [M, N]."""
+    N = w.shape[0]
+    xq = np.ascontiguousarray(xq, np.int8).reshape(-1, K)
+    M = xq.shape[0]
+    xd = np.ascontiguousarray(xd, np.float32)
+    y = np.empty((M, N), np.float64)
+    rsa = None if rs is None else np.ascontiguousarray(rs, np.float32)
+    lib().orc_gemv_q8s(_p(w), K, N, M, _p(xq), _p(xd), None if rsa is None else _p(rsa), _p(y))
+    return y
+
+
+def f32_to_bf16(x):
+    """fp32 -> bf16 bit patterns, round to nearest even (finite inputs)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return r.astype(np.uint16)
+
+
+def bf16_to_f32(b):
+    return (np.ascontiguousarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
 def q5k_scale(scales12, js):

@@ -62,3 +62,25 @@ def test_host_repack_rejects_bad_shape():
     buf = (ctypes.c_uint8 * 1024)()
     assert L.bq_repack_q6k_host(buf, 100, 1, buf) == bq.BQ_EINVAL
     assert L.bq_repack_q6k_host(None, 256, 1, buf) == bq.BQ_EINVAL
+
+
+def test_quantize_q8s_host_matches_oracle(oracle):
+    """bq_quantize_q8s_host (q8k_quant_host, bruce.cu:4843-4867) on the CPU."""
+    import bq
+    for N, K in [(3, 256), (11, 2560)]:
+        w = oracle.f32_to_bf16(oracle.gaussian(500 + N, N * K, 0.0, 0.02).reshape(N, K))
+        w[0, :32] = 0
+        w[0, 32:64] = oracle.f32_to_bf16(np.full(32, 1e-38, np.float32))   # tiny (denormal half scale)
+        w[1, 64:96] = oracle.f32_to_bf16(np.linspace(-3e4, 3e4, 32).astype(np.float32))
+        got = bq.quantize_q8s_host(w, K, N)
+        assert np.array_equal(got, oracle.quantize_q8s(w))
+
+
+def test_q8s_sizes_and_rejects():
+    import bq
+    L = bq.load()
+    assert L.bq_q8s_bytes(2560, 131072) == 356515840      # the reference's 356.5 MB logits head
+    assert L.bq_q8s_bytes(3072, 131072) == 427819008
+    buf = (ctypes.c_uint8 * 1024)()
+    assert L.bq_quantize_q8s_host(buf, 100, 1, buf) == bq.BQ_EINVAL
+    assert L.bq_quantize_q8s_host(None, 256, 1, buf) == bq.BQ_EINVAL
