@@ -58,6 +58,13 @@ __global__ void __launch_bounds__(256) k_quant_q8s(const uint16_t* __restrict__ 
     if ((tid & 1) == 0) *(uint16_t*)(blk + 2 * ((kin & 255) >> 5)) = f2h_rn(d);
 }
 
+// Buffer resource over one row (gfx9 raw buffer: base, stride 0, byte count,
+// word 3 = 0x00020000).  A wave-uniform base keeps the descriptor in SGPRs and
+// every load is then base + 32-bit lane offset.
+BQ_DEV __amdgpu_buffer_rsrc_t row_rsrc(const uint8_t* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)bytes, 0x00020000);
+}
+
 template <int M, int R, int CPL>
 __global__ void __launch_bounds__(256)
 k_gemv_q8s(const uint8_t* __restrict__ W, int K, int N, const int8_t* __restrict__ xq,
@@ -67,13 +74,15 @@ k_gemv_q8s(const uint8_t* __restrict__ W, int K, int N, const int8_t* __restrict
     const size_t rowb = (size_t)(K >> 8) * kQ8S;
     u32x4 xv[M][CPL];
     float xs[M][CPL];
+    // lanes past the row's last chunk (K % 1024 != 0) read chunk 0 of the row
+    // (a valid address) and contribute zero: their xq and xd are zero
     uint32_t woff[CPL], soff[CPL];
-    bool ok[CPL];
+    bool ok[CPL];  // chunk c of this lane exists
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const int cc = c * 64 + lane;
         ok[c] = cc < nchunk;
-        const int sb = cc >> 4, p = cc & 15;
+        const int sb = ok[c] ? cc >> 4 : 0, p = ok[c] ? cc & 15 : 0;
         woff[c] = sb * kQ8S + 16 + p * 16;
         soff[c] = sb * kQ8S + 2 * (p >> 1);
 #pragma unroll
@@ -82,22 +91,23 @@ k_gemv_q8s(const uint8_t* __restrict__ W, int K, int N, const int8_t* __restrict
             xs[m][c] = ok[c] ? xd[(size_t)m * nb + (cc >> 1)] : 0.f;
         }
     }
-    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6), tw = gridDim.x * 4;
+    // the wave index is uniform (readfirstlane), so row bases are scalar
+    const int gw = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), tw = gridDim.x * 4;
     for (int r0 = gw * R; r0 < N; r0 += tw * R) {
         u32x4 wv[R][CPL];
         uint32_t sv[R][CPL];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const bool rv = r0 + r < N;
-            const uint8_t* wr = W + (size_t)(r0 + r) * rowb;
+            // a row past N keeps row N-1 as its base and an empty record range:
+            // its loads return zero (results are not stored).  No branches, so
+            // all R*CPL loads are in flight together.
+            const int row = r0 + r;
+            const __amdgpu_buffer_rsrc_t rs_ = row_rsrc(W + (size_t)min(row, N - 1) * rowb,
+                                                        row < N ? (uint32_t)rowb : 0u);
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
-                wv[r][c] = u32x4{0u, 0u, 0u, 0u};
-                sv[r][c] = 0u;
-                if (rv && ok[c]) {
-                    wv[r][c] = ld16_stream(wr + woff[c]);
-                    sv[r][c] = *(const uint16_t*)(wr + soff[c]);
-                }
+                wv[r][c] = __builtin_amdgcn_raw_buffer_load_b128(rs_, woff[c], 0, 0);
+                sv[r][c] = __builtin_amdgcn_raw_buffer_load_b16(rs_, soff[c], 0, 0);
             }
         }
 #pragma unroll
@@ -107,6 +117,8 @@ k_gemv_q8s(const uint8_t* __restrict__ W, int K, int N, const int8_t* __restrict
             for (int m = 0; m < M; ++m) acc[m] = 0.f;
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
+                // lanes past the last chunk read the row's group-0 scale (or 0
+                // past N) and have xq = xd = 0, so they add exactly zero
                 const float ws = h2f(sv[r][c]);
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
@@ -144,8 +156,17 @@ hipError_t launch_q8s_mc(const uint8_t* W, int K, int N, const int8_t* xq, const
     // rows per wave iteration: enough 16-byte loads in flight per wave while
     // the activation registers (M*CPL*5 VGPRs) grow with M
     constexpr int R = M <= 2 ? 4 : (M <= 4 ? 2 : 1);
+    // persistent grid: as many workgroups as are resident at once, so no
+    // partial second round of workgroups trails the stream
+    static int per_cu = 0;
+    if (per_cu == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv_q8s<M, R, CPL>, 256, 0) != hipSuccess || n < 1)
+            n = 2;
+        per_cu = n;
+    }
     const long long want = ((long long)N + 4 * R - 1) / (4 * R);
-    const int blocks = (int)std::min<long long>(want, (long long)g_cus * 8);
+    const int blocks = (int)std::min<long long>(want, (long long)g_cus * per_cu);
     launch_kernel((k_gemv_q8s<M, R, CPL>), dim3(blocks), dim3(256), 0, st, W, K, N, xq, xd, rs, y);
     return hipGetLastError();
 }
