@@ -172,6 +172,43 @@ def q8s_head(B, bq, torch, sp, ptr, steps=50):
             "kernel": "k_gemv_q8s", **res}
 
 
+def q8_producers(B, torch, sp, ptr, steps=100):
+    """The norm kernels that emit q8 activations (bruce.cu:541-641): each op at
+    its decode shape (1 row: launch/latency-bound) and as a 2048-row prompt
+    batch (HBM-bound: bytes = inputs + fp32 out + q8 out)."""
+    out_t = (ctypes.c_double * 4)()
+    # op id, name, n, fp32 row arrays read, per-column vectors read, fp32 out written
+    ops = [(0, "norm", 3072, 1, 0, 1), (1, "add_norm", 3072, 2, 0, 1), (2, "resid", 3072, 2, 1, 1),
+           (3, "gate_norm", 4096, 2, 1, 1), (4, "silu_mul_norm", 9216, 2, 2, 0)]
+    g = torch.Generator(device="cuda").manual_seed(SEED + 10)
+    res = {}
+    for op, name, n, nin, nvec, nout in ops:
+        r_ = {}
+        for rows in (1, 2048):
+            bufs = [torch.randn((rows, n), generator=g, device="cuda") for _ in range(nin)]
+            vecs = [torch.rand(n, generator=g, device="cuda") + 0.5 for _ in range(nvec)]
+            outb = torch.empty((rows, n), device="cuda") if op in (0, 3) else None
+            xq = torch.empty((rows, n), dtype=torch.int8, device="cuda")
+            xd = torch.empty((rows, n // 32), device="cuda")
+            xs = torch.empty((rows, n // 32), dtype=torch.int32, device="cuda")
+            ab = bufs + vecs
+            a = ab[0]
+            b = ab[1] if len(ab) > 1 else None
+            c = ab[2] if len(ab) > 2 else None
+            d = ab[3] if len(ab) > 3 else None
+            rc = B.bqb_norm(op, steps, 10, None if outb is None else ptr(outb), ptr(a),
+                            None if b is None else ptr(b), None if c is None else ptr(c),
+                            None if d is None else ptr(d), rows, n, ptr(xq), ptr(xd), ptr(xs), sp, out_t)
+            if rc != 0:
+                raise RuntimeError(f"bqb_norm({name}) failed: {rc}")
+            kms = out_t[1] / steps
+            nbytes = rows * n * 4 * (nin + nout) + nvec * n * 4 + rows * (n + n // 32 * 8)
+            r_[f"rows{rows}"] = {"us": round(kms * 1e3, 2), "GBps": round(gbs(nbytes, kms), 1)}
+            del bufs, vecs, outb, xq, xd, xs
+        res[f"{name}_n{n}"] = r_
+    return {"kernel": "k_norm_q8<op>", **res}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -203,6 +240,7 @@ def main():
     B.bqb_gemv_rows.argtypes = [I, I, I, WP, I, P, P, P, P, P, P]
     B.bqb_stack.argtypes = [I, I, I, WP, WP, P, P, P, P, P, P, P, P, P, P]
     B.bqb_q8s.argtypes = [I, I, I, P, I, I, I, P, P, P, P, P, P]
+    B.bqb_norm.argtypes = [I, I, I, P, P, P, P, P, I, I, P, P, P, P, P]
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
     ptr = lambda t: ctypes.c_void_p(t.data_ptr())
@@ -271,7 +309,7 @@ def main():
     dn_bytes = w_down.nbytes + 4 * FF + q8_bytes(1, FF) + 4 * K
     achieved = gbs(gu_bytes, gu_ms)
 
-    gemm_obj, rows_res, c1_obj, stack_obj, q8s_obj = None, None, None, None, None
+    gemm_obj, rows_res, c1_obj, stack_obj, q8s_obj, norm_obj = None, None, None, None, None, None
     if not args.decode_only:
         # ---------------------------------------------------------------- prefill GEMM (config 4)
         gemm = {}
@@ -328,6 +366,9 @@ def main():
         # ------------------------------------------------------------ Q8_0 logits head
         q8s_obj = q8s_head(B, bq, torch, sp, ptr)
 
+        # ------------------------------------------------------------ q8 producers (norm + quantize)
+        norm_obj = q8_producers(B, torch, sp, ptr)
+
     # ---------------------------------------------------------------- CPU baseline
     cpu = None
     if not (args.no_cpu or args.decode_only):
@@ -363,6 +404,7 @@ def main():
         "gemv_config3_9216x3072": rows_res,
         "config5_whole_stack": stack_obj,
         "q8s_logits_head": q8s_obj,
+        "q8_producers": norm_obj,
         "gemm": gemm_obj,
         "cpu_baseline": cpu,
     }

@@ -16,6 +16,9 @@ Host-side mirror of the reference's launchers (engine/src/bruce.cu):
     quantize_q8           k_q8_quant / k_q8_rows :518, :1081
     quantize_q8s(_host)   k_bf16_to_q8 / q8k_quant_host :5159, :4843
     gemv_q8s              k_gemm_q8_logits       :4409 (launch_logits_b :7570)
+    norm_q8 / add_norm_q8 / resid_q8 / gate_norm_q8 / silu_mul_norm_q8
+                          k_norm :541, k_add_norm :556, k_resid :571, k_gate_norm :602,
+                          k_silu_mul_norm :622 (and their _rows / _vec4 forms)
 """
 import ctypes
 import os
@@ -34,7 +37,8 @@ EXPORTS = [
     "bq_gemm_q6k_mma", "bq_gemm_b", "bq_gemm_b_fused", "bq_repack_q5k", "bq_repack_q5k_bytes",
     "bq_repack_q5k_min_bytes", "bq_repack_q6k", "bq_repack_q6k_host", "bq_repack_q6k_bytes",
     "bq_time_next_launch", "bq_gemv_q8_fused", "bq_q8s_bytes", "bq_quantize_q8s",
-    "bq_quantize_q8s_host", "bq_gemv_q8s",
+    "bq_quantize_q8s_host", "bq_gemv_q8s", "bq_norm_q8", "bq_add_norm_q8", "bq_resid_q8",
+    "bq_gate_norm_q8", "bq_silu_mul_norm_q8",
 ]
 
 
@@ -92,6 +96,11 @@ def load(path=LIB_PATH):
         "bq_quantize_q8s": (I, [P, I, I, P, P]),
         "bq_quantize_q8s_host": (I, [P, I, I, P]),
         "bq_gemv_q8s": (I, [P, P, P, P, I, I, I, P, P]),
+        "bq_norm_q8": (I, [P, P, I, I, P, P, P, P]),
+        "bq_add_norm_q8": (I, [P, P, I, I, P, P, P, P]),
+        "bq_resid_q8": (I, [P, P, P, I, I, P, P, P, P]),
+        "bq_gate_norm_q8": (I, [P, P, P, P, I, I, P, P, P, P]),
+        "bq_silu_mul_norm_q8": (I, [P, P, P, P, P, I, I, P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -288,3 +297,40 @@ def gemv_q8s(y, w, xq, xd, K, N, rows, rs=None):
     if r not in (BQ_OK, BQ_UNSUPPORTED):
         raise BqError(r, "bq_gemv_q8s")
     return r
+
+
+# ---------------------------------------------------------------- q8 producers
+def _q8_out(rows, n, device):
+    import torch
+    return (torch.empty((rows, n), dtype=torch.int8, device=device),
+            torch.empty((rows, n // 32), dtype=torch.float32, device=device),
+            torch.empty((rows, n // 32), dtype=torch.int32, device=device))
+
+
+def norm_q8(op, rows, n, out=None, a=None, b=None, c=None, d=None, q8=None):
+    """op in {"norm", "add", "resid", "gate", "silu"}; returns (out, (xq, xd, xsum)).
+    norm: out = norm(a); add: a = norm(a + b) in place; resid: a = norm(norm(a) +
+    (norm(b) - norm(a))*c) in place; gate: out = norm(a / (1 + exp(-b*c)));
+    silu: out = norm(silu(a*c) * b * d)."""
+    _need_gpu(out, a, b, c, d)
+    if q8 is None:
+        q8 = _q8_out(rows, n, a.device)
+    xq, xd, xs = q8
+    L = load()
+    S = _stream()
+    if op == "norm":
+        r = L.bq_norm_q8(_ptr(out), _ptr(a), rows, n, _ptr(xq), _ptr(xd), _ptr(xs), S)
+    elif op == "add":
+        r = L.bq_add_norm_q8(_ptr(a), _ptr(b), rows, n, _ptr(xq), _ptr(xd), _ptr(xs), S)
+    elif op == "resid":
+        r = L.bq_resid_q8(_ptr(a), _ptr(b), _ptr(c), rows, n, _ptr(xq), _ptr(xd), _ptr(xs), S)
+    elif op == "gate":
+        r = L.bq_gate_norm_q8(_ptr(out), _ptr(a), _ptr(b), _ptr(c), rows, n, _ptr(xq), _ptr(xd), _ptr(xs), S)
+    elif op == "silu":
+        r = L.bq_silu_mul_norm_q8(_ptr(out), _ptr(a), _ptr(b), _ptr(c), _ptr(d), rows, n, _ptr(xq), _ptr(xd),
+                                  _ptr(xs), S)
+    else:
+        raise ValueError(op)
+    if r not in (BQ_OK, BQ_UNSUPPORTED):
+        raise BqError(r, f"norm_q8({op})")
+    return r, q8

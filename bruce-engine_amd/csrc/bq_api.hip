@@ -387,6 +387,52 @@ int bq_repack_q6k_host(const void* rawv, int K, int N, void* dstv) {
     return BQ_OK;
 }
 
+// ---- q8 producers (norm + quantize) -----------------------------------------
+
+namespace {
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+int norm_q8(int op, float* out, const float* a, const float* b, const float* c, const float* d, int rows,
+            int n, int8_t* xq, float* xd, int32_t* xsum, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (rows < 0 || n <= 0 || (n % 32) != 0) return BQ_EINVAL;
+    if (rows == 0) return BQ_OK;
+    if (!a || !xq || !xd || !xsum) return BQ_EINVAL;
+    if (!al16(out) || !al16(a) || !al16(b) || !al16(c) || !al16(d) || !al16(xq)) return BQ_EINVAL;
+    if (n > kNormMaxN) return BQ_UNSUPPORTED;
+    return from_hip(launch_norm_q8(op, out, a, b, c, d, rows, n, xq, xd, xsum, (hipStream_t)st));
+}
+}  // namespace
+
+int bq_norm_q8(float* dst, const float* src, int rows, int n, int8_t* xq, float* xd, int32_t* xsum,
+               bq_stream_t st) {
+    return norm_q8(0, dst, src, nullptr, nullptr, nullptr, rows, n, xq, xd, xsum, st);
+}
+
+int bq_add_norm_q8(float* x, const float* h, int rows, int n, int8_t* xq, float* xd, int32_t* xsum,
+                   bq_stream_t st) {
+    if (!x || !h) return BQ_EINVAL;
+    return norm_q8(1, x, x, h, nullptr, nullptr, rows, n, xq, xd, xsum, st);
+}
+
+int bq_resid_q8(float* x, const float* upd, const float* alpha, int rows, int n, int8_t* xq, float* xd,
+                int32_t* xsum, bq_stream_t st) {
+    if (!x || !upd || !alpha) return BQ_EINVAL;
+    return norm_q8(2, x, x, upd, alpha, nullptr, rows, n, xq, xd, xsum, st);
+}
+
+int bq_gate_norm_q8(float* dst, const float* aout, const float* gate, const float* sg, int rows, int n,
+                    int8_t* xq, float* xd, int32_t* xsum, bq_stream_t st) {
+    if (!gate || !sg) return BQ_EINVAL;
+    return norm_q8(3, dst, aout, gate, sg, nullptr, rows, n, xq, xd, xsum, st);
+}
+
+int bq_silu_mul_norm_q8(float* dst, const float* g, const float* u, const float* sg, const float* su, int rows,
+                        int n, int8_t* xq, float* xd, int32_t* xsum, bq_stream_t st) {
+    if (!u || !sg || !su) return BQ_EINVAL;
+    return norm_q8(4, dst, g, u, sg, su, rows, n, xq, xd, xsum, st);
+}
+
 // ---- Q8_0 logits head ------------------------------------------------------
 
 size_t bq_q8s_bytes(int K, int N) { return (size_t)N * (K / 256) * 272; }

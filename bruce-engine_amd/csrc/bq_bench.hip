@@ -216,6 +216,40 @@ int bqb_q8s(int steps, int warmup, int nsets, const void* const* ws, int K, int 
     return 0;
 }
 
+// q8 producers: `steps` launches of one norm op over `rows` rows of n values
+// (op 0 norm, 1 add, 2 resid, 3 gate, 4 silu*mul; buffers a..d as the op
+// reads them, out may be NULL).  out_t[0] = timed region (ms), out_t[1] =
+// sum of the kernels' own durations (ms).
+int bqb_norm(int op, int steps, int warmup, float* out, float* a, const float* b, const float* c,
+             const float* d, int rows, int n, int8_t* xq, float* xd, int32_t* xs, bq_stream_t st,
+             double* out_t) {
+    auto launch = [&]() -> int {
+        switch (op) {
+            case 0: return bq_norm_q8(out, a, rows, n, xq, xd, xs, st);
+            case 1: return bq_add_norm_q8(a, b, rows, n, xq, xd, xs, st);
+            case 2: return bq_resid_q8(a, b, c, rows, n, xq, xd, xs, st);
+            case 3: return bq_gate_norm_q8(out, a, b, c, rows, n, xq, xd, xs, st);
+            default: return bq_silu_mul_norm_q8(out, a, b, c, d, rows, n, xq, xd, xs, st);
+        }
+    };
+    for (int i = 0; i < warmup; ++i)
+        if (int r = launch()) return r;
+    EventPool pool((size_t)steps * 2 + 2);
+    hipDeviceSynchronize();
+    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    for (int i = 0; i < steps; ++i) {
+        bq_time_next_launch(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
+        if (int r = launch()) return r;
+    }
+    hipEventRecord(pool.ev[1], (hipStream_t)st);
+    hipDeviceSynchronize();
+    out_t[0] = elapsed(pool.ev[0], pool.ev[1]);
+    double k = 0;
+    for (int i = 0; i < steps; ++i) k += elapsed(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
+    out_t[1] = k;
+    return 0;
+}
+
 // Whole-stack decode weight stream: per token, for each of
 // `nlayers` layers, QKV, O, fused gate+up and down GEMVs, then the lm_head --
 // each one a bq_gemv_q8_fused launch that quantizes its fp32 input row (the

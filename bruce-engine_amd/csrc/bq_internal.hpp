@@ -76,4 +76,11 @@ void q8s_set_cus(int cus);
 hipError_t launch_gemv_q8s(const void* W, int K, int N, int rows, const int8_t* xq, const float* xd,
                            const float* rs, float* y, hipStream_t st);
 
+// q8 producers: elementwise op -> L2 norm -> q8 (op: 0 norm, 1 add, 2 resid,
+// 3 gate, 4 silu*mul); n % 32 == 0, n <= kNormMaxN
+constexpr int kNormMaxN = 32768;
+hipError_t launch_norm_q8(int op, float* out, const float* a, const float* b, const float* c,
+                          const float* d, int rows, int n, int8_t* xq, float* xd, int32_t* xsum,
+                          hipStream_t st);
+
 }  // namespace bq

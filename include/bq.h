@@ -67,6 +67,36 @@ int bq_quantize_q8(const float* x, int rows, int K, int8_t* xq, float* xd, int32
 /* xdh = half(xd*xsum) on its own (k_fill_xdh, bruce.cu:6598-6602). */
 int bq_fill_xdh(const float* xd, const int32_t* xsum, int n, uint16_t* xdh, bq_stream_t st);
 
+/* ---- q8 producers: elementwise op -> row L2 norm -> q8 ---------------------
+ * The kernels that feed the GEMVs on the reference's decode / batch paths emit
+ * the q8 activations themselves.  Per row of n values (rows >= 0, one
+ * workgroup each): t = op(inputs), v = t * l2_scale(sum t^2, n) with
+ * l2_scale(ss, n) = (1/sqrt(ss/n + 1e-6/n)) * (1/sqrt(n)) (bruce.cu:305-307),
+ * then the q8 row of v exactly as bq_quantize_q8 would produce it from v
+ * (q8_emit, bruce.cu:338-366).  The fp32 output is written unless it is NULL
+ * (it is x itself for add / resid).  alpha, sg, su are per-column vectors [n].
+ * n % 32 == 0 and n <= 32768 (else BQ_UNSUPPORTED); every pointer 16-byte
+ * aligned except xd / xsum.  exp is the accurate expf (the reference uses the
+ * fast __expf), so fp32 outputs agree to rounding, not bit for bit. */
+/* dst = norm(src); k_norm (bruce.cu:541-554), k_norm_rows (:1110-1126). */
+int bq_norm_q8(float* dst, const float* src, int rows, int n, int8_t* xq, float* xd, int32_t* xsum,
+               bq_stream_t st);
+/* x = norm(x + h); k_add_norm (:556-569), k_add_norm_rows (:1128-1145). */
+int bq_add_norm_q8(float* x, const float* h, int rows, int n, int8_t* xq, float* xd, int32_t* xsum,
+                   bq_stream_t st);
+/* x = norm(a + (b - a)*alpha), a = norm(x), b = norm(upd); k_resid (:571-600),
+ * k_resid_rows (:1146-1179), k_resid_vec4 (:1475-1527). */
+int bq_resid_q8(float* x, const float* upd, const float* alpha, int rows, int n, int8_t* xq, float* xd,
+                int32_t* xsum, bq_stream_t st);
+/* dst = norm(aout / (1 + exp(-gate*sg))); k_gate_norm (:602-620),
+ * k_gate_norm_rows (:1181-1203), k_gate_norm_vec4 (:1529-1572). */
+int bq_gate_norm_q8(float* dst, const float* aout, const float* gate, const float* sg, int rows, int n,
+                    int8_t* xq, float* xd, int32_t* xsum, bq_stream_t st);
+/* dst = norm(silu(g*sg) * u * su); k_silu_mul_norm (:622-641),
+ * k_silu_mul_norm_rows (:1205-1228), k_silu_mul_norm_vec4 (:1427-1473). */
+int bq_silu_mul_norm_q8(float* dst, const float* g, const float* u, const float* sg, const float* su, int rows,
+                        int n, int8_t* xq, float* xd, int32_t* xsum, bq_stream_t st);
+
 /* ---- decode GEMV ----------------------------------------------------------
  * The GEMV / multi-row entry points take K <= 49152 (BQ_UNSUPPORTED above). 
  * y[N] = W x for one activation row.  Replaces launch_gemv(y, w, x, st)

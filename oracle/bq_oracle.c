@@ -527,3 +527,46 @@ void orc_gemv_q8s(const uint8_t* w, int K, int N, int M, const int8_t* xq, const
             y[(size_t)m * N + n] = rs ? acc * (double)rs[n] : acc;
         }
 }
+
+/* ------------------------------------------------------------------------- */
+/* q8 producers: elementwise op -> L2 norm (bruce.cu:541-641, 1110-1228)      */
+/* ------------------------------------------------------------------------- */
+/* l2_scale (bruce.cu:305-307) with eps = 1e-6f (:73), in double */
+static double l2_scale_d(double ss, int n) {
+    const double eps = (double)1e-6f;
+    return (1.0 / sqrt(ss / n + eps / n)) * (1.0 / sqrt((double)n));
+}
+
+void orc_norm_rows(int op, const float* a, const float* b, const float* c, const float* d, int rows, int n,
+                   double* out) {
+    for (int m = 0; m < rows; ++m) {
+        const float* ar = a + (size_t)m * n;
+        const float* br = b ? b + (size_t)m * n : 0;
+        double* o = out + (size_t)m * n;
+        if (op == 2) { /* k_resid :571-600 */
+            double sa = 0.0, sb = 0.0;
+            for (int i = 0; i < n; ++i) { sa += (double)ar[i] * ar[i]; sb += (double)br[i] * br[i]; }
+            const double ka = l2_scale_d(sa, n), kb = l2_scale_d(sb, n);
+            for (int i = 0; i < n; ++i) {
+                const double an = ar[i] * ka, bn = br[i] * kb;
+                o[i] = an + (bn - an) * c[i];
+            }
+        } else {
+            for (int i = 0; i < n; ++i) {
+                double t;
+                if (op == 0) t = ar[i];                         /* k_norm :541-554 */
+                else if (op == 1) t = (double)ar[i] + br[i];     /* k_add_norm :556-569 */
+                else if (op == 3) t = ar[i] / (1.0 + exp(-((double)br[i] * c[i])));  /* k_gate_norm :602-620 */
+                else {                                           /* k_silu_mul_norm :622-641 */
+                    const double gv = (double)ar[i] * c[i];
+                    t = gv / (1.0 + exp(-gv)) * br[i] * d[i];
+                }
+                o[i] = t;
+            }
+        }
+        double ss = 0.0;
+        for (int i = 0; i < n; ++i) ss += o[i] * o[i];
+        const double k = l2_scale_d(ss, n);
+        for (int i = 0; i < n; ++i) o[i] *= k;
+    }
+}

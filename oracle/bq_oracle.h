@@ -20,6 +20,9 @@
  *   orc_quantize_q8s       codes and scales equal orc_q8_rows on the widened bf16 values
  *                          (scale = half_rn(xd)); hand-built layout KAT with numpy
  *                          float32/float16 arithmetic; round-trip bound |w - s*q| <= s/2
+ *   orc_norm_rows          unit-L2 closed form (|v|^2 = ss/(ss+eps)), scale invariance,
+ *                          alpha = 0 / 1 / sg = 0 special cases, scipy.special.expit
+ *                          restatements of the gate / silu products (tests/test_norm_oracle.py)
  *   orc_gemv_q8s           float64 matmul of the dequantized operands (numpy, built from
  *                          a reshape of the block layout); "y = K" KAT; exact scaling in rs
  * None of the functions is "parity unpinned".
@@ -98,6 +101,14 @@ void orc_quantize_q8s(const uint16_t* bf16, int K, int N, uint8_t* dst);
  * k_gemm_q8_logits, bruce.cu:4409-4449. */
 void orc_gemv_q8s(const uint8_t* w, int K, int N, int M, const int8_t* xq, const float* xd,
                   const float* rs, double* y);
+
+/* ---- q8 producers (bruce.cu:305-307, 541-641, 1110-1228) ------------------ */
+/* The fp32 rows v = t * l2_scale(sum t^2, n) of the reference's norm kernels,
+ * evaluated in double: op 0 norm(a), 1 norm(a + b), 2 resid (a = x, b = upd,
+ * c = alpha[n]), 3 gate (a = aout, b = gate, c = sg[n]), 4 silu*mul (a = g,
+ * b = u, c = sg[n], d = su[n]).  The q8 rows are orc_q8_rows of the result. */
+void orc_norm_rows(int op, const float* a, const float* b, const float* c, const float* d, int rows, int n,
+                   double* out);
 
 #ifdef __cplusplus
 }

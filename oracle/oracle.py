@@ -58,6 +58,7 @@ def lib():
             "orc_repack_q6k_160": (None, [P, I, I, P]),
             "orc_quantize_q8s": (None, [P, I, I, P]),
             "orc_gemv_q8s": (None, [P, I, I, I, P, P, P, P]),
+            "orc_norm_rows": (None, [I, P, P, P, P, I, I, P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -219,6 +220,19 @@ def gemv_q8s(w, K, xq, xd, rs=None):
     rsa = None if rs is None else np.ascontiguousarray(rs, np.float32)
     lib().orc_gemv_q8s(_p(w), K, N, M, _p(xq), _p(xd), None if rsa is None else _p(rsa), _p(y))
     return y
+
+
+NORM_OPS = {"norm": 0, "add": 1, "resid": 2, "gate": 3, "silu": 4}
+
+
+def norm_rows(op, a, b=None, c=None, d=None):
+    """float64 rows v of the reference's norm kernels (see orc_norm_rows)."""
+    a = np.ascontiguousarray(a, np.float32)
+    rows, n = a.shape
+    arr = [None if t is None else np.ascontiguousarray(t, np.float32) for t in (b, c, d)]
+    out = np.empty((rows, n), np.float64)
+    lib().orc_norm_rows(NORM_OPS[op], _p(a), *[None if t is None else _p(t) for t in arr], rows, n, _p(out))
+    return out
 
 
 def f32_to_bf16(x):
