@@ -38,7 +38,8 @@ EXPORTS = [
     "bq_repack_q5k_min_bytes", "bq_repack_q6k", "bq_repack_q6k_host", "bq_repack_q6k_bytes",
     "bq_time_next_launch", "bq_gemv_q8_fused", "bq_q8s_bytes", "bq_quantize_q8s",
     "bq_quantize_q8s_host", "bq_gemv_q8s", "bq_norm_q8", "bq_add_norm_q8", "bq_resid_q8",
-    "bq_gate_norm_q8", "bq_silu_mul_norm_q8",
+    "bq_gate_norm_q8", "bq_silu_mul_norm_q8", "bq_gguf_open", "bq_gguf_close", "bq_gguf_n_tensors",
+    "bq_gguf_find", "bq_gguf_tensor_info", "bq_gguf_kv_num", "bq_gguf_kv_str", "bq_gguf_read", "bq_gguf_load",
 ]
 
 
@@ -52,6 +53,13 @@ class Weight(ctypes.Structure):
     """bq_weight == the reference's TensorW {d, dp, dm, type, K, N} (bruce.cu:78)."""
     _fields_ = [("raw", ctypes.c_void_p), ("rep", ctypes.c_void_p), ("rep_min", ctypes.c_void_p),
                 ("ggml_type", ctypes.c_uint32), ("K", ctypes.c_int32), ("N", ctypes.c_int32)]
+
+
+class GgufTensor(ctypes.Structure):
+    """bq_gguf_tensor (include/bq.h)."""
+    _fields_ = [("name", ctypes.c_char_p), ("suffix", ctypes.c_char_p), ("ne", ctypes.c_uint64 * 4),
+                ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64), ("ggml_type", ctypes.c_uint32),
+                ("ndim", ctypes.c_uint32), ("block", ctypes.c_int32)]
 
 
 _lib = None
@@ -101,6 +109,15 @@ def load(path=LIB_PATH):
         "bq_resid_q8": (I, [P, P, P, I, I, P, P, P, P]),
         "bq_gate_norm_q8": (I, [P, P, P, P, I, I, P, P, P, P]),
         "bq_silu_mul_norm_q8": (I, [P, P, P, P, P, I, I, P, P, P, P]),
+        "bq_gguf_open": (I, [ctypes.c_char_p, ctypes.POINTER(P)]),
+        "bq_gguf_close": (None, [P]),
+        "bq_gguf_n_tensors": (ctypes.c_int64, [P]),
+        "bq_gguf_find": (ctypes.c_int64, [P, ctypes.c_char_p]),
+        "bq_gguf_tensor_info": (I, [P, ctypes.c_int64, ctypes.POINTER(GgufTensor)]),
+        "bq_gguf_kv_num": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+        "bq_gguf_kv_str": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)]),
+        "bq_gguf_read": (I, [P, ctypes.c_int64, P, S, ctypes.c_uint64]),
+        "bq_gguf_load": (I, [P, ctypes.c_int64, P, P, P, WP, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -334,3 +351,62 @@ def norm_q8(op, rows, n, out=None, a=None, b=None, c=None, d=None, q8=None):
     if r not in (BQ_OK, BQ_UNSUPPORTED):
         raise BqError(r, f"norm_q8({op})")
     return r, q8
+
+
+# ---------------------------------------------------------------- GGUF
+class Gguf:
+    """GGUF v3 file opened by libbq's reader (bq_gguf_*)."""
+
+    def __init__(self, path):
+        self._h = ctypes.c_void_p()
+        _check(load().bq_gguf_open(os.fsencode(path), ctypes.byref(self._h)), f"bq_gguf_open({path})")
+
+    def close(self):
+        if self._h:
+            load().bq_gguf_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __len__(self):
+        return load().bq_gguf_n_tensors(self._h)
+
+    def find(self, name):
+        return load().bq_gguf_find(self._h, name.encode())
+
+    def tensor(self, i):
+        t = GgufTensor()
+        _check(load().bq_gguf_tensor_info(self._h, i, ctypes.byref(t)), "bq_gguf_tensor_info")
+        return {"name": t.name.decode(), "suffix": t.suffix.decode(), "ne": list(t.ne)[:t.ndim],
+                "offset": t.offset, "nbytes": t.nbytes, "type": t.ggml_type, "ndim": t.ndim, "block": t.block}
+
+    def kv_num(self, key):
+        v = ctypes.c_double()
+        r = load().bq_gguf_kv_num(self._h, key.encode(), ctypes.byref(v))
+        return v.value if r == BQ_OK else None
+
+    def kv_str(self, key):
+        v = ctypes.c_char_p()
+        r = load().bq_gguf_kv_str(self._h, key.encode(), ctypes.byref(v))
+        return v.value.decode() if r == BQ_OK else None
+
+    def read(self, i, n=None, off=0):
+        import numpy as np
+        nb = self.tensor(i)["nbytes"]
+        n = nb - off if n is None else n
+        out = np.empty(n, np.uint8)
+        _check(load().bq_gguf_read(self._h, i, out.ctypes.data_as(ctypes.c_void_p), n, off), "bq_gguf_read")
+        return out
+
+    def load(self, i, raw, rep=None, rep_min=None):
+        """Stream tensor i into device tensor `raw` (+ repack into rep / rep_min); returns a Weight."""
+        w = Weight()
+        r = load().bq_gguf_load(self._h, i, _ptr(raw), _ptr(rep), _ptr(rep_min), ctypes.byref(w), _stream())
+        if r != BQ_OK:
+            raise BqError(r, "bq_gguf_load")
+        w._keep = (raw, rep, rep_min)
+        return w

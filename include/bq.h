@@ -207,6 +207,49 @@ int bq_quantize_q8s_host(const uint16_t* bf16, int K, int N, void* dst);
 int bq_gemv_q8s(float* y, const void* w, const int8_t* xq, const float* xd, int K, int N, int rows,
                 const float* rs, bq_stream_t st);
 
+/* ---- GGUF reader and streaming loader ---------------------------------------
+ * Replaces GgufFile (engine/src/gguf.h:146-346: v3 header, key/value metadata,
+ * tensor table, pread streaming) and the k-quant part of the streamed weight
+ * loader (bruce.cu:4869-5131, bind_weights :5186-5443).  Host calls; the
+ * reader needs no GPU.  Strings returned stay valid until bq_gguf_close. */
+typedef struct bq_gguf bq_gguf;
+typedef struct bq_gguf_tensor {
+    const char* name;
+    const char* suffix;   /* "attn_q.weight" for "blk.3.attn_q.weight", else "" */
+    uint64_t ne[4];       /* ne[0] = K (row length), ne[1] = N (rows) */
+    uint64_t offset;      /* absolute file offset of the tensor data */
+    uint64_t nbytes;
+    uint32_t ggml_type;
+    uint32_t ndim;
+    int32_t block;        /* N of "blk.N." names, else -1 */
+} bq_gguf_tensor;
+/* BQ_EINVAL: unreadable file, bad magic, version != 3, unknown value or tensor
+ * type, truncated header, or a tensor extending past the end of the file. */
+int bq_gguf_open(const char* path, bq_gguf** out);
+void bq_gguf_close(bq_gguf* g);
+int64_t bq_gguf_n_tensors(const bq_gguf* g);
+int64_t bq_gguf_find(const bq_gguf* g, const char* name);  /* -1 if absent */
+int bq_gguf_tensor_info(const bq_gguf* g, int64_t i, bq_gguf_tensor* out);
+/* numeric (types 0-7, 10-12) and string (type 8) metadata; BQ_UNSUPPORTED if
+ * the key is absent or of another type */
+int bq_gguf_kv_num(const bq_gguf* g, const char* key, double* out);
+int bq_gguf_kv_str(const bq_gguf* g, const char* key, const char** out);
+/* n bytes of tensor i from byte `off` of its data into host memory */
+int bq_gguf_read(const bq_gguf* g, int64_t i, void* dst, size_t n, uint64_t off);
+/* Stream 2-D tensor i into device memory `raw` (nbytes) through two pinned
+ * staging slots (file reads overlap the copies), then on the same stream:
+ *   Q5_K: rep/rep_min given -> W144 + Dm (bq_repack_q5k);
+ *   Q6_K: rep given -> W160 (bq_repack_q6k);
+ *   BF16: rep required -> Q8S logits head (bq_quantize_q8s); raw is the BF16
+ *         staging buffer and may be reused once the stream has passed it.
+ * *w (optional) receives the descriptor: bq_weight of the Q5_K / Q6_K tensor,
+ * or for BF16 raw = the Q8S matrix with ggml_type 8 (Q8_0), for bq_gemv_q8s.
+ * Returns when the file has been read and the copies are done; the repack is
+ * enqueued.  The staging slots (2 x 64 MiB pinned) are allocated on the first
+ * call and freed by bq_gguf_close.  BQ_UNSUPPORTED: not 2-D, another type, or
+ * K % 256 != 0. */
+int bq_gguf_load(bq_gguf* g, int64_t i, void* raw, void* rep, void* rep_min, bq_weight* w, bq_stream_t st);
+
 /* ---- tooling ---------------------------------------------------------------
  * No counterpart in the reference (its harnesses bracket launches with
  * cudaEventRecord, tools/gemvbench.cu:360-371).  Times the calling thread's

@@ -1,0 +1,106 @@
+"""CPU checks of libbq's GGUF v3 reader (bq_gguf_*; engine/src/gguf.h:146-346)
+against files written by tests/gguf_writer.py: metadata of every value type,
+the tensor table (types, dims, absolute offsets, byte sizes, blk.N names), the
+alignment rule, byte reads, and the malformed files the reader must reject."""
+import struct
+
+import numpy as np
+import pytest
+
+import gguf_writer as W
+
+KV = [
+    ("general.architecture", W.T_STR, "bruce"),
+    ("general.alignment", W.T_U32, 64),
+    ("u8", W.T_U8, 200), ("i8", W.T_I8, -100), ("u16", W.T_U16, 60000), ("i16", W.T_I16, -30000),
+    ("u32", W.T_U32, 4000000000), ("i32", W.T_I32, -2000000000), ("f32", W.T_F32, 1.5),
+    ("bool", W.T_BOOL, 1), ("u64", W.T_U64, 2 ** 40), ("i64", W.T_I64, -(2 ** 40)), ("f64", W.T_F64, -2.25),
+    ("tokens", W.T_ARR, (W.T_STR, ["a", "bb", ""])),
+    ("scores", W.T_ARR, (W.T_F32, [0.5, -1.0])),
+    ("ids", W.T_ARR, (W.T_I64, [1, 2, 3])),
+]
+
+
+def make_file(tmp_path, kv=KV):
+    q5 = W.random_kquant(1, 16, 512, 176)
+    q6 = W.random_kquant(2, 8, 768, 210)
+    bf = np.arange(4 * 256, dtype=np.uint16).reshape(4, 256)
+    f32 = np.linspace(-1, 1, 100).astype(np.float32)
+    tensors = [("blk.0.ffn_gate.weight", 13, (512, 16), q5.tobytes()),
+               ("blk.12.ffn_down.weight", 14, (768, 8), q6.tobytes()),
+               ("output.weight", 30, (256, 4), bf.tobytes()),
+               ("output_norm.weight", 0, (100,), f32.tobytes())]
+    path = str(tmp_path / "t.gguf")
+    data_off = W.write_gguf(path, kv, tensors, alignment=64)
+    return path, data_off, tensors
+
+
+def test_gguf_metadata_and_table(tmp_path):
+    import bq
+    path, data_off, tensors = make_file(tmp_path)
+    with bq.Gguf(path) as g:
+        assert len(g) == 4
+        assert g.kv_str("general.architecture") == "bruce"
+        expect = {"u8": 200, "i8": -100, "u16": 60000, "i16": -30000, "u32": 4000000000, "i32": -2000000000,
+                  "f32": 1.5, "bool": 1, "u64": 2 ** 40, "i64": -(2 ** 40), "f64": -2.25, "general.alignment": 64}
+        for k, v in expect.items():
+            assert g.kv_num(k) == v, k
+        assert g.kv_num("tokens") is None and g.kv_str("u8") is None and g.kv_num("missing") is None
+        off = data_off
+        for i, (name, gt, ne, payload) in enumerate(tensors):
+            t = g.tensor(i)
+            assert g.find(name) == i
+            assert t["name"] == name and t["type"] == gt and t["ne"] == list(ne) and t["ndim"] == len(ne)
+            assert t["nbytes"] == len(payload) and t["offset"] == off and t["offset"] % 64 == 0
+            off += (len(payload) + 63) // 64 * 64
+            assert g.read(i).tobytes() == payload
+            assert g.read(i, 10, 5).tobytes() == payload[5:15]
+        assert g.tensor(0)["block"] == 0 and g.tensor(0)["suffix"] == "ffn_gate.weight"
+        assert g.tensor(1)["block"] == 12 and g.tensor(1)["suffix"] == "ffn_down.weight"
+        assert g.tensor(2)["block"] == -1 and g.tensor(2)["suffix"] == ""
+        assert g.find("nope") == -1
+        with pytest.raises(bq.BqError):
+            g.read(0, 10, len(tensors[0][3]) - 5)          # past the tensor's end
+
+
+def test_gguf_default_alignment_and_big_header(tmp_path):
+    """No general.alignment -> 32; a header larger than the reader's first
+    prefix (1 MiB of string array) is still parsed."""
+    import bq
+    big = [("vocab", W.T_ARR, (W.T_STR, ["tok%06d" % i for i in range(120000)]))]
+    q5 = W.random_kquant(3, 4, 256, 176)
+    path = str(tmp_path / "b.gguf")
+    data_off = W.write_gguf(path, big, [("w", 13, (256, 4), q5.tobytes())])
+    assert data_off > (1 << 20) and data_off % 32 == 0
+    with bq.Gguf(path) as g:
+        t = g.tensor(0)
+        assert t["offset"] == data_off and g.read(0).tobytes() == q5.tobytes()
+
+
+@pytest.mark.parametrize("case", ["magic", "version", "truncated", "kvtype", "ttype", "past_end", "ndim"])
+def test_gguf_rejects(tmp_path, case):
+    import bq
+    q5 = W.random_kquant(4, 2, 256, 176).tobytes()
+    kv = [("a", W.T_U32, 1)]
+    tensors = [("w", 13, (256, 2), q5)]
+    if case == "magic":
+        blob, _ = W.gguf_bytes(kv, tensors, magic=0x12345678)
+    elif case == "version":
+        blob, _ = W.gguf_bytes(kv, tensors, version=2)
+    elif case == "truncated":
+        blob = W.gguf_bytes(kv, tensors)[0][:30]
+    elif case == "kvtype":
+        blob, _ = W.gguf_bytes([], tensors)     # n_kv = 0; splice in one pair of value type 99
+        blob = blob[:16] + struct.pack("<Q", 1) + W._str("k") + struct.pack("<I", 99) + blob[24:]
+    elif case == "ttype":
+        blob, _ = W.gguf_bytes(kv, [("w", 77, (256, 2), q5)])
+    elif case == "past_end":
+        blob = W.gguf_bytes(kv, tensors)[0][:-100]
+    else:
+        blob, _ = W.gguf_bytes(kv, [("w", 13, (256, 2, 1, 1, 1), q5)])
+    path = tmp_path / "bad.gguf"
+    path.write_bytes(blob)
+    with pytest.raises(bq.BqError):
+        bq.Gguf(str(path))
+    with pytest.raises(bq.BqError):
+        bq.Gguf(str(tmp_path / "missing.gguf"))
