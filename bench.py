@@ -123,6 +123,24 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
     if r != 0:
         raise RuntimeError(f"bqb_stack failed: {r}")
     ms = out[0] / steps
+    # the same weights in the reference's dependent decode sequence, with the
+    # q8 producers (gate norm, resid, silu*mul norm, final norm) between GEMVs
+    g = torch.Generator(device="cuda").manual_seed(SEED + 15)
+    fb = [torch.randn(n, generator=g, device="cuda") for n in (K, K, NQKV, KO, FF, FF, VOCAB)]
+    fb += [torch.rand(n, generator=g, device="cuda") * 0.5 + 0.25 for n in (K, K, KO, FF, FF)]
+    qb = []
+    for n in (K, KO, FF):
+        qb += [torch.empty(n, dtype=torch.int8, device="cuda"), torch.empty(n // 32, device="cuda"),
+               torch.empty(n // 32, dtype=torch.int32, device="cuda")]
+    xq0, xd0, xs0 = bq.quantize_q8(fb[0].view(1, K))
+    qb[0].copy_(xq0.view(-1)); qb[1].copy_(xd0.view(-1)); qb[2].copy_(xs0.view(-1))
+    farr = (ctypes.c_void_p * len(fb))(*[t.data_ptr() for t in fb])
+    qarr = (ctypes.c_void_p * len(qb))(*[t.data_ptr() for t in qb])
+    r = B.bqb_chain(steps, warmup, LAYERS, ws, ctypes.byref(lmw), farr, qarr, K, KO, FF, sp, out)
+    if r != 0:
+        raise RuntimeError(f"bqb_chain failed: {r}")
+    chain_ms = out[0] / steps
+    del fb, qb
     wbytes = LAYERS * sum(a.nbytes for a in (w_qkv, w_o, w_gate, w_up, w_down)) + lm.numel()
     act = LAYERS * (2 * (4 * K + q8_bytes(1, K)) + (4 * KO + q8_bytes(1, KO)) + (4 * FF + q8_bytes(1, FF))) \
         + 4 * K + q8_bytes(1, K)
@@ -133,7 +151,12 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
                       "Q6_K) + lm_head Q6_K 131072x3072, batch 1, one HIP graph per token",
             "weight_bytes_per_token": wbytes, "bytes_per_token": tot, "ms_per_token": round(ms, 4),
             "GBps": round(gbs(tot, ms), 1), "hbm_frac": round(gbs(tot, ms) / HBM_PEAK_GBS, 4),
-            "launches_per_token": 4 * LAYERS + 1}
+            "launches_per_token": 4 * LAYERS + 1,
+            "decode_chain": {"what": "the reference's dependent decode sequence per layer: QKV GEMV, gate norm -> q8, "
+                                     "O GEMV, resid -> q8, gate+up GEMV, silu*mul norm -> q8, down GEMV, resid -> q8; "
+                                     "final norm -> q8, lm_head (attention excluded; aout a fixed input)",
+                             "ms_per_token": round(chain_ms, 4), "GBps": round(gbs(tot, chain_ms), 1),
+                             "launches_per_token": 8 * LAYERS + 2}}
 
 
 def q8s_head(B, bq, torch, sp, ptr, steps=50):
@@ -286,6 +309,7 @@ def main():
     B.bqb_stack.argtypes = [I, I, I, WP, WP, P, P, P, P, P, P, P, P, P, P]
     B.bqb_q8s.argtypes = [I, I, I, P, I, I, I, P, P, P, P, P, P]
     B.bqb_norm.argtypes = [I, I, I, P, P, P, P, P, I, I, P, P, P, P, P]
+    B.bqb_chain.argtypes = [I, I, I, WP, WP, P, P, I, I, I, P, P]
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
     ptr = lambda t: ctypes.c_void_p(t.data_ptr())

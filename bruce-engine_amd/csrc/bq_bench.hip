@@ -194,6 +194,66 @@ int bqb_gemv_rows(int steps, int warmup, int nsets, const bq_weight* w, int rows
     return 0;
 }
 
+// The reference's decode sequence for the matmul path, per layer (bruce.cu
+// forward_launch :7902-8037, attention itself excluded): QKV GEMV on q8 x;
+// gate norm of the attention output -> q8 a (aout is a fixed input here, its
+// gate the first KO QKV outputs); O GEMV on q8 a; resid -> q8 x; fused
+// gate+up GEMV; silu*mul norm -> q8 t; down GEMV on q8 t; resid -> q8 x.  Then
+// the final norm -> q8 and the lm_head GEMV.  Every launch reads what the one
+// before it wrote.  One HIP graph per token; out[0] = timed region (ms).
+// w = [nlayers][5] (qkv, o, gate, up, down); f = fp32 buffers {x, proj, yqkv,
+// aout, yg, yu, logits, alpha, alpha2, sgate, sg, su}; q = q8 buffers
+// {xq, xd, xs, aq, ad, as, tq, td, ts} (as void*).
+int bqb_chain(int steps, int warmup, int nlayers, const bq_weight* w, const bq_weight* lm_head, float* const* f,
+              void* const* q, int K, int KO, int FF, bq_stream_t st, double* out) {
+    float *x = f[0], *proj = f[1], *yqkv = f[2], *aout = f[3], *yg = f[4], *yu = f[5], *logits = f[6];
+    const float *alpha = f[7], *alpha2 = f[8], *sgate = f[9], *sg = f[10], *su = f[11];
+    int8_t *xq = (int8_t*)q[0], *aq = (int8_t*)q[3], *tq = (int8_t*)q[6];
+    float *xd = (float*)q[1], *ad = (float*)q[4], *td = (float*)q[7];
+    int32_t *xs = (int32_t*)q[2], *as_ = (int32_t*)q[5], *ts = (int32_t*)q[8];
+    hipStream_t cs;
+    if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) return -1;
+    auto token = [&](bq_stream_t s) -> int {
+        for (int l = 0; l < nlayers; ++l) {
+            const bq_weight* lw = w + 5 * l;
+            float* y1[1] = {yqkv};
+            const bq_weight* p1[1] = {&lw[0]};
+            if (int r = bq_verify_fused(y1, p1, 1, 1, xq, xd, xs, 0, s)) return r;
+            if (int r = bq_gate_norm_q8(nullptr, aout, yqkv, sgate, 1, KO, aq, ad, as_, s)) return r;
+            if (int r = bq_gemv(proj, &lw[1], aq, ad, as_, s)) return r;
+            if (int r = bq_resid_q8(x, proj, alpha, 1, K, xq, xd, xs, s)) return r;
+            float* y2[2] = {yg, yu};
+            const bq_weight* p2[2] = {&lw[2], &lw[3]};
+            if (int r = bq_verify_fused(y2, p2, 2, 1, xq, xd, xs, 0, s)) return r;
+            if (int r = bq_silu_mul_norm_q8(nullptr, yg, yu, sg, su, 1, FF, tq, td, ts, s)) return r;
+            if (int r = bq_gemv(proj, &lw[4], tq, td, ts, s)) return r;
+            if (int r = bq_resid_q8(x, proj, alpha2, 1, K, xq, xd, xs, s)) return r;
+        }
+        if (int r = bq_norm_q8(nullptr, x, 1, K, xq, xd, xs, s)) return r;
+        return bq_gemv(logits, lm_head, xq, xd, xs, s);
+    };
+    for (int i = 0; i < warmup; ++i)
+        if (int r = token(st)) return r;
+    hipGraph_t g;
+    hipGraphExec_t ex;
+    hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+    const int r = token((bq_stream_t)cs);
+    if (hipStreamEndCapture(cs, &g) != hipSuccess || r) return r ? r : -1;
+    if (hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) != hipSuccess) return -1;
+    hipGraphDestroy(g);
+    hipGraphLaunch(ex, (hipStream_t)st);
+    EventPool pool(2);
+    hipDeviceSynchronize();
+    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    for (int i = 0; i < steps; ++i) hipGraphLaunch(ex, (hipStream_t)st);
+    hipEventRecord(pool.ev[1], (hipStream_t)st);
+    hipDeviceSynchronize();
+    out[0] = elapsed(pool.ev[0], pool.ev[1]);
+    hipGraphExecDestroy(ex);
+    hipStreamDestroy(cs);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // Q8_0 logits head: `steps` launches of bq_gemv_q8s, weight copy s = i % nsets.
 // out[0] = timed region (ms), out[1] = sum of the kernels' own durations (ms).
 int bqb_q8s(int steps, int warmup, int nsets, const void* const* ws, int K, int N, int rows, const int8_t* xq,
