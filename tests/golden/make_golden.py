@@ -1,6 +1,7 @@
 """Writes tests/golden/golden.npz: small seeded inputs and the oracle's outputs
 for every function of the path (q8 quantizer incl. edge values, Q5_K/Q6_K GEMV
-in double and fp32 order, both repacks, the W144 GEMM).
+in double and fp32 order, both repacks, the W144 GEMM, the BF16 -> Q8S
+conversion and Q8S GEMV of the logits head, and the five q8-producing norms).
 
 These are regression fixtures of this repository's CPU oracle (oracle/), not
 vectors produced by the reference: the reference ships none for this path and
@@ -60,6 +61,25 @@ def main():
     g.update(gemm_w5=wg, gemm_xq=gq, gemm_xd=gd, gemm_xs=gs)
     g["gemm_y144"] = O.gemm_q5k_144(w144, dm, gq, gd, xdh, Ng).astype(np.float32)
     g["gemm_y_exact"] = O.gemm_q5k(wg, gq, gd, gs).astype(np.float32)
+    # Q8_0 logits head: BF16 6 x 512 with a zero group, a denormal-scale group
+    # and a +-3e4 group; Q8S GEMV of 3 q8 rows with a per-row scale
+    Kh, Nh = 512, 6
+    wb = O.f32_to_bf16(O.gaussian(0xC0E4, Nh * Kh, 0.0, 0.02).reshape(Nh, Kh))
+    wb[0, :32] = 0
+    wb[1, 32:64] = O.f32_to_bf16(np.full(32, 1e-38, np.float32))
+    wb[2, 64:96] = O.f32_to_bf16(np.linspace(-3e4, 3e4, 32).astype(np.float32))
+    hq = O.quantize_q8s(wb)
+    rs = O.gaussian(0xC0E5, Nh, 1.0, 0.2)
+    g.update(q8s_bf16=wb, q8s_w=hq, q8s_rs=rs)
+    g["q8s_y"] = O.gemv_q8s(hq, Kh, xq[:, :Kh], xd[:, :Kh // 32], rs)
+    # q8 producers: 2 rows x 256 per op, fp64 rows of the oracle
+    n = 256
+    a, b = O.gaussian(0xC0E6, 2 * n).reshape(2, n), O.gaussian(0xC0E7, 2 * n, 0.0, 2.0).reshape(2, n)
+    c, d = O.gaussian(0xC0E8, n, 0.5, 0.3), O.gaussian(0xC0E9, n, 1.0, 0.3)
+    g.update(norm_a=a, norm_b=b, norm_c=c, norm_d=d)
+    for op, args in (("norm", (a,)), ("add", (a, b)), ("resid", (a, b, c)), ("gate", (a, b, c)),
+                     ("silu", (b, a, c, d))):
+        g[f"norm_{op}"] = O.norm_rows(op, *args)
     np.savez_compressed(os.path.join(HERE, "golden.npz"), **g)
     print("wrote", os.path.join(HERE, "golden.npz"), {k: v.shape for k, v in g.items()})
 

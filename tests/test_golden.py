@@ -45,6 +45,17 @@ def test_oracle_reproduces_golden(oracle, gold):
     xdh = oracle.fill_xdh(g["gemm_xd"], g["gemm_xs"])
     y = oracle.gemm_q5k_144(w144g, dmg, g["gemm_xq"], g["gemm_xd"], xdh, g["gemm_w5"].shape[0])
     assert np.array_equal(_bits(y.astype(np.float32)), _bits(g["gemm_y144"]))
+    assert np.array_equal(oracle.quantize_q8s(g["q8s_bf16"]), g["q8s_w"])
+    Kh = g["q8s_bf16"].shape[1]
+    yh = oracle.gemv_q8s(g["q8s_w"], Kh, g["gemv_xq"][:, :Kh], g["gemv_xd"][:, :Kh // 32], g["q8s_rs"])
+    assert np.array_equal(_bits(yh), _bits(g["q8s_y"]))
+    for op, args in NORM_ARGS.items():
+        got = oracle.norm_rows(op, *[g[k] for k in args])
+        assert np.array_equal(_bits(got), _bits(g[f"norm_{op}"])), op
+
+
+NORM_ARGS = {"norm": ("norm_a",), "add": ("norm_a", "norm_b"), "resid": ("norm_a", "norm_b", "norm_c"),
+             "gate": ("norm_a", "norm_b", "norm_c"), "silu": ("norm_b", "norm_a", "norm_c", "norm_d")}
 
 
 @pytest.mark.gpu
@@ -82,3 +93,33 @@ def test_hip_matches_golden(bq, oracle, gold):
         assert bq.try_mmq([y], [w], Mg, dev(g["gemm_xq"]), dev(g["gemm_xd"]), dev(g["gemm_xs"]), xdh) == bq.BQ_OK
         torch.cuda.synchronize()
         assert oracle.normwise_err(host(y), ref.astype(np.float64)) < TOL
+
+
+@pytest.mark.gpu
+def test_hip_matches_golden_head_and_producers(bq, oracle, gold):
+    import torch
+    g = gold
+    Nh, Kh = g["q8s_bf16"].shape
+    hq = bq.quantize_q8s(dev(g["q8s_bf16"].view(np.int16)), Kh, Nh)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(hq), g["q8s_w"])
+    M = g["gemv_xq"].shape[0]
+    y = torch.full((M, Nh), float("nan"), device="cuda")
+    xq = dev(np.ascontiguousarray(g["gemv_xq"][:, :Kh]))
+    xd = dev(np.ascontiguousarray(g["gemv_xd"][:, :Kh // 32]))
+    assert bq.gemv_q8s(y, hq, xq, xd, Kh, Nh, M, dev(g["q8s_rs"])) == bq.BQ_OK
+    torch.cuda.synchronize()
+    assert oracle.normwise_err(host(y), g["q8s_y"]) < TOL
+    n = g["norm_a"].shape[1]
+    for op, args in NORM_ARGS.items():
+        ins = [dev(g[k]) for k in args]
+        out = ins[0] if op in ("add", "resid") else torch.empty((2, n), device="cuda")
+        kw = dict(out=out, a=ins[0])
+        kw.update({k: t for k, t in zip("bcd", ins[1:])})
+        r, (q, d_, s_) = bq.norm_q8(op, 2, n, **kw)
+        assert r == bq.BQ_OK
+        torch.cuda.synchronize()
+        o = host(out)
+        assert oracle.normwise_err(o, g[f"norm_{op}"]) < 2e-6, op
+        rq, rd, rs_ = oracle.q8_rows(o)
+        assert np.array_equal(host(q), rq) and np.array_equal(host(s_), rs_), op
