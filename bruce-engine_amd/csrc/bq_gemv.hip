@@ -425,12 +425,15 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     // The fused quantizer's fp32 row comes from memory that the whole grid's
     // weight stream is also queueing on: issued together, the row lands only
     // after several microseconds (measured: median 3.5-4 us, p90 5-6 us, with
-    // the compute waiting for it).  So with QN > 0 every wave stages and
-    // quantizes first and issues its weight loads after the barrier: the row
-    // lands in ~1.5 us and the weight stream is overlapped with the compute.
+    // the compute waiting for it).  With a 9216-value row (36 KB of fp32 per
+    // workgroup: the down projection) every wave therefore stages and
+    // quantizes first and issues its weight loads after the barrier.  With the
+    // 3072 / 4096-value rows of the compile-time-K decode instances the row is
+    // a third of that and issuing the weights first measured faster (gate+up
+    // 10.3 -> 9.8 us, whole stack 1.008 -> 0.998 ms/token, interleaved A/B).
     // q8 staging (DMA of a row the previous kernel just wrote) stays ahead of
     // the weight loads.
-    constexpr bool kLate = QN > 0;
+    constexpr bool kLate = QN > 0 && KC != 3072 && KC != 4096;
     constexpr int kEarly = kLate ? 0 : SPS;  // steps whose loads go out before the staging wait
                                              // (issuing 1 or 2 of 3 early measured slower)
     auto issue_weights = [&](int s0, int s1) {
