@@ -519,15 +519,35 @@ static void build_tiles(PartTable& pt, int rows_per_tile = kRowsPerTile) {
     pt.ntiles = acc;
 }
 
-// K split: ceil(K/1024) steps per row, at most 3 per wave (BQ_GEMV_SPS=1|2
-// lowers the cap: a dev A/B switch, read once)
-static void k_split(int K, int& KS, int& SPS) {
-    static int cap = -1;
-    if (cap < 0) {
+// K split: ceil(K/1024) steps per row, at most `cap` per wave.  The cap
+// decides how many waves share a row (KS = steps / cap) and so the workgroup
+// shape; it is chosen per shape class from interleaved A/B measurements
+// (kernel durations, us):
+//   fused quantize + GEMV: 3 (gate+up, QKV, O); K = 9216 (down): 2 (9.03 -> 8.47)
+//   Q6_K, 2..8 rows (3072 x 9216): 2 (8 rows: 29.1 -> 15.8 -- the 92 KB of
+//     staged activations per workgroup want more rows per workgroup); 1 row: 3
+//   Q5_K 1..2 rows: 1 if N*K >= 16M values (9216 x 3072: 5.91 -> 5.37), else 3
+//   Q5_K 3..4 rows: 1 (9216 x 3072, 4 rows: 8.24 -> 7.53)
+//   Q5_K 5..8 rows: 2 if N*K >= 16M values (8 rows 12.70 -> 12.42), else 1
+// BQ_GEMV_SPS=1|2|3 overrides the cap (a dev A/B switch, read once).
+static int sps_cap(GemvKind kind, int K, long long N, int MR, bool fused) {
+    static int env = -1;
+    if (env < 0) {
         const char* e = getenv("BQ_GEMV_SPS");
-        cap = e ? std::max(1, std::min(3, atoi(e))) : 3;
+        env = e ? std::max(1, std::min(3, atoi(e))) : 0;
     }
+    if (env) return env;
+    if (fused) return K > 4096 ? 2 : 3;
+    if (kind != GemvKind::Q5K) return MR == 1 ? 3 : 2;
+    const bool big = N * K >= (16ll << 20);
+    if (MR <= 2) return big ? 1 : 3;
+    if (MR <= 4) return 1;
+    return big ? 2 : 1;
+}
+
+static void k_split(int K, int cap, int& KS, int& SPS) {
     const int spt = (K / 64 + kTasksPerStep - 1) / kTasksPerStep;
+    cap = std::min(3, std::max(cap, (spt + 15) / 16));  // at most 16 slices (K <= 49152)
     KS = (spt + cap - 1) / cap;
     SPS = (spt + KS - 1) / KS;
 }
@@ -593,11 +613,16 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     return hipGetLastError();
 }
 
+template <class F> struct KindOf;
+template <> struct KindOf<FmtQ5K> { static constexpr GemvKind v = GemvKind::Q5K; };
+template <> struct KindOf<FmtQ6KRaw> { static constexpr GemvKind v = GemvKind::Q6KRaw; };
+template <> struct KindOf<FmtQ6KRep> { static constexpr GemvKind v = GemvKind::Q6KRep; };
+
 template <class F, int MR>
 static hipError_t dispatch_mr(const PartTable& pt, int K, const int8_t* xq, const float* xd,
                               const int32_t* xsum, hipStream_t st) {
     int KS, SPS;
-    k_split(K, KS, SPS);
+    k_split(K, sps_cap(KindOf<F>::v, K, (long long)pt.ntiles * kRowsPerTile, MR, false), KS, SPS);
     if (KS > 16) return hipErrorInvalidValue;  // K > 49152
     switch (SPS) {
         case 1: return launch_fmt<F, MR, 1>(pt, K, KS, xq, xd, xsum, st);
@@ -660,7 +685,7 @@ static hipError_t dispatch_fused_qn(const PartTable& pt, int K, int KS, const Fu
 template <class F>
 static hipError_t dispatch_fused(const PartTable& pt, int K, const FusedQ8& fq, hipStream_t st) {
     int KS, SPS;
-    k_split(K, KS, SPS);
+    k_split(K, sps_cap(KindOf<F>::v, K, (long long)pt.ntiles * kRowsPerTile, 1, true), KS, SPS);
     if (K > kFusedMaxK || KS > 16) return hipErrorInvalidValue;
     switch (SPS) {
         case 1: return dispatch_fused_qn<F, 1>(pt, K, KS, fq, st);

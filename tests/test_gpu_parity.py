@@ -230,8 +230,9 @@ def test_q6_verify_fused(bq, oracle):
 ])
 def test_gemv_q8_fused(bq, oracle, qtype, K, Ns, rep):
     """One launch quantizes x and runs the GEMV: q8 outputs bit-exact with the
-    oracle quantizer, y within TOL of the oracle and bit-identical to the
-    unfused pair (same kernel arithmetic once the codes are in LDS)."""
+    oracle quantizer, y within TOL of the oracle and within 1e-6 of the
+    unfused pair (the same per-group arithmetic once the codes are in LDS; the
+    two paths may split K differently, which reorders the slice sums)."""
     import torch
     x, _ = acts(1000 + K, 1, K)
     x[0, :32] = 0.0                                  # an all-zero group
@@ -255,10 +256,12 @@ def test_gemv_q8_fused(bq, oracle, qtype, K, Ns, rep):
     for r, y, w in zip(raws, ys, ws):
         ref = oracle.gemm_q5k(r, xq, xd, xs) if qtype == "q5k" else oracle.gemm_q6k(r, xq, xd)
         assert oracle.normwise_err(host(y)[None], ref) < TOL
+        # the two-launch pair: the same per-group arithmetic; the K split (and
+        # so the order in which slice sums are added) may differ per path
         y2 = torch.full_like(y, float("nan"))
         bq.gemv(y2, w, gq, gd, gs)
         torch.cuda.synchronize()
-        assert np.array_equal(host(y2).view(np.uint32), host(y).view(np.uint32))
+        assert oracle.normwise_err(host(y2)[None], host(y).astype(np.float64)[None]) < 1e-6
     ys3 = [torch.full((n,), float("nan"), device="cuda") for n in Ns]   # without q8 outputs
     assert bq.gemv_q8_fused(ys3, ws, gx) == bq.BQ_OK
     torch.cuda.synchronize()
