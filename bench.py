@@ -136,10 +136,16 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
     qb[0].copy_(xq0.view(-1)); qb[1].copy_(xd0.view(-1)); qb[2].copy_(xs0.view(-1))
     farr = (ctypes.c_void_p * len(fb))(*[t.data_ptr() for t in fb])
     qarr = (ctypes.c_void_p * len(qb))(*[t.data_ptr() for t in qb])
-    r = B.bqb_chain(steps, warmup, LAYERS, ws, ctypes.byref(lmw), farr, qarr, K, KO, FF, sp, out)
+    r = B.bqb_chain(steps, warmup, LAYERS, ws, ctypes.byref(lmw), farr, qarr, K, KO, FF, 0, None, sp, out)
     if r != 0:
         raise RuntimeError(f"bqb_chain failed: {r}")
     chain_ms = out[0] / steps
+    # the same sequence with every q8 producer folded into its consuming GEMV
+    x2 = torch.empty(K, device="cuda")
+    r = B.bqb_chain(steps, warmup, LAYERS, ws, ctypes.byref(lmw), farr, qarr, K, KO, FF, 1, ptr(x2), sp, out)
+    if r != 0:
+        raise RuntimeError(f"bqb_chain (folded) failed: {r}")
+    folded_ms = out[0] / steps
     del fb, qb
     wbytes = LAYERS * sum(a.nbytes for a in (w_qkv, w_o, w_gate, w_up, w_down)) + lm.numel()
     act = LAYERS * (2 * (4 * K + q8_bytes(1, K)) + (4 * KO + q8_bytes(1, KO)) + (4 * FF + q8_bytes(1, FF))) \
@@ -156,7 +162,12 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
                                      "O GEMV, resid -> q8, gate+up GEMV, silu*mul norm -> q8, down GEMV, resid -> q8; "
                                      "final norm -> q8, lm_head (attention excluded; aout a fixed input)",
                              "ms_per_token": round(chain_ms, 4), "GBps": round(gbs(tot, chain_ms), 1),
-                             "launches_per_token": 8 * LAYERS + 2}}
+                             "launches_per_token": 8 * LAYERS + 2},
+            "decode_chain_folded": {"what": "the same dependent sequence with the q8 producers of the small GEMVs "
+                                            "folded into them (bq_gemv_norm_fused): QKV+resid, O+gate norm; resid, "
+                                            "gate+up, silu*mul norm, down as before; last resid; lm_head+final norm",
+                                    "ms_per_token": round(folded_ms, 4), "GBps": round(gbs(tot, folded_ms), 1),
+                                    "launches_per_token": 6 * LAYERS + 2}}
 
 
 def q8s_head(B, bq, torch, sp, ptr, steps=50):
@@ -309,7 +320,7 @@ def main():
     B.bqb_stack.argtypes = [I, I, I, WP, WP, P, P, P, P, P, P, P, P, P, P]
     B.bqb_q8s.argtypes = [I, I, I, P, I, I, I, P, P, P, P, P, P]
     B.bqb_norm.argtypes = [I, I, I, P, P, P, P, P, I, I, P, P, P, P, P]
-    B.bqb_chain.argtypes = [I, I, I, WP, WP, P, P, I, I, I, P, P]
+    B.bqb_chain.argtypes = [I, I, I, WP, WP, P, P, I, I, I, I, P, P, P]
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
     ptr = lambda t: ctypes.c_void_p(t.data_ptr())

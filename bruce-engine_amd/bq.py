@@ -40,6 +40,7 @@ EXPORTS = [
     "bq_quantize_q8s_host", "bq_gemv_q8s", "bq_norm_q8", "bq_add_norm_q8", "bq_resid_q8",
     "bq_gate_norm_q8", "bq_silu_mul_norm_q8", "bq_gguf_open", "bq_gguf_close", "bq_gguf_n_tensors",
     "bq_gguf_find", "bq_gguf_tensor_info", "bq_gguf_kv_num", "bq_gguf_kv_str", "bq_gguf_read", "bq_gguf_load",
+    "bq_gemv_norm_fused",
 ]
 
 
@@ -100,6 +101,7 @@ def load(path=LIB_PATH):
         "bq_repack_q6k_bytes": (S, [I, I]),
         "bq_time_next_launch": (I, [P, P]),
         "bq_gemv_q8_fused": (I, [P, P, I, P, P, P, P, P]),
+        "bq_gemv_norm_fused": (I, [P, P, I, I, P, P, P, P, P, P, P, P, P]),
         "bq_q8s_bytes": (S, [I, I]),
         "bq_quantize_q8s": (I, [P, I, I, P, P]),
         "bq_quantize_q8s_host": (I, [P, I, I, P]),
@@ -214,6 +216,24 @@ def gemv_q8_fused(ys, ws, x, xq=None, xd=None, xsum=None):
     r = load().bq_gemv_q8_fused(yarr, warr, len(ws), _ptr(x), _ptr(xq), _ptr(xd), _ptr(xsum), _stream())
     if r not in (BQ_OK, BQ_UNSUPPORTED):
         raise BqError(r, "bq_gemv_q8_fused")
+    return r
+
+
+OPS = {"norm": 0, "add": 1, "resid": 2, "gate": 3, "silu": 4}
+
+
+def gemv_norm_fused(ys, ws, op, a, b=None, c=None, d=None, out=None, q8=None):
+    """q8 producer (op as norm_q8: norm a; add a+b; resid x=a, upd=b, alpha=c;
+    gate aout=a, gate=b, sg=c; silu g=a, u=b, sg=c, su=d) and the GEMV of its
+    row over every part, one launch.  out receives the produced fp32 row, q8 =
+    (xq, xd, xsum) its q8 row.  Returns the raw code (BQ_UNSUPPORTED: nothing ran)."""
+    _need_gpu(a, b, c, d, out)
+    yarr, warr = _arrays(ys, ws)
+    xq, xd, xs = q8 if q8 is not None else (None, None, None)
+    r = load().bq_gemv_norm_fused(yarr, warr, len(ws), OPS[op], _ptr(out), _ptr(a), _ptr(b), _ptr(c), _ptr(d),
+                                  _ptr(xq), _ptr(xd), _ptr(xs), _stream())
+    if r not in (BQ_OK, BQ_UNSUPPORTED):
+        raise BqError(r, "bq_gemv_norm_fused")
     return r
 
 

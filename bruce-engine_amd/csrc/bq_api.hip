@@ -238,6 +238,51 @@ int bq_gemv_q8_fused(float* const* ys, const bq_weight* const* ws, int nparts, c
     return from_hip(launch_gemv_fused_q8(kind, pt, K, x, xq, xd, xsum, s));
 }
 
+int bq_gemv_norm_fused(float* const* ys, const bq_weight* const* ws, int nparts, int op, float* out,
+                       const float* a, const float* b, const float* c, const float* d, int8_t* xq,
+                       float* xd, int32_t* xsum, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (nparts < 1 || nparts > BQ_MAX_PARTS) return BQ_UNSUPPORTED;
+    if (!ys || !ws || !ws[0] || !a || op < BQ_OP_NORM || op > BQ_OP_SILU) return BQ_EINVAL;
+    if ((xq != nullptr) != (xd != nullptr) || (xq != nullptr) != (xsum != nullptr)) return BQ_EINVAL;
+    // inputs of the op
+    if (op != BQ_OP_NORM && !b) return BQ_EINVAL;
+    if (op >= BQ_OP_RESID && !c) return BQ_EINVAL;
+    if (op == BQ_OP_SILU && !d) return BQ_EINVAL;
+    if (out && (out == a || out == b)) return BQ_EINVAL;  // read by every workgroup
+    const int K = ws[0]->K;
+    const uint32_t type = ws[0]->ggml_type;
+    const bool q6rep = type == BQ_TYPE_Q6_K && ws[0]->rep;
+    PartTable pt;
+    memset(&pt, 0, sizeof(pt));
+    for (int p = 0; p < nparts; ++p) {
+        const bq_weight* w = ws[p];
+        if (!weight_ok(w) || !ys[p]) return BQ_EINVAL;
+        if (w->K != K || w->ggml_type != type) return BQ_UNSUPPORTED;
+        if (type == BQ_TYPE_Q5_K) {
+            if (!w->raw) return BQ_UNSUPPORTED;
+            pt.W[p] = w->raw;
+        } else if (type == BQ_TYPE_Q6_K) {
+            if ((w->rep != nullptr) != q6rep || (!q6rep && !w->raw)) return BQ_UNSUPPORTED;
+            pt.W[p] = q6rep ? w->rep : w->raw;
+        } else {
+            return BQ_UNSUPPORTED;
+        }
+        pt.Y[p] = ys[p];
+        pt.N[p] = w->N;
+    }
+    pt.nparts = nparts;
+    if (!gemv_producer_supported(K)) return BQ_UNSUPPORTED;
+    const float* in[4] = {a, b, c, d};
+    for (const float* q : in)
+        if ((uintptr_t)q % 16) return BQ_EINVAL;
+    if ((uintptr_t)out % 16 || (uintptr_t)xq % 16) return BQ_EINVAL;
+    const GemvKind kind = type == BQ_TYPE_Q5_K ? GemvKind::Q5K : (q6rep ? GemvKind::Q6KRep : GemvKind::Q6KRaw);
+    return from_hip(launch_gemv_producer(kind, pt, K, op, out, a, op != BQ_OP_NORM ? b : nullptr,
+                                         op >= BQ_OP_RESID ? c : nullptr, op == BQ_OP_SILU ? d : nullptr, xq, xd,
+                                         xsum, (hipStream_t)st));
+}
+
 int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
                const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
                bq_stream_t st) {

@@ -126,6 +126,51 @@ BQ_DEV void q8_quant16(const f32x4 (&v)[4], uint32_t (&q)[4], float& d, int& s) 
     s = acc + __builtin_amdgcn_mov_dpp(acc, 0xB1, 0xF, 0xF, false);
 }
 
+// Row L2 norm helpers shared by the q8 producers and the producer-fused
+// GEMV (one definition, so both produce identical bits).
+constexpr float kEpsL2 = 1e-6f;
+
+// l2_scale (bruce.cu:305-307), IEEE division and square root
+BQ_DEV float l2_scale(float ss, int n) {
+    return (1.0f / sqrtf(ss / (float)n + kEpsL2 / (float)n)) * (1.0f / sqrtf((float)n));
+}
+
+// Workgroup sum of one (X = 1) or two (X = 2) floats; every thread gets the totals.
+template <int X>
+BQ_DEV void block_sum(float (&v)[X], float* red) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+    for (int i = 0; i < X; ++i) v[i] = wave_sum(v[i]);
+    __syncthreads();  // red may still be read by a previous reduction
+    if (lane == 0)
+#pragma unroll
+        for (int i = 0; i < X; ++i) red[i * 16 + w] = v[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < X; ++i) {
+        float t = 0.f;
+        for (int k = 0; k < nw; ++k) t += red[i * 16 + k];
+        v[i] = t;
+    }
+}
+
+BQ_DEV float sigmoid_den(float x) { return 1.f + expf(-x); }
+
+// The elementwise parts of the q8 producers (one definition each, so the
+// standalone producers and the GEMV-fused ones compile to the same arithmetic).
+// gate: aout / (1 + exp(-gate*sg))  (k_gate_norm, bruce.cu:602)
+BQ_DEV float gate_div(float a, float gate, float sg) { return a / sigmoid_den(gate * sg); }
+// silu(g*sg) * u * su  (k_silu_mul_norm, bruce.cu:622)
+BQ_DEV float silu_mul(float g, float u, float sg, float su) {
+    const float gv = g * sg;
+    return (gv / sigmoid_den(gv)) * u * su;
+}
+// resid: a = x*ka, b = upd*kb, a + (b - a)*alpha  (k_resid, bruce.cu:571)
+BQ_DEV float resid_blend(float x, float ka, float u, float kb, float al) {
+    const float an = x * ka, bn = u * kb;
+    return an + (bn - an) * al;
+}
+
 // 6-bit scale and min of Q5_K sub-block j from the three scale words
 // (s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11]); GGUF layout:
 // j < 4: sc = s[j] & 63, m = s[j+4] & 63; j >= 4: low nibbles from s[j+4],

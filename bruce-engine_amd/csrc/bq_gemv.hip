@@ -279,15 +279,25 @@ BQ_DEV void dma_to_lds(uint8_t* lds, const void* src, int bytes, int wave, int w
 }
 
 // Fused-quantizer arguments: the fp32 activation row and optional q8 outputs
-// (written by workgroup 0 only; NULL = not written).
+// (written by workgroup 0 only; NULL = not written).  With a q8 producer
+// (QN == kQnProducer) x is the producer's first input, b/c/d the others (as
+// in bq_norm_q8 .. bq_silu_mul_norm_q8) and out (optional, workgroup 0)
+// receives the fp32 row the producer emits.
 struct FusedQ8 {
     const float* x;
     int8_t* xq;
     float* xd;
     int32_t* xsum;
+    int op = 0;             // NormOp of the producer
+    float* out = nullptr;
+    const float* b = nullptr;
+    const float* c = nullptr;
+    const float* d = nullptr;
 };
+constexpr int kQnProducer = -1;  // QN value of the producer-fused instances
 // fused quantizer limit: 16 waves x 3 chunks of 1024 values in registers
 constexpr int kFusedMaxK = kGemvMaxK;
+constexpr int kProducerMaxK = 16 * 1024;  // one 1024-value chunk per wave, 16 waves
 constexpr int kChunk = 1024;       // values one wave quantizes at a time (16 per lane)
 
 // Fused quantizer, part 1: issue the fp32 loads of this wave's chunks (chunk c
@@ -342,6 +352,134 @@ BQ_DEV void fq_quantize(const f32x4 (&xv)[QN][4], uint8_t* smem, int K, int wave
     BQ_WAIT_LGKM0();
 }
 
+// q8 producer fused into the GEMV (QN == kQnProducer): the row is cut into
+// 1024-value chunks, chunk c belongs to wave c (one chunk per wave, K <=
+// 16384) and lane l holds values 1024c + 16l .. +15 -- exactly the lane
+// layout of k_norm_q8 (bq_norm.hip) for one row of that length, whose thread
+// 64c + l holds the same 16 values and whose wave c is this wave.  The sums of
+// squares therefore follow the same order: per lane over the 16 values, the
+// same wave64 butterfly, then the per-wave totals in wave order; the
+// elementwise ops are the same shared functions.  The emitted row and its q8
+// codes are bit-identical to the standalone producer's.
+// Part 1: issue the loads of this wave's chunk (zeros outside the row).
+BQ_DEV void fp_load(f32x4 (&in)[4][4], const FusedQ8& fq, int K, int wave, int lane) {
+    const int v0 = wave * kChunk + 16 * lane;
+    const int op = fq.op;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) in[0][i] = in[1][i] = in[2][i] = in[3][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (v0 < K) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            in[0][i] = *(const f32x4*)(fq.x + v0 + 4 * i);
+            if (op != kOpNorm) in[1][i] = *(const f32x4*)(fq.b + v0 + 4 * i);
+            if (op >= kOpResid) in[2][i] = *(const f32x4*)(fq.c + v0 + 4 * i);
+            if (op == kOpSilu) in[3][i] = *(const f32x4*)(fq.d + v0 + 4 * i);
+        }
+    }
+}
+
+// Workgroup sum of per-wave values over the first nch waves, wave order.  Uses
+// only LDS waits and s_barrier (no wait on vector memory: the weight loads
+// stay in flight).  Every wave of the workgroup must call it.
+template <int X>
+BQ_DEV void chunk_sum(float (&v)[X], float* red, int wave, int lane, int nch) {
+#pragma unroll
+    for (int i = 0; i < X; ++i) v[i] = wave_sum(v[i]);
+    if (lane == 0 && wave < nch)
+#pragma unroll
+        for (int i = 0; i < X; ++i) red[i * 16 + wave] = v[i];
+    asm volatile("" ::: "memory");
+    BQ_WAIT_LGKM0();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < X; ++i) {
+        float t = 0.f;
+        for (int k = 0; k < nch; ++k) t += red[i * 16 + k];
+        v[i] = t;
+    }
+}
+
+// Part 2 (after the loads have returned): the producer's row, its L2 norm and
+// q8 codes into the LDS activation row (+ workgroup 0's optional outputs).
+// red: 48 floats of LDS.  Ends with the LDS writes complete.
+template <bool XS>
+BQ_DEV void fp_produce(const f32x4 (&in)[4][4], uint8_t* smem, float* red, int K, int wave, int lane,
+                       const FusedQ8& fq) {
+    const int op = fq.op, nch = (K + kChunk - 1) / kChunk;
+    const int v0 = wave * kChunk + 16 * lane;
+    f32x4 t[4];
+    if (op == kOpResid) {
+        float s2[2] = {0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                s2[0] += in[0][i][e] * in[0][i][e];
+                s2[1] += in[1][i][e] * in[1][i][e];
+            }
+        chunk_sum<2>(s2, red, wave, lane, nch);
+        const float ka = l2_scale(s2[0], K), kb = l2_scale(s2[1], K);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t[i][e] = resid_blend(in[0][i][e], ka, in[1][i][e], kb, in[2][i][e]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (op == kOpNorm) {
+                t[i] = in[0][i];
+            } else if (op == kOpAdd) {
+                t[i] = in[0][i] + in[1][i];
+            } else if (op == kOpGate) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) t[i][e] = gate_div(in[0][i][e], in[1][i][e], in[2][i][e]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) t[i][e] = silu_mul(in[0][i][e], in[1][i][e], in[2][i][e], in[3][i][e]);
+            }
+        }
+    }
+    float ss[1] = {0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss[0] += t[i][e] * t[i][e];
+    chunk_sum<1>(ss, red + 32, wave, lane, nch);
+    const float k = l2_scale(ss[0], K);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = t[i] * k;
+    uint32_t q[4];
+    float d;
+    int s;
+    q8_quant16(t, q, d, s);
+    if (v0 < K) {
+        uint8_t* lx = smem;
+        float* lxd = (float*)(smem + K);
+        int32_t* lxs = (int32_t*)(lxd + (K >> 5));
+        const int gi = v0 >> 5;
+        *(u32x4*)(lx + v0) = u32x4{q[0], q[1], q[2], q[3]};
+        if ((lane & 1) == 0) {
+            lxd[gi] = d;
+            if constexpr (XS) lxs[gi] = s;
+        }
+        if (blockIdx.x == 0) {
+            if (fq.out)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) *(f32x4*)(fq.out + v0 + 4 * i) = t[i];
+            if (fq.xq) {
+                *(u32x4*)(fq.xq + v0) = u32x4{q[0], q[1], q[2], q[3]};
+                if ((lane & 1) == 0) {
+                    fq.xd[gi] = d;
+                    fq.xsum[gi] = s;
+                }
+            }
+        }
+    }
+    asm volatile("" ::: "memory");
+    BQ_WAIT_LGKM0();
+}
+
 #ifdef BQ_EXP_TIMING
 // timing experiment: s_memrealtime stamps per wave of the last launch
 __device__ uint64_t g_tstamp[1 << 17];
@@ -368,6 +506,9 @@ extern "C" int bq_tstamp_copy(void* dst, size_t bytes) {
 // into 1024-value chunks, chunk c belongs to wave c % waves (QN = most chunks
 // of one wave); the fp32 loads are issued before the weight loads and the
 // codes go from registers into LDS.
+// QN == kQnProducer: the same with a q8 producer (norm / add / resid / gate /
+// silu*mul, then the row L2 norm) in front of the quantizer, one chunk per
+// wave (fp_load / fp_produce).
 // ---------------------------------------------------------------------------
 // K slices of a row of K values (ceil(K/1024) steps, at most 3 per wave)
 __host__ __device__ constexpr int ks_for(int K) { return ((K + 1023) / 1024 + 2) / 3; }
@@ -376,7 +517,7 @@ template <class F, int MR, int SPS, int QN, int LB, int KC = 0>
 __global__ void __launch_bounds__(LB)
 k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float* __restrict__ xd,
        const int32_t* __restrict__ xsum, FusedQ8 fq) {
-    static_assert(QN == 0 || MR == 1, "fused quantizer: one activation row");
+    static_assert(QN == 0 || MR == 1, "fused quantizer / producer: one activation row");
     // KC > 0: the row length (and so the K split and the 4-wave workgroup) is
     // a compile-time constant -- the decode shapes get their own instances
     const int K = KC ? KC : K_;
@@ -395,11 +536,14 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     float* part_sums = (float*)(smem + act_lds_bytes<F>(MR, K));  // [waves][MR][4]
     constexpr int QA = QN > 0 ? QN : 1;
     f32x4 xv[QA][4];
+    [[maybe_unused]] f32x4 pin[QN < 0 ? 4 : 1][4];
     // (BQ_EXP_NOSTAGE / BQ_EXP_NOCOMPUTE: timing experiments that skip the
     // activation staging / the dot products; results are meaningless)
 #ifndef BQ_EXP_NOSTAGE
     if constexpr (QN > 0) {
         fq_load<QA>(xv, fq.x, K, wave, waves, lane);
+    } else if constexpr (QN < 0) {
+        fp_load(pin, fq, K, wave, lane);
     } else {
         dma_to_lds(smem, xq, MR * K, wave, waves, lane);
         dma_to_lds(smem + MR * K, xd, MR * nb * 4, wave, waves, lane);
@@ -433,7 +577,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     // 10.3 -> 9.8 us, whole stack 1.008 -> 0.998 ms/token, interleaved A/B).
     // q8 staging (DMA of a row the previous kernel just wrote) stays ahead of
     // the weight loads.
-    constexpr bool kLate = QN > 0 && KC != 3072 && KC != 4096;
+    constexpr bool kLate = QN != 0 && KC != 3072 && KC != 4096;
     constexpr int kEarly = kLate ? 0 : SPS;  // steps whose loads go out before the staging wait
                                              // (issuing 1 or 2 of 3 early measured slower)
     auto issue_weights = [&](int s0, int s1) {
@@ -453,6 +597,8 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     BQ_TS(1);
 #ifndef BQ_EXP_NOSTAGE
     if constexpr (QN > 0) fq_quantize<QA, std::is_same<F, FmtQ5K>::value>(xv, smem, K, wave, waves, lane, fq);
+    if constexpr (QN < 0)
+        fp_produce<std::is_same<F, FmtQ5K>::value>(pin, smem, part_sums + waves * MR * 4, K, wave, lane, fq);
 #endif
     BQ_TS(2);
     __builtin_amdgcn_s_barrier();
@@ -575,8 +721,12 @@ static int gemv_waves(int KS, int MR) {
 template <class F, int MR, int SPS, int QN = 0>
 static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* xq, const float* xd,
                              const int32_t* xsum, hipStream_t st, FusedQ8 fq = {}) {
-    const int waves = gemv_waves(KS, MR), RT = waves / KS;
-    const size_t lds = act_lds_bytes<F>(MR, K) + (size_t)waves * MR * 4 * sizeof(float);
+    int waves = gemv_waves(KS, MR);
+    // the producer needs a wave per 1024-value chunk
+    if (QN < 0 && waves < (K + kChunk - 1) / kChunk) waves = 16;
+    const int RT = waves / KS;  // the kernel derives the same from blockDim
+    const size_t lds = act_lds_bytes<F>(MR, K) + (size_t)waves * MR * 4 * sizeof(float) +
+                       (QN != 0 ? 48 * sizeof(float) : 0);
     const int blocks = (pt.ntiles + RT - 1) / RT;
     // the launch-bounds class sets the compiler's occupancy target; the
     // single-row decode shapes run compile-time-K instances
@@ -695,6 +845,39 @@ static hipError_t dispatch_fused(const PartTable& pt, int K, const FusedQ8& fq, 
 }
 
 bool gemv_fused_supported(int K) { return K > 0 && K % 256 == 0 && K <= kFusedMaxK; }
+bool gemv_producer_supported(int K) { return K > 0 && K % 256 == 0 && K <= kProducerMaxK; }
+
+template <class F>
+static hipError_t dispatch_producer(const PartTable& pt, int K, const FusedQ8& fq, hipStream_t st) {
+    int KS, SPS;
+    k_split(K, sps_cap(KindOf<F>::v, K, (long long)pt.ntiles * kRowsPerTile, 1, true), KS, SPS);
+    switch (SPS) {
+        case 1: return launch_fmt<F, 1, 1, kQnProducer>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
+        case 2: return launch_fmt<F, 1, 2, kQnProducer>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
+        default: return launch_fmt<F, 1, 3, kQnProducer>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
+    }
+}
+
+// q8 producer (op) + GEMV of its one row, fused; out / xq.. optional
+hipError_t launch_gemv_producer(GemvKind kind, PartTable pt, int K, int op, float* out, const float* a,
+                                const float* b, const float* c, const float* d, int8_t* xq, float* xd,
+                                int32_t* xsum, hipStream_t st) {
+    if (!gemv_producer_supported(K)) return hipErrorInvalidValue;
+    build_tiles(pt);
+    if (pt.ntiles == 0)  // no weight rows: the producer's outputs are still written
+        return launch_norm_q8(op, out, a, b, c, d, 1, K, xq, xd, xsum, st);
+    FusedQ8 fq{a, xq, xd, xsum};
+    fq.op = op;
+    fq.out = out;
+    fq.b = b;
+    fq.c = c;
+    fq.d = d;
+    switch (kind) {
+        case GemvKind::Q5K: return dispatch_producer<FmtQ5K>(pt, K, fq, st);
+        case GemvKind::Q6KRaw: return dispatch_producer<FmtQ6KRaw>(pt, K, fq, st);
+        default: return dispatch_producer<FmtQ6KRep>(pt, K, fq, st);
+    }
+}
 
 // one fp32 activation row x[K], quantized inside the GEMV; q8 outputs optional
 hipError_t launch_gemv_fused_q8(GemvKind kind, PartTable pt, int K, const float* x, int8_t* xq,

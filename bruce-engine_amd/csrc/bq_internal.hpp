@@ -54,6 +54,14 @@ void gemv_set_cus(int cus);
 bool gemv_fused_supported(int K);
 hipError_t launch_gemv_fused_q8(GemvKind kind, PartTable pt, int K, const float* x, int8_t* xq,
                                 float* xd, int32_t* xsum, hipStream_t st);
+// q8 producer (op as launch_norm_q8, K % 256 == 0, K <= 16384) + GEMV of the
+// produced row in one launch; out (the emitted fp32 row) and xq/xd/xsum are
+// optional outputs written by workgroup 0.  Bit-identical to launch_norm_q8
+// followed by launch_gemv_fused_q8 on its fp32 output.
+bool gemv_producer_supported(int K);
+hipError_t launch_gemv_producer(GemvKind kind, PartTable pt, int K, int op, float* out, const float* a,
+                                const float* b, const float* c, const float* d, int8_t* xq, float* xd,
+                                int32_t* xsum, hipStream_t st);
 size_t gemv_lds_bytes(GemvKind kind, int rows, int K);
 hipError_t launch_gemv(GemvKind kind, PartTable pt, int rows, int K, const int8_t* xq,
                        const float* xd, const int32_t* xsum, hipStream_t st);
@@ -78,6 +86,7 @@ hipError_t launch_gemv_q8s(const void* W, int K, int N, int rows, const int8_t* 
 
 // q8 producers: elementwise op -> L2 norm -> q8 (op: 0 norm, 1 add, 2 resid,
 // 3 gate, 4 silu*mul); n % 32 == 0, n <= kNormMaxN
+enum NormOp { kOpNorm = 0, kOpAdd = 1, kOpResid = 2, kOpGate = 3, kOpSilu = 4 };
 constexpr int kNormMaxN = 32768;
 hipError_t launch_norm_q8(int op, float* out, const float* a, const float* b, const float* c,
                           const float* d, int rows, int n, int8_t* xq, float* xd, int32_t* xsum,

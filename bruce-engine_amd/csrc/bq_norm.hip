@@ -28,7 +28,6 @@
 
 namespace bq {
 
-enum NormOp { kOpNorm = 0, kOpAdd = 1, kOpResid = 2, kOpGate = 3, kOpSilu = 4 };
 
 struct NormArgs {
     float* out;          // fp32 output rows (NULL: not written); for Add/Resid this is x
@@ -41,34 +40,6 @@ struct NormArgs {
     int32_t* xsum;
     int n;
 };
-
-constexpr float kEpsL2 = 1e-6f;
-
-// l2_scale (bruce.cu:305-307), IEEE division and square root
-BQ_DEV float l2_scale(float ss, int n) {
-    return (1.0f / sqrtf(ss / (float)n + kEpsL2 / (float)n)) * (1.0f / sqrtf((float)n));
-}
-
-// Workgroup sum of one (X = 1) or two (X = 2) floats; every thread gets the totals.
-template <int X>
-BQ_DEV void block_sum(float (&v)[X], float* red) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-#pragma unroll
-    for (int i = 0; i < X; ++i) v[i] = wave_sum(v[i]);
-    __syncthreads();  // red may still be read by a previous reduction
-    if (lane == 0)
-#pragma unroll
-        for (int i = 0; i < X; ++i) red[i * 16 + w] = v[i];
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < X; ++i) {
-        float t = 0.f;
-        for (int k = 0; k < nw; ++k) t += red[i * 16 + k];
-        v[i] = t;
-    }
-}
-
-BQ_DEV float sigmoid_den(float x) { return 1.f + expf(-x); }
 
 template <int OP, int CH>
 __global__ void __launch_bounds__(1024) k_norm_q8(NormArgs p) {
@@ -110,8 +81,7 @@ __global__ void __launch_bounds__(1024) k_norm_q8(NormArgs p) {
                 if (i0 < n) al = *(const f32x4*)(p.c + i0 + 4 * i);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float an = xa[c][i][e] * ka, bn = ub[c][i][e] * kb;
-                    const float v = an + (bn - an) * al[e];
+                    const float v = resid_blend(xa[c][i][e], ka, ub[c][i][e], kb, al[e]);
                     t[c][i][e] = v;
                     ss[0] += v * v;
                 }
@@ -134,16 +104,13 @@ __global__ void __launch_bounds__(1024) k_norm_q8(NormArgs p) {
                         const f32x4 gt = *(const f32x4*)(p.b + ro + i0 + 4 * i);
                         const f32x4 sg = *(const f32x4*)(p.c + i0 + 4 * i);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v[e] = a[e] / sigmoid_den(gt[e] * sg[e]);
+                        for (int e = 0; e < 4; ++e) v[e] = gate_div(a[e], gt[e], sg[e]);
                     } else {  // kOpSilu
                         const f32x4 u = *(const f32x4*)(p.b + ro + i0 + 4 * i);
                         const f32x4 sg = *(const f32x4*)(p.c + i0 + 4 * i);
                         const f32x4 su = *(const f32x4*)(p.d + i0 + 4 * i);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const float gv = a[e] * sg[e];
-                            v[e] = (gv / sigmoid_den(gv)) * u[e] * su[e];
-                        }
+                        for (int e = 0; e < 4; ++e) v[e] = silu_mul(a[e], u[e], sg[e], su[e]);
                     }
                 }
                 t[c][i] = v;

@@ -142,6 +142,33 @@ int bq_gemm_q6k_raw(float* y, const bq_weight* w, int rows, const int8_t* xq, co
 int bq_gemv_q8_fused(float* const* ys, const bq_weight* const* ws, int nparts, const float* x,
                      int8_t* xq, float* xd, int32_t* xsum, bq_stream_t st);
 
+/* q8 producer + GEMV of the produced row in one launch: one of the q8
+ * producers above (op: BQ_OP_NORM, BQ_OP_ADD, BQ_OP_RESID, BQ_OP_GATE,
+ * BQ_OP_SILU with the inputs a, b, c, d in the order of bq_norm_q8 ..
+ * bq_silu_mul_norm_q8: norm a; add a, h=b; resid x=a, upd=b, alpha=c; gate
+ * aout=a, gate=b, sg=c; silu g=a, u=b, sg=c, su=d) computed by every
+ * workgroup for the one activation row, quantized and consumed by the GEMV
+ * over nparts (1..4) matrices sharing K (types as bq_gemv_q8_fused).
+ * Replaces the decode pair "q8 producer, then GEMV" of the reference --
+ * e.g. k_silu_mul_norm (bruce.cu:622) + launch_gemv (:5624) for the down
+ * projection, k_resid (:571) + launch_verify_fused (:7141) for gate+up, k_gate_norm
+ * (:602) + launch_gemv for the O projection -- with one launch.
+ * out (optional) receives the producer's fp32 row (the new x for add /
+ * resid: the reference updates x in place, here out must not be a or b,
+ * which every workgroup reads; BQ_EINVAL otherwise); xq/xd/xsum (all or
+ * none) its q8 row.  ys, out and the q8 row are bit-identical to the
+ * standalone producer followed by bq_gemv_q8_fused on its fp32 output.
+ * K % 256 == 0 and K <= 16384, else BQ_UNSUPPORTED.  An extension of this
+ * library: the reference has no fused form. */
+#define BQ_OP_NORM 0
+#define BQ_OP_ADD 1
+#define BQ_OP_RESID 2
+#define BQ_OP_GATE 3
+#define BQ_OP_SILU 4
+int bq_gemv_norm_fused(float* const* ys, const bq_weight* const* ws, int nparts, int op, float* out,
+                       const float* a, const float* b, const float* c, const float* d, int8_t* xq,
+                       float* xd, int32_t* xsum, bq_stream_t st);
+
 /* ---- prefill GEMM ----------------------------------------------------------
  * Y_p[M][N_p] for nparts (1..4) Q5_K matrices, 128x128 tiles on int8 MFMA.
  * Replaces try_launch_mmq (bruce.cu:7366-7419).  rows >= 96 (the reference's
