@@ -31,6 +31,14 @@
 namespace bq {
 
 constexpr int kRowsPerTile = 4;    // one row per 16-lane DPP row
+// Q5_K multi-row: dot products on the matrix cores from this many activation
+// rows up.  The matrix-core lane map (4 lanes = one task across the 4 rows)
+// loses the address merging of the per-block header / qh loads that the
+// dot4 map gets (4 lanes of one row read the same 16 bytes), measured at
+// +0.8 us for 2..4 rows with dot4 arithmetic on the new map; from 6 rows the
+// faster arithmetic wins (9216 x 3072: 6 / 7 / 8 rows 10.5 / 11.7 / 13.0 ->
+// 10.3 / 10.9 / 11.5 us).
+constexpr int kQ5kMfmaMinRows = 6;
 constexpr int kTasksPerStep = 16;  // tasks of one row per step
 
 BQ_DEV int find_part(const PartTable& pt, int tile) {
@@ -139,6 +147,72 @@ struct FmtQ5K {
         }
     }
 };
+
+// Multi-row dot products of FmtQ5K on the matrix cores: v_mfma_i32_4x4x4i8
+// runs 16 independent 4x4x4 blocks per instruction; block b (lanes 4b..4b+3)
+// gives C[i][j] = sum_k A(lane 4b+i)[k] * B(lane 4b+j)[k] and lane 4b+j holds
+// C[0..3][j] (measured on gfx950).  With the multi-row lane map (lane = 4 *
+// task + row, kMmLanes) block b is one task across the wave's 4 weight rows:
+// lane 4b+r feeds weight row r's code dword as B and activation row 4ms+r's
+// dword as A, so after 8 instructions per 32-value sub-block the lane holds
+// the exact integer dots of its weight row with activation rows 4ms..4ms+3.
+// The float epilogue is the dot4 path's expression, term for term.
+template <int MR>
+BQ_DEV void q5k_dot_mm(const FmtQ5K::Task& a, int t, const ActLds& act, int K, float (&acc)[MR], int lane) {
+    const int jp = t & 3, j0 = 2 * jp, j1 = j0 + 1;
+    const uint32_t sm = FmtQ5K::scale_min4(a.hdr, jp);
+    const float d = h2f(a.hdr.x & 0xFFFF), dmin = h2f(a.hdr.x >> 16);
+    const float ds0 = d * (float)(sm & 0xFF), ds1 = d * (float)((sm >> 8) & 0xFF);
+    const float dm0 = dmin * (float)((sm >> 16) & 0xFF), dm1 = dmin * (float)(sm >> 24);
+    uint32_t u0[8], u1[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        u0[i] = q5_codes(a.qs0[i], a.qh0[i], j0, false);
+        u0[i + 4] = q5_codes(a.qs1[i], a.qh1[i], j0, false);
+        u1[i] = q5_codes(a.qs0[i], a.qh0[i], j1, true);
+        u1[i + 4] = q5_codes(a.qs1[i], a.qh1[i], j1, true);
+    }
+    const int nb = K >> 5;
+    const int g0 = (t >> 2) * 8 + j0;
+    const int r = lane & 3;
+#pragma unroll
+    for (int ms = 0; ms < (MR + 3) / 4; ++ms) {
+        const int m = 4 * ms + r;  // activation row fed as A by this lane
+        const int8_t* xp = act.x + (m < MR ? m : MR - 1) * K + 32 * g0;
+        u32x4 x0 = *(const u32x4*)(xp), x1 = *(const u32x4*)(xp + 16);
+        u32x4 x2 = *(const u32x4*)(xp + 32), x3 = *(const u32x4*)(xp + 48);
+        // one accumulator chain per sub-block (split chains measured slower)
+        i32x4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int xa = (int)(k < 4 ? x0[k] : x1[k - 4]), xb = (int)(k < 4 ? x2[k] : x3[k - 4]);
+            c0 = __builtin_amdgcn_mfma_i32_4x4x4i8(xa, (int)u0[k], c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_i32_4x4x4i8(xb, (int)u1[k], c1, 0, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int mm = 4 * ms + q;
+            if (mm < MR) {
+                const float2 xdv = *(const float2*)(act.xd + mm * nb + g0);
+                const int2 xsv = *(const int2*)(act.xs + mm * nb + g0);
+                acc[mm] += xdv.x * (ds0 * (float)c0[q] - dm0 * (float)xsv.x) +
+                           xdv.y * (ds1 * (float)c1[q] - dm1 * (float)xsv.y);
+            }
+        }
+    }
+}
+
+// sum over the 16 lanes 4i + (lane & 3): the row16_sum scan (shift 1, 2, 4,
+// 8 tasks, zero below the first) on the multi-row lane map; lanes 60..63 end
+// with the totals, in the same association as row16_sum
+BQ_DEV float lane4_sum(float v, int li) {
+#pragma unroll
+    for (int sh = 1; sh < 16; sh <<= 1) {
+        const float u = __shfl_up(v, 4 * sh, 64);
+        v += li >= sh ? u : 0.f;
+    }
+    return v;
+}
 
 struct FmtQ6KRep {
     static constexpr int kLoads = 5;
@@ -523,7 +597,11 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     const int K = KC ? KC : K_;
     const int KS = KC ? ks_for(KC) : KS_;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
+    // multi-row Q5_K from kQ5kMfmaMinRows rows: dot products on the matrix
+    // cores, lane = 4 * task + row
+    constexpr bool kMmLanes = MR >= kQ5kMfmaMinRows && std::is_same<F, FmtQ5K>::value;
+    const int lane = threadIdx.x & 63;
+    const int g = kMmLanes ? (lane & 3) : (lane >> 4), li = kMmLanes ? (lane >> 2) : (lane & 15);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
     const int waves = KC ? 4 : blockDim.x >> 6;
     const int nb = K >> 5;
@@ -617,7 +695,19 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
 #ifdef BQ_EXP_NOCOMPUTE
         if (rowok && t < tpr) acc[0] += as_float(((const uint32_t*)&w[s])[0] & 0x3F800000u);
 #else
-        if (rowok && t < tpr) F::template dot<MR>(w[s], rowp, t, act, K, acc);
+        if constexpr (kMmLanes) {
+            // every lane of the block takes part in the matrix instruction;
+            // the lane's own contribution is dropped afterwards if not valid
+            float tmp[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) tmp[m] = 0.f;
+            if constexpr (std::is_same<F, FmtQ5K>::value) q5k_dot_mm<MR>(w[s], min(t, tpr - 1), act, K, tmp, lane);
+            if (rowok && t < tpr)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) acc[m] += tmp[m];
+        } else {
+            if (rowok && t < tpr) F::template dot<MR>(w[s], rowp, t, act, K, acc);
+        }
 #endif
         if (s == 0) BQ_TS(6);
     }
@@ -627,7 +717,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     if (KS == 1) {
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            const float v = row16_sum(acc[m]);
+            const float v = kMmLanes ? lane4_sum(acc[m], li) : row16_sum(acc[m]);
             if (li == 15 && rowok) Y[(size_t)m * Nloc + row] = v;
         }
         BQ_TS(5);
@@ -635,7 +725,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
-        const float v = row16_sum(acc[m]);
+        const float v = kMmLanes ? lane4_sum(acc[m], li) : row16_sum(acc[m]);
         if (li == 15) part_sums[(wave * MR + m) * 4 + g] = v;
     }
     __syncthreads();
