@@ -39,6 +39,20 @@ constexpr int kRowsPerTile = 4;    // one row per 16-lane DPP row
 // faster arithmetic wins (9216 x 3072: 6 / 7 / 8 rows 10.5 / 11.7 / 13.0 ->
 // 10.3 / 10.9 / 11.5 us).
 constexpr int kQ5kMfmaMinRows = 6;
+// Q6_K (W160 and raw) from 3 rows: no per-block header is shared between the
+// lanes of a row there (W160), or only 2 of 8 loads (raw), and the dot4 path
+// needs two dot4 per dword for the -32 offset (raw).  Measured 3072 x 9216,
+// rows 3 / 4 / 8: W160 11.5 / 12.7 / 17.1 -> 11.0 / 11.7 / 14.8 us, raw
+// 10.0 / 11.2 / 16.1 -> 9.8 / 10.5 / 13.9 us; at 2 rows equal (W160) or
+// slower (raw 8.7 -> 9.2).
+#ifndef BQ_Q6REP_MFMA_MIN_ROWS
+#define BQ_Q6REP_MFMA_MIN_ROWS 3
+#endif
+constexpr int kQ6RepMfmaMinRows = BQ_Q6REP_MFMA_MIN_ROWS;
+#ifndef BQ_Q6RAW_MFMA_MIN_ROWS
+#define BQ_Q6RAW_MFMA_MIN_ROWS 3
+#endif
+constexpr int kQ6RawMfmaMinRows = BQ_Q6RAW_MFMA_MIN_ROWS;
 constexpr int kTasksPerStep = 16;  // tasks of one row per step
 
 BQ_DEV int find_part(const PartTable& pt, int tile) {
@@ -246,6 +260,38 @@ struct FmtQ6KRep {
     }
 };
 
+// Multi-row dot products of FmtQ6KRep (W160: signed codes q-32, one fp32
+// scale per 16 values) on v_mfma_i32_4x4x4i8, with the lane map and block
+// layout of q5k_dot_mm: per 16-value group 4 instructions into one
+// accumulator; the float epilogue is FmtQ6KRep::dot's expression.
+template <int MR>
+BQ_DEV void q6rep_dot_mm(const FmtQ6KRep::Task& a, int t, const ActLds& act, int K, float (&acc)[MR], int lane) {
+    const int k0 = 64 * t, nb = K >> 5;
+    const int r = lane & 3;
+#pragma unroll
+    for (int ms = 0; ms < (MR + 3) / 4; ++ms) {
+        const int m = 4 * ms + r;  // activation row fed as A by this lane
+        const int8_t* xp = act.x + (m < MR ? m : MR - 1) * K + k0;
+        i32x4 c[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const u32x4 x = *(const u32x4*)(xp + 16 * g);
+            c[g] = i32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) c[g] = __builtin_amdgcn_mfma_i32_4x4x4i8((int)x[i], (int)a.c[g][i], c[g], 0, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int mm = 4 * ms + q;
+            if (mm < MR) {
+                const float2 xdv = *(const float2*)(act.xd + mm * nb + (k0 >> 5));
+                acc[mm] += xdv.x * (a.sc.x * (float)c[0][q] + a.sc.y * (float)c[1][q]) +
+                           xdv.y * (a.sc.z * (float)c[2][q] + a.sc.w * (float)c[3][q]);
+            }
+        }
+    }
+}
+
 // round a pointer down to 4 bytes, keeping it a (global) pointer
 BQ_DEV const uint8_t* align4(const uint8_t* p) { return p - ((uintptr_t)p & 3); }
 
@@ -323,6 +369,61 @@ struct FmtQ6KRaw {
                 v += act.xd[m * nb + (k >> 5)] * sc[u] * (float)s;
             }
             acc[m] += v;
+        }
+    }
+    // the same on v_mfma_i32_4x4x4i8 (block layout of q5k_dot_mm): the codes
+    // become signed q - 32 per byte, ((q | 0x80) - 0x20) ^ 0x80 with no
+    // carry between bytes, then 4 instructions per 16-value quarter
+    template <int MR>
+    static BQ_DEV void dot_mm(const Task& a, const uint8_t* row, int t, const ActLds& act, int K, float (&acc)[MR],
+                              int lane) {
+        const int h = (t >> 1) & 1, l0 = 16 * (t & 1);
+        const uint8_t* blk = row + (t >> 2) * kQ6Bytes;
+        const uint32_t sh = (uint32_t)(uintptr_t)blk & 2;
+        const u32x4 qlA = shift16(a.qlA, a.qlA4, sh), qlB = shift16(a.qlB, a.qlB4, sh);
+        const u32x4 qh = shift16(a.qh, a.qh4, sh);
+        const uint32_t s0 = sh ? __builtin_amdgcn_alignbyte(a.sc[1], a.sc[0], 2) : a.sc[1];
+        const uint32_t s1 = sh ? __builtin_amdgcn_alignbyte(a.sc[2], a.sc[1], 2) : a.sc[2];
+        const float d = h2f(a.d);
+        float sc[4];
+        uint32_t q[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int gi = 2 * u + (l0 >> 4);
+            const uint32_t w = gi < 4 ? s0 : s1;
+            sc[u] = d * (float)(int8_t)(w >> (8 * (gi & 3)));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ql = (u & 1) ? qlB[i] : qlA[i];
+                const uint32_t nib = ((u >= 2) ? (ql >> 4) : ql) & 0x0F0F0F0Fu;
+                const uint32_t code = nib | (((qh[i] >> (2 * u)) & 0x03030303u) << 4);
+                q[u][i] = ((code | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+            }
+        }
+        const int kb = (t >> 2) * 256 + 128 * h + l0, nb = K >> 5;
+        const int r = lane & 3;
+#pragma unroll
+        for (int ms = 0; ms < (MR + 3) / 4; ++ms) {
+            const int m = 4 * ms + r;
+            const int8_t* xp = act.x + (m < MR ? m : MR - 1) * K + kb;
+            i32x4 c[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const u32x4 x = *(const u32x4*)(xp + 32 * u);
+                c[u] = i32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) c[u] = __builtin_amdgcn_mfma_i32_4x4x4i8((int)x[i], (int)q[u][i], c[u], 0, 0, 0);
+            }
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+                const int mm = 4 * ms + qq;
+                if (mm < MR) {
+                    float v = 0.f;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) v += act.xd[mm * nb + ((kb + 32 * u) >> 5)] * sc[u] * (float)c[u][qq];
+                    acc[mm] += v;
+                }
+            }
         }
     }
 };
@@ -599,7 +700,9 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // multi-row Q5_K from kQ5kMfmaMinRows rows: dot products on the matrix
     // cores, lane = 4 * task + row
-    constexpr bool kMmLanes = MR >= kQ5kMfmaMinRows && std::is_same<F, FmtQ5K>::value;
+    constexpr bool kMmLanes = (MR >= kQ5kMfmaMinRows && std::is_same<F, FmtQ5K>::value) ||
+                              (MR >= kQ6RepMfmaMinRows && std::is_same<F, FmtQ6KRep>::value) ||
+                              (MR >= kQ6RawMfmaMinRows && std::is_same<F, FmtQ6KRaw>::value);
     const int lane = threadIdx.x & 63;
     const int g = kMmLanes ? (lane & 3) : (lane >> 4), li = kMmLanes ? (lane >> 2) : (lane & 15);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
@@ -702,6 +805,10 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
 #pragma unroll
             for (int m = 0; m < MR; ++m) tmp[m] = 0.f;
             if constexpr (std::is_same<F, FmtQ5K>::value) q5k_dot_mm<MR>(w[s], min(t, tpr - 1), act, K, tmp, lane);
+            if constexpr (std::is_same<F, FmtQ6KRep>::value)
+                q6rep_dot_mm<MR>(w[s], min(t, tpr - 1), act, K, tmp, lane);
+            if constexpr (std::is_same<F, FmtQ6KRaw>::value)
+                FmtQ6KRaw::template dot_mm<MR>(w[s], rowp, min(t, tpr - 1), act, K, tmp, lane);
             if (rowok && t < tpr)
 #pragma unroll
                 for (int m = 0; m < MR; ++m) acc[m] += tmp[m];
