@@ -864,16 +864,22 @@ static void build_tiles(PartTable& pt, int rows_per_tile = kRowsPerTile) {
 
 // K split: ceil(K/1024) steps per row, at most `cap` per wave.  The cap
 // decides how many waves share a row (KS = steps / cap) and so the workgroup
-// shape; it is chosen per shape class from interleaved A/B measurements
-// (kernel durations, us):
+// shape and count.  It is chosen per shape class from interleaved sweeps of
+// caps 1 / 2 / 3 (kernel-event medians, us; N*K = weight values):
 //   fused quantize + GEMV: 3 (gate+up, QKV, O); K = 9216 (down): 2 (9.03 -> 8.47)
-//   Q6_K, 2..8 rows (3072 x 9216): 2 (8 rows: 29.1 -> 15.8 -- the 92 KB of
-//     staged activations per workgroup want more rows per workgroup); 1 row: 3
-//   Q5_K 1..2 rows: 1 if N*K >= 16M values (9216 x 3072: 5.91 -> 5.37), else 3
-//   Q5_K 3..4 rows: 1 (9216 x 3072, 4 rows: 8.24 -> 7.53)
-//   Q5_K 5..8 rows: 2 if N*K >= 16M values (8 rows 12.70 -> 12.42), else 1
+//   Q5_K, q8 input (9216 x 3072 = 28M, 18432 x 3072 = 57M, 3072 x 4096 = 12.6M):
+//     6..8 rows (matrix-core dots): 3 from 20M (28M, 8 rows 11.0 -> 9.6; 57M
+//       18.9 -> 14.6), else 1 (12.6M, 8 rows 8.9 -> 8.3)
+//     5 rows: 2 from 20M (9.65 / 9.63 -> 9.16), else 1 (7.0 -> 6.2)
+//     1..4 rows: 3 from 40M (57M: 1 row 9.4 -> 8.5, 2 rows 10.0 -> 9.4), else
+//       1 (28M, 4 rows 8.5 -> 7.8; 12.6M, 2 rows 5.2 -> 4.5; 5120 x 3072, 1
+//       row 5.15 -> 4.97); below 12M values 1..2 rows keep 3 (3072 x 3072 tie)
+//   Q6_K raw 3072 x 9216: 3 up to 5 rows (4 rows 10.6 -> 10.2), 2 from 6
+//     (8 rows 26.7 -> 13.9: the 92 KB of staged activations per workgroup
+//     want more rows per workgroup)
+//   Q6_K W160 3072 x 9216: 3 up to 2 rows (2 rows 10.2 -> 9.7), else 2
 // BQ_GEMV_SPS=1|2|3 overrides the cap (a dev A/B switch, read once).
-static int sps_cap(GemvKind kind, int K, long long N, int MR, bool fused) {
+int sps_cap(GemvKind kind, int K, long long N, int MR, bool fused) {
     static int env = -1;
     if (env < 0) {
         const char* e = getenv("BQ_GEMV_SPS");
@@ -881,14 +887,17 @@ static int sps_cap(GemvKind kind, int K, long long N, int MR, bool fused) {
     }
     if (env) return env;
     if (fused) return K > 4096 ? 2 : 3;
-    if (kind != GemvKind::Q5K) return MR == 1 ? 3 : 2;
-    const bool big = N * K >= (16ll << 20);
-    if (MR <= 2) return big ? 1 : 3;
-    if (MR <= 4) return 1;
-    return big ? 2 : 1;
+    if (kind == GemvKind::Q6KRaw) return MR <= 5 ? 3 : 2;
+    if (kind == GemvKind::Q6KRep) return MR <= 2 ? 3 : 2;
+    const long long nk = N * K;
+    if (MR >= kQ5kMfmaMinRows) return nk >= (20ll << 20) ? 3 : 1;
+    if (MR == 5) return nk >= (20ll << 20) ? 2 : 1;
+    if (nk >= (40ll << 20)) return 3;
+    if (nk < (12ll << 20) && MR <= 2) return 3;
+    return 1;
 }
 
-static void k_split(int K, int cap, int& KS, int& SPS) {
+void k_split(int K, int cap, int& KS, int& SPS) {
     const int spt = (K / 64 + kTasksPerStep - 1) / kTasksPerStep;
     cap = std::min(3, std::max(cap, (spt + 15) / 16));  // at most 16 slices (K <= 49152)
     KS = (spt + cap - 1) / cap;

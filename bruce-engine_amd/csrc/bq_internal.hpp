@@ -49,6 +49,10 @@ hipError_t launch_quant_q8(const float* x, int rows, int K, int8_t* xq, float* x
 hipError_t launch_fill_xdh(const float* xd, const int32_t* xsum, int n, uint16_t* xdh, hipStream_t st);
 
 void gemv_set_cus(int cus);
+// GEMV K split (bq_gemv.hip): steps per wave capped per shape class, then
+// KS = K slices per row and SPS = steps per slice
+int sps_cap(GemvKind kind, int K, long long N, int MR, bool fused);
+void k_split(int K, int cap, int& KS, int& SPS);
 // Fused quantize + GEMV of one fp32 activation row (K % 256 == 0, K <= 49152);
 // xq/xd/xsum receive the q8 row when xq != NULL.
 bool gemv_fused_supported(int K);
