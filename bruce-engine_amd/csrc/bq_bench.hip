@@ -297,6 +297,34 @@ int bqb_chain(int steps, int warmup, int nlayers, const bq_weight* w, const bq_w
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// Fused quantize + GEMV: `steps` launches of bq_gemv_q8_fused over nparts
+// matrices, weight set s = i % nsets (w = [nsets][nparts]); out[1] = sum of
+// the kernels' own durations (ms), out[0] = timed region.
+int bqb_gemv_fused(int steps, int warmup, int nsets, int nparts, const bq_weight* w, const float* x,
+                   float* const* ys, bq_stream_t st, double* out) {
+    auto launch = [&](int i) -> int {
+        const bq_weight* wp[4];
+        for (int p = 0; p < nparts; ++p) wp[p] = &w[(i % nsets) * nparts + p];
+        return bq_gemv_q8_fused(ys, wp, nparts, x, nullptr, nullptr, nullptr, st);
+    };
+    for (int i = 0; i < warmup; ++i)
+        if (int r = launch(i)) return r;
+    EventPool pool((size_t)steps * 2 + 2);
+    hipDeviceSynchronize();
+    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    for (int i = 0; i < steps; ++i) {
+        bq_time_next_launch(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
+        if (int r = launch(i)) return r;
+    }
+    hipEventRecord(pool.ev[1], (hipStream_t)st);
+    hipDeviceSynchronize();
+    out[0] = elapsed(pool.ev[0], pool.ev[1]);
+    double k = 0;
+    for (int i = 0; i < steps; ++i) k += elapsed(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
+    out[1] = k;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // Q8_0 logits head: `steps` launches of bq_gemv_q8s, weight copy s = i % nsets.
 // out[0] = timed region (ms), out[1] = sum of the kernels' own durations (ms).
 int bqb_q8s(int steps, int warmup, int nsets, const void* const* ws, int K, int N, int rows, const int8_t* xq,

@@ -866,7 +866,9 @@ static void build_tiles(PartTable& pt, int rows_per_tile = kRowsPerTile) {
 // decides how many waves share a row (KS = steps / cap) and so the workgroup
 // shape and count.  It is chosen per shape class from interleaved sweeps of
 // caps 1 / 2 / 3 (kernel-event medians, us; N*K = weight values):
-//   fused quantize + GEMV: 3 (gate+up, QKV, O); K = 9216 (down): 2 (9.03 -> 8.47)
+//   fused quantize + GEMV: K > 4096 (down 3072 x 9216): 2 (8.10 -> 7.83);
+//     else 3 from 20M values (gate+up 2 x 9216 x 3072: 12.07 -> 9.02), else
+//     1 (QKV 5120 x 3072: 5.66 -> 5.40; O 3072 x 4096: 4.84 -> 4.70)
 //   Q5_K, q8 input (9216 x 3072 = 28M, 18432 x 3072 = 57M, 3072 x 4096 = 12.6M):
 //     6..8 rows (matrix-core dots): 3 from 20M (28M, 8 rows 11.0 -> 9.6; 57M
 //       18.9 -> 14.6), else 1 (12.6M, 8 rows 8.9 -> 8.3)
@@ -886,7 +888,7 @@ int sps_cap(GemvKind kind, int K, long long N, int MR, bool fused) {
         env = e ? std::max(1, std::min(3, atoi(e))) : 0;
     }
     if (env) return env;
-    if (fused) return K > 4096 ? 2 : 3;
+    if (fused) return K > 4096 ? 2 : (N * K >= (20ll << 20) ? 3 : 1);
     if (kind == GemvKind::Q6KRaw) return MR <= 5 ? 3 : 2;
     if (kind == GemvKind::Q6KRep) return MR <= 2 ? 3 : 2;
     const long long nk = N * K;
@@ -1055,8 +1057,11 @@ bool gemv_producer_supported(int K) { return K > 0 && K % 256 == 0 && K <= kProd
 
 template <class F>
 static hipError_t dispatch_producer(const PartTable& pt, int K, const FusedQ8& fq, hipStream_t st) {
+    // every workgroup redoes the producer, so the split keeps the fewest
+    // workgroups (the fused quantizer's cap 1 for small GEMVs measured slower
+    // here: folded decode chain 1.51 -> 1.68 ms/token)
     int KS, SPS;
-    k_split(K, sps_cap(KindOf<F>::v, K, (long long)pt.ntiles * kRowsPerTile, 1, true), KS, SPS);
+    k_split(K, K > 4096 ? 2 : 3, KS, SPS);
     switch (SPS) {
         case 1: return launch_fmt<F, 1, 1, kQnProducer>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);
         case 2: return launch_fmt<F, 1, 2, kQnProducer>(pt, K, KS, nullptr, nullptr, nullptr, st, fq);

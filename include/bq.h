@@ -156,8 +156,10 @@ int bq_gemv_q8_fused(float* const* ys, const bq_weight* const* ws, int nparts, c
  * out (optional) receives the producer's fp32 row (the new x for add /
  * resid: the reference updates x in place, here out must not be a or b,
  * which every workgroup reads; BQ_EINVAL otherwise); xq/xd/xsum (all or
- * none) its q8 row.  ys, out and the q8 row are bit-identical to the
- * standalone producer followed by bq_gemv_q8_fused on its fp32 output.
+ * none) its q8 row.  out and the q8 row are bit-identical to the standalone
+ * producer's; ys equal bq_gemv_q8_fused on that fp32 row up to fp32
+ * summation order (the K split may differ: this path keeps the fewest
+ * workgroups, since each one recomputes the producer).
  * K % 256 == 0 and K <= 16384, else BQ_UNSUPPORTED.  An extension of this
  * library: the reference has no fused form. */
 #define BQ_OP_NORM 0

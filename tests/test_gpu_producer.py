@@ -3,9 +3,10 @@ silu*mul, then the row L2 norm and q8) and the GEMV of its row in one launch.
 
 Reference: the two launches it replaces -- the standalone producer
 (bq_*_q8, pinned against the oracle in test_gpu_norm.py) followed by
-bq_gemv_q8_fused on the producer's fp32 row.  The emitted fp32 row, its q8
-row and every GEMV output must be bit-identical to that pair; the GEMV output
-is also checked against the oracle on the q8 codes (normwise < 1e-4).
+bq_gemv_q8_fused on the producer's fp32 row.  The emitted fp32 row and its q8
+row must be bit-identical to that pair; the GEMV outputs agree to fp32
+summation order (normwise < 1e-6: the K split may differ) and are checked
+against the oracle on the q8 codes (normwise < 1e-4).
 """
 import numpy as np
 import pytest
@@ -86,8 +87,10 @@ def test_producer_gemv_matches_two_launches(bq, oracle, op, fmt, K, N, parts):
     assert np.array_equal(host(out).view(np.uint32), host(row1).view(np.uint32))
     for u, v in zip(q8a, q8b):
         assert np.array_equal(host(u), host(v))
+    # the GEMV may split K differently from bq_gemv_q8_fused (the producer
+    # path keeps the fewest workgroups): same terms, fp32 summation order
     for p in range(parts):
-        assert np.array_equal(host(y1[p]).view(np.uint32), host(y2[p]).view(np.uint32)), p
+        assert oracle.normwise_err(host(y2[p])[None], host(y1[p])[None]) < 1e-6, p
     # --- oracle on the q8 codes
     xq, xd, xs = (host(t).reshape(1, -1) for t in q8b)
     for p, (raw, _) in enumerate(W):
