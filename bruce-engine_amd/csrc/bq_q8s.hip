@@ -154,8 +154,13 @@ template <int M, int CPL>
 hipError_t launch_q8s_mc(const uint8_t* W, int K, int N, const int8_t* xq, const float* xd, const float* rs,
                          float* y, hipStream_t st) {
     // rows per wave iteration: enough 16-byte loads in flight per wave while
-    // the activation registers (M*CPL*5 VGPRs) grow with M
-    constexpr int R = M <= 2 ? 4 : (M <= 4 ? 2 : 1);
+    // the activation registers (M*CPL*5 VGPRs) grow with M.  At 7..8 rows the
+    // occupancy is 3 waves/SIMD either way and two rows per wave keep more
+    // bytes in flight (131072 x 3072: 7 / 8 rows 128 / 140 -> 121 / 131 us);
+    // at 5..6 rows two rows per wave cost occupancy (6 rows 102 -> 113 us).
+    // Activation rows in LDS instead of registers measured far slower (8 rows
+    // 221 us: the per-use LDS reads bound the kernel).
+    constexpr int R = M <= 2 ? 4 : (M <= 4 ? 2 : (M <= 6 ? 1 : 2));
     // persistent grid: as many workgroups as are resident at once, so no
     // partial second round of workgroups trails the stream
     static int per_cu = 0;
