@@ -876,10 +876,13 @@ static void build_tiles(PartTable& pt, int rows_per_tile = kRowsPerTile) {
 //     1..4 rows: 3 from 40M (57M: 1 row 9.4 -> 8.5, 2 rows 10.0 -> 9.4), else
 //       1 (28M, 4 rows 8.5 -> 7.8; 12.6M, 2 rows 5.2 -> 4.5; 5120 x 3072, 1
 //       row 5.15 -> 4.97); below 12M values 1..2 rows keep 3 (3072 x 3072 tie)
-//   Q6_K raw 3072 x 9216: 3 up to 5 rows (4 rows 10.6 -> 10.2), 2 from 6
-//     (8 rows 26.7 -> 13.9: the 92 KB of staged activations per workgroup
-//     want more rows per workgroup)
-//   Q6_K W160 3072 x 9216: 3 up to 2 rows (2 rows 10.2 -> 9.7), else 2
+//   Q6_K: 2 once rows * K staged activation bytes per workgroup are large
+//     (want several row tiles per workgroup), else 3:
+//     raw 3072 x 9216: 3 up to 5 rows (4 rows 10.6 -> 10.2), 2 from 6 rows
+//       (rows * K >= 48K; 8 rows 26.7 -> 13.9); 131072 x 3072 (the lm_head):
+//       3 for 2..8 rows (8 rows 115 -> 85), 1 row 2 (60.0 -> 57.5)
+//     W160 3072 x 9216: 3 up to 2 rows (2 rows 10.2 -> 9.7), else 2 (rows * K
+//       >= 27K); 131072 x 3072: 3 for all rows (8 rows 121.6 -> 99)
 // BQ_GEMV_SPS=1|2|3 overrides the cap (a dev A/B switch, read once).
 int sps_cap(GemvKind kind, int K, long long N, int MR, bool fused) {
     static int env = -1;
@@ -889,8 +892,9 @@ int sps_cap(GemvKind kind, int K, long long N, int MR, bool fused) {
     }
     if (env) return env;
     if (fused) return K > 4096 ? 2 : (N * K >= (20ll << 20) ? 3 : 1);
-    if (kind == GemvKind::Q6KRaw) return MR <= 5 ? 3 : 2;
-    if (kind == GemvKind::Q6KRep) return MR <= 2 ? 3 : 2;
+    // Q6_K: the staged activation bytes per workgroup (rows * K) decide
+    if (kind == GemvKind::Q6KRaw) return MR == 1 ? (K <= 4096 ? 2 : 3) : (MR * K >= 48 * 1024 ? 2 : 3);
+    if (kind == GemvKind::Q6KRep) return MR * K >= 3 * 9216 ? 2 : 3;
     const long long nk = N * K;
     if (MR >= kQ5kMfmaMinRows) return nk >= (20ll << 20) ? 3 : 1;
     if (MR == 5) return nk >= (20ll << 20) ? 2 : 1;
