@@ -31,6 +31,7 @@
 #include <algorithm>
 #include <new>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -140,6 +141,40 @@ struct bq_gguf {
             n -= (size_t)got;
             off += (uint64_t)got;
         }
+        return true;
+    }
+    // The same with the range split over up to kReadThreads threads (pread is
+    // position-independent): one thread copies page-cached data at ~20 GB/s,
+    // below what the pinned host-to-device copy of the chunk takes (330 MB
+    // streamed load: 1 / 2 / 4 / 8 threads 22 / 32 / 39 / 41 GB/s).  At most
+    // half the hardware threads are used.
+    static constexpr int kReadThreads = 8;
+    bool read_at_parallel(void* dst, size_t n, uint64_t off) const {
+        constexpr size_t kMinPiece = 4u << 20;
+        const int hw = std::max(1, (int)std::thread::hardware_concurrency() / 2);
+        const int nt = (int)std::min<size_t>(std::min(kReadThreads, hw), std::max<size_t>(1, n / kMinPiece));
+        if (nt == 1) return read_at(dst, n, off);
+        const size_t piece = (n / nt + 4095) & ~(size_t)4095;
+        bool ok[kReadThreads] = {};
+        std::thread th[kReadThreads - 1];
+        int started = 0;
+        for (int k = 1; k < nt; ++k) {
+            const size_t b = std::min(n, piece * k), e = std::min(n, piece * (k + 1));
+            try {
+                th[k - 1] = std::thread([this, &ok, k, dst, b, e, off] {
+                    ok[k] = read_at((uint8_t*)dst + b, e - b, off + b);
+                });
+                started = k;
+            } catch (...) {  // no thread: read that piece here
+                ok[k] = read_at((uint8_t*)dst + b, e - b, off + b);
+                started = k;
+            }
+        }
+        ok[0] = read_at(dst, std::min(n, piece), off);
+        for (int k = 1; k <= started; ++k)
+            if (th[k - 1].joinable()) th[k - 1].join();
+        for (int k = 0; k < nt; ++k)
+            if (!ok[k]) return false;
         return true;
     }
 
@@ -261,7 +296,7 @@ int stream_to_device(bq_gguf* g, uint64_t off, size_t n, uint8_t* dst, hipStream
     for (size_t done = 0; done < n; done += g->slot_bytes, s ^= 1) {
         const size_t len = std::min(g->slot_bytes, n - done);
         if (used[s] && hipEventSynchronize(g->done[s]) != hipSuccess) return -(int)hipErrorUnknown;
-        if (!g->read_at(g->slot[s], len, off + done)) return BQ_EINVAL;
+        if (!g->read_at_parallel(g->slot[s], len, off + done)) return BQ_EINVAL;
         if (hipMemcpyAsync(dst + done, g->slot[s], len, hipMemcpyHostToDevice, st) != hipSuccess ||
             hipEventRecord(g->done[s], st) != hipSuccess)
             return -(int)hipErrorUnknown;
