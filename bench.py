@@ -410,6 +410,37 @@ def main():
                 res[name] = {"ms": round(kms, 4), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)}
             gemm[f"M{M}"] = res
             del xm, mq, md, ms_, mh, ym
+        # prompt-batch tail (rows 9..95, bq_gemm_b: 8-row GEMV chunks or the
+        # MMQ tile) and the Q6_K GEMM (down projection over W160, M = 2048)
+        def ev_time(fn, n=20):
+            for _ in range(3):
+                fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(n):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / n
+        wp = bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF, rep=gw144, rep_min=gdm)
+        xt = torch.from_numpy(synth.gaussian(SEED + 9, (96, K))).cuda()
+        tq, td_, ts_, th = bq.quantize_q8(xt, with_xdh=True)
+        yt = torch.empty((96, FF), device="cuda")
+        tail = {}
+        for rows in (16, 32, 48, 64, 95):
+            tms = ev_time(lambda: bq.gemm_b(yt, wp, rows, tq, td_, ts_, th))
+            tail[f"rows{rows}"] = {"us": round(tms * 1e3, 1),
+                                   "tops": round(2.0 * rows * FF * K / (tms * 1e-3) / 1e12, 1)}
+        del xt, tq, td_, ts_, th, yt
+        w160 = bq.repack_q6k(g_down, FF, K)
+        wd6 = bq.make_weight(g_down, bq.TYPE_Q6_K, FF, K, rep=w160)
+        x6 = torch.from_numpy(synth.gaussian(SEED + 10, (2048, FF))).cuda()
+        q6q, q6d, _ = bq.quantize_q8(x6)
+        y6 = torch.empty((2048, K), device="cuda")
+        q6ms = ev_time(lambda: bq.gemm_q6k_mma(y6, wd6, 2048, q6q, q6d), n=10)
+        q6tops = 2.0 * 2048 * K * FF / (q6ms * 1e-3) / 1e12
+        del w160, x6, q6q, q6d, y6
         g = gemm["M2048"]["w144"]
         gemm_obj = {
             "config": "prefill GEMM Q5_K 9216x3072 (W144 repack, fp16 min term), M=2048 q8 tokens, fp32 out",
@@ -418,6 +449,10 @@ def main():
                          "frac": g["frac"], "traffic": traffic_for("mmq_w144_M2048"),
                          "kernel": "k_mmq_w144", "ops_per_launch": 2 * 2048 * FF * K},
             "shapes": gemm,
+            "tail_rows_bq_gemm_b": {"what": "Q5_K 9216x3072 W144, bq_gemm_b: 8-row GEMV chunks below 44 rows, "
+                                            "the 128-row MMQ tile from 44", **tail},
+            "q6k_down_M2048": {"what": "Q6_K 3072x9216 over W160 (k_mmq_q6k), M=2048", "ms": round(q6ms, 4),
+                               "tops": round(q6tops, 1), "frac": round(q6tops / INT8_PEAK_TOPS, 4)},
         }
 
         # ---------------------------------------------------------------- config 3 / config 1 GEMV

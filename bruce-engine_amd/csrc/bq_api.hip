@@ -45,6 +45,17 @@ int ensure_init() {
     return g_init_status;
 }
 
+// try_launch_mmq's row threshold (bruce.cu:7369: rows >= 96); BQ_MMQ_MIN_ROWS
+// overrides it (a dev A/B switch, read once)
+int mmq_min_rows() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("BQ_MMQ_MIN_ROWS");
+        v = e ? std::max(9, atoi(e)) : 96;
+    }
+    return v;
+}
+
 bool weight_ok(const bq_weight* w) { return w && w->K > 0 && w->N > 0 && (w->K % 256) == 0; }
 
 // Run a multi-row GEMV in row chunks that fit the per-block LDS limit.
@@ -283,11 +294,14 @@ int bq_gemv_norm_fused(float* const* ys, const bq_weight* const* ws, int nparts,
                                          xsum, (hipStream_t)st));
 }
 
-int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
-               const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
-               bq_stream_t st) {
-    if (int s = ensure_init()) return s;
-    if (nparts < 1 || nparts > BQ_MAX_PARTS || rows < 96) return BQ_UNSUPPORTED;
+namespace {
+// The MMQ launch behind bq_try_mmq and the bq_gemm_b dispatchers.  min_w144 /
+// min_raw: the smallest row count taken by the prepacked / raw tier (below
+// it BQ_UNSUPPORTED, nothing enqueued).
+int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int rows, const int8_t* xq,
+                 const float* xd, const int32_t* xsum, uint16_t* xdh, bq_stream_t st, int min_w144,
+                 int min_raw) {
+    if (nparts < 1 || nparts > BQ_MAX_PARTS || rows < std::min(min_w144, min_raw)) return BQ_UNSUPPORTED;
     if (!ys || !ws || !ws[0] || !xq || !xd || !xsum) return BQ_EINVAL;
     const int K = ws[0]->K;
     PartTable pt;
@@ -303,6 +317,7 @@ int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int row
     }
     if (K <= 0 || (K % 256) != 0) return BQ_UNSUPPORTED;
     if (prepacked && !xdh) prepacked = false;
+    if (rows < (prepacked ? min_w144 : min_raw)) return BQ_UNSUPPORTED;
     pt.nparts = nparts;
     hipStream_t s = (hipStream_t)st;
     if (prepacked) {
@@ -316,6 +331,22 @@ int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int row
     }
     for (int p = 0; p < nparts; ++p) pt.W[p] = ws[p]->raw;
     return from_hip(launch_mmq_q5k_raw(pt, rows, K, xq, xd, xsum, s));
+}
+
+// bq_gemm_b / bq_gemm_b_fused: one 128-row MMQ tile costs the same for any
+// row count up to 128 (9216 x 3072: 53 us prepacked, 64 us raw), while the
+// 8-row GEMV chunks stream the weights once per chunk (48 rows 57 us, 95 rows
+// 108 us): the tile wins from 44 rows prepacked and 56 rows raw.  (The
+// reference sends rows 9..95 to its 64x64 MMA tile.)
+constexpr int kGemmBMmqW144 = 44;
+constexpr int kGemmBMmqRaw = 56;
+}  // namespace
+
+int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
+               const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
+               bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    return try_mmq_impl(ys, ws, nparts, rows, xq, xd, xsum, xdh, st, mmq_min_rows(), mmq_min_rows());
 }
 
 int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
@@ -338,7 +369,8 @@ int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const fl
         if (q5) {
             float* ys[1] = {y};
             const bq_weight* wsp[1] = {w};
-            const int r = bq_try_mmq(ys, wsp, 1, rows, xq, xd, xsum, xdh, st);
+            const int r = try_mmq_impl(ys, wsp, 1, rows, xq, xd, xsum, xdh, st, std::min(kGemmBMmqW144, mmq_min_rows()),
+                                       std::min(kGemmBMmqRaw, mmq_min_rows()));
             if (r != BQ_UNSUPPORTED) return r;
         } else if (w->rep && (w->N % 128) == 0) {
             return bq_gemm_q6k_mma(y, w, rows, xq, xd, st);
@@ -368,7 +400,8 @@ int bq_gemm_b_fused(float* const* ys, const bq_weight* const* ws, int nparts, in
     if (int s = ensure_init()) return s;
     if (!ys || !ws || nparts < 1 || nparts > BQ_MAX_PARTS) return BQ_EINVAL;
     if (rows > BQ_MAX_ROWS) {
-        const int r = bq_try_mmq(ys, ws, nparts, rows, xq, xd, xsum, xdh, st);
+        const int r = try_mmq_impl(ys, ws, nparts, rows, xq, xd, xsum, xdh, st,
+                                   std::min(kGemmBMmqW144, mmq_min_rows()), std::min(kGemmBMmqRaw, mmq_min_rows()));
         if (r != BQ_UNSUPPORTED) return r;
     }
     for (int p = 0; p < nparts; ++p) {

@@ -189,13 +189,16 @@ int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, co
                     bq_stream_t st);
 
 /* Prompt-batch dispatcher.  Replaces launch_gemm_b (bruce.cu:7428-7568): rows
- * <= 8 -> the verify / GEMV kernels above; rows > 8 -> the MFMA GEMMs, else
- * 8-row chunks of the multi-row kernels.  Never returns BQ_UNSUPPORTED for a
- * Q5_K/Q6_K weight with K % 256 == 0. */
+ * <= 8 -> the verify / GEMV kernels above; Q5_K from 44 rows (W144 prepack)
+ * or 56 rows (raw) and Q6_K W160 above 8 rows -> the MFMA GEMMs (one 128-row
+ * tile costs the same at any row count up to 128, the 8-row chunks stream the
+ * weights once per chunk); otherwise 8-row chunks of the multi-row kernels.
+ * (The reference sends rows 9..95 to a 64x64 MMA tile.)  Never returns
+ * BQ_UNSUPPORTED for a Q5_K/Q6_K weight with K % 256 == 0. */
 int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
               const int32_t* xsum, uint16_t* xdh, bq_stream_t st);
 /* launch_gemm_b_fused (bruce.cu:7421-7426): one MMQ launch over the parts if
- * possible, otherwise bq_gemm_b per part. */
+ * possible (row thresholds of bq_gemm_b), otherwise bq_gemm_b per part. */
 int bq_gemm_b_fused(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
                     const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
                     bq_stream_t st);

@@ -450,8 +450,10 @@ def test_mmq_config4_full_slices(bq, oracle):
 
 
 # ---------------------------------------------------------------- dispatcher
-@pytest.mark.parametrize("rows", [3, 20, 130])
+@pytest.mark.parametrize("rows", [3, 20, 43, 47, 60, 130])
 def test_gemm_b_dispatch(bq, oracle, rows):
+    """bq_gemm_b: 8-row GEMV chunks below 44 rows (W144) / 56 rows (raw), the
+    MMQ tile from there; bq_try_mmq keeps the reference's rows >= 96."""
     import torch
     K, N = 1024, 256
     raw5 = weights(1400, N, K, "q5k")
@@ -464,6 +466,21 @@ def test_gemm_b_dispatch(bq, oracle, rows):
     bq.gemm_b(y, bq.make_weight(g5, bq.TYPE_Q5_K, K, N), rows, gq, gd, gs, xdh)
     torch.cuda.synchronize()
     assert oracle.normwise_err(host(y), oracle.gemm_q5k(raw5, xq, xd, xs)) < TOL
+    # prepacked: the W144 tile (fp16 min term) from 44 rows
+    w144, dm = bq.repack_q5k(g5, K, N)
+    yp = torch.full((rows, N), float("nan"), device="cuda")
+    bq.gemm_b(yp, bq.make_weight(g5, bq.TYPE_Q5_K, K, N, rep=w144, rep_min=dm), rows, gq, gd, gs, xdh)
+    torch.cuda.synchronize()
+    if rows >= 44:
+        r144, rdm = oracle.repack_q5k_144(raw5, K)
+        ref = oracle.gemm_q5k_144(r144, rdm, xq, xd, oracle.fill_xdh(xd, xs), N)
+    else:
+        ref = oracle.gemm_q5k(raw5, xq, xd, xs)
+    assert oracle.normwise_err(host(yp), ref) < TOL
+    if rows < 96:
+        yt = torch.empty((rows, N), device="cuda")
+        assert bq.try_mmq([yt], [bq.make_weight(g5, bq.TYPE_Q5_K, K, N, rep=w144, rep_min=dm)], rows,
+                          gq, gd, gs, xdh) == bq.BQ_UNSUPPORTED
     g6 = dev(raw6)
     y6 = torch.full((rows, N), float("nan"), device="cuda")
     bq.gemm_b(y6, bq.make_weight(g6, bq.TYPE_Q6_K, K, N, rep=bq.repack_q6k(g6, K, N)), rows, gq, gd, gs, xdh)
