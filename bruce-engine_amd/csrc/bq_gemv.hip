@@ -685,6 +685,11 @@ extern "C" int bq_tstamp_copy(void* dst, size_t bytes) {
 // silu*mul, then the row L2 norm) in front of the quantizer, one chunk per
 // wave (fp_load / fp_produce).
 // ---------------------------------------------------------------------------
+// BQ_GEMV_STEP_ORDER=0 builds the previous load order (a dev A/B switch)
+#ifndef BQ_GEMV_STEP_ORDER
+#define BQ_GEMV_STEP_ORDER 1
+#endif
+
 // K slices of a row of K values (ceil(K/1024) steps, at most 3 per wave)
 __host__ __device__ constexpr int ks_for(int K) { return ((K + 1023) / 1024 + 2) / 3; }
 
@@ -767,6 +772,11 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
             if (s < s0 || s >= s1) continue;
             const int t = (ks * SPS + s) * kTasksPerStep + li;
             F::load(w[s], rowp, min(t, tpr - 1));
+#if BQ_GEMV_STEP_ORDER
+            // keep the steps' loads in step order, so that step s waits only
+            // for its own loads (left alone, the scheduler interleaves them)
+            __builtin_amdgcn_sched_barrier(0);
+#endif
         }
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
