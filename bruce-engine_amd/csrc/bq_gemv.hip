@@ -685,6 +685,27 @@ extern "C" int bq_tstamp_copy(void* dst, size_t bytes) {
 // silu*mul, then the row L2 norm) in front of the quantizer, one chunk per
 // wave (fp_load / fp_produce).
 // ---------------------------------------------------------------------------
+// Wave priority during the activation staging: the staging loads of a wave
+// that starts late queue behind the weight loads other waves of the CU have
+// already issued (per-wave timestamps, fused gate+up: the fp32 row landed at
+// a median 3.75 us, p90 6.2 us, into a ~9 us kernel).  s_setprio(3) from the
+// staging loads through the quantization and the workgroup barrier lets them
+// win the issue arbitration; measured (kernel-event medians) gate+up 8.75 ->
+// 8.3-8.5 us, QKV 5.6 -> 5.2-5.4, O 5.0 -> 4.7-4.8, decode FFN step 17.66 ->
+// 17.12 us.  Raising it only around the loads (1) gained about half of that.
+// Large grids (several rounds of workgroups: the 131072-row lm_head at 2..8
+// rows) lose with it (54.9 -> 58.0 us at 2 rows), so the launch sets it only
+// up to kPrioMaxBlocks workgroups.  BQ_GEMV_PRIO=0|1|2 is a dev A/B switch.
+constexpr int kPrioMaxBlocks = 4096;
+#ifndef BQ_GEMV_PRIO
+#define BQ_GEMV_PRIO 2
+#endif
+// BQ_GEMV_LATE=0: the 9216-value fused rows also issue their weights before
+// the staging (measured slower: down 7.4 -> 8.0-8.2 us, with or without the
+// priority)
+#ifndef BQ_GEMV_LATE
+#define BQ_GEMV_LATE 1
+#endif
 // BQ_GEMV_STEP_ORDER=0 builds the previous load order (a dev A/B switch)
 #ifndef BQ_GEMV_STEP_ORDER
 #define BQ_GEMV_STEP_ORDER 1
@@ -725,6 +746,9 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     [[maybe_unused]] f32x4 pin[QN < 0 ? 4 : 1][4];
     // (BQ_EXP_NOSTAGE / BQ_EXP_NOCOMPUTE: timing experiments that skip the
     // activation staging / the dot products; results are meaningless)
+#if BQ_GEMV_PRIO
+    if (pt.prio) __builtin_amdgcn_s_setprio(3);
+#endif
 #ifndef BQ_EXP_NOSTAGE
     if constexpr (QN > 0) {
         fq_load<QA>(xv, fq.x, K, wave, waves, lane);
@@ -739,6 +763,9 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
 #endif
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
+#if BQ_GEMV_PRIO == 1
+    __builtin_amdgcn_s_setprio(0);
+#endif
 
     // ---- 2. this wave's weight loads, all issued now (addresses clamped so the
     //         instruction count is fixed; results of clamped lanes are unused)
@@ -763,7 +790,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     // 10.3 -> 9.8 us, whole stack 1.008 -> 0.998 ms/token, interleaved A/B).
     // q8 staging (DMA of a row the previous kernel just wrote) stays ahead of
     // the weight loads.
-    constexpr bool kLate = QN != 0 && KC != 3072 && KC != 4096;
+    constexpr bool kLate = QN != 0 && KC != 3072 && KC != 4096 && BQ_GEMV_LATE;
     constexpr int kEarly = kLate ? 0 : SPS;  // steps whose loads go out before the staging wait
                                              // (issuing 1 or 2 of 3 early measured slower)
     auto issue_weights = [&](int s0, int s1) {
@@ -794,6 +821,9 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     BQ_TS(2);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+#if BQ_GEMV_PRIO == 2
+    __builtin_amdgcn_s_setprio(0);
+#endif
     BQ_TS(3);
     if constexpr (kEarly < SPS) issue_weights(kEarly, SPS);
 
@@ -827,6 +857,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
         }
 #endif
         if (s == 0) BQ_TS(6);
+        if (s == 1) BQ_TS(7);
     }
     BQ_TS(4);
     // ---- 5. row sums; K slices combined through LDS
@@ -950,37 +981,39 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     const size_t lds = act_lds_bytes<F>(MR, K) + (size_t)waves * MR * 4 * sizeof(float) +
                        (QN != 0 ? 48 * sizeof(float) : 0);
     const int blocks = (pt.ntiles + RT - 1) / RT;
+    PartTable ptl = pt;
+    ptl.prio = blocks <= kPrioMaxBlocks;
     // the launch-bounds class sets the compiler's occupancy target; the
     // single-row decode shapes run compile-time-K instances
     if constexpr (SPS == 3 && (MR == 1 || QN == 0)) {
         if (waves == 4 && K == 3072 && KS == ks_for(K)) {
-            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072>), dim3(blocks), dim3(256), lds, st, pt, K, KS, xq, xd,
+            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
                           xsum, fq);
             return hipGetLastError();
         }
     }
     if constexpr (SPS == 3 && MR == 1) {
         if (waves == 4 && K == 9216 && KS == ks_for(K)) {
-            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 9216>), dim3(blocks), dim3(256), lds, st, pt, K, KS, xq, xd,
+            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 9216>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
                           xsum, fq);
             return hipGetLastError();
         }
     }
     if constexpr (MR == 1 && SPS == 2) {
         if (waves == 4 && K == 4096 && KS == ks_for(K)) {
-            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 4096>), dim3(blocks), dim3(256), lds, st, pt, K, KS, xq, xd,
+            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 4096>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
                           xsum, fq);
             return hipGetLastError();
         }
     }
     if (waves <= 4)
-        launch_kernel((k_gemv<F, MR, SPS, QN, 256>), dim3(blocks), dim3(64 * waves), lds, st, pt, K, KS,
+        launch_kernel((k_gemv<F, MR, SPS, QN, 256>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
                       xq, xd, xsum, fq);
     else if (waves <= 9 && MR == 1)
-        launch_kernel((k_gemv<F, MR, SPS, QN, 576>), dim3(blocks), dim3(64 * waves), lds, st, pt, K, KS,
+        launch_kernel((k_gemv<F, MR, SPS, QN, 576>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
                       xq, xd, xsum, fq);
     else
-        launch_kernel((k_gemv<F, MR, SPS, QN, 1024>), dim3(blocks), dim3(64 * waves), lds, st, pt, K, KS,
+        launch_kernel((k_gemv<F, MR, SPS, QN, 1024>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
                       xq, xd, xsum, fq);
     return hipGetLastError();
 }

@@ -21,6 +21,7 @@ struct PartTable {
     int tile0[kMaxParts];
     int nparts;
     int ntiles;
+    int prio = 0;  // GEMV: raise the wave priority during the activation staging
 };
 
 enum class GemvKind { Q5K, Q6KRaw, Q6KRep };
