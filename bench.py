@@ -165,9 +165,9 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
                              "launches_per_token": 8 * LAYERS + 2},
             "decode_chain_folded": {"what": "the same dependent sequence with the q8 producers of the small GEMVs "
                                             "folded into them (bq_gemv_norm_fused): QKV+resid, O+gate norm; resid, "
-                                            "gate+up, silu*mul norm, down as before; last resid; lm_head+final norm",
+                                            "gate+up, silu*mul norm, down as before; last resid, final norm -> q8, lm_head",
                                     "ms_per_token": round(folded_ms, 4), "GBps": round(gbs(tot, folded_ms), 1),
-                                    "launches_per_token": 6 * LAYERS + 2}}
+                                    "launches_per_token": 6 * LAYERS + 3}}
 
 
 def q8s_head(B, bq, torch, sp, ptr, steps=50):

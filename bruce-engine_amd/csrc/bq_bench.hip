@@ -210,9 +210,11 @@ int bqb_gemv_rows(int steps, int warmup, int nsets, const bq_weight* w, int rows
 // previous layer's down output (layer 0 reads the q8 x), O with the gate norm;
 // the resid before gate+up and the silu*mul norm before down stay standalone
 // (folded into those large GEMVs they cost more than their own launch); then
-// the last resid and the lm_head with the final norm -- 6 launches per layer
-// instead of 8.  x ping-pongs between x and x2 where a fused producer writes
-// the new x (it cannot update x in place: every workgroup reads it).
+// the last resid, the final norm and the lm_head as in the plain chain (the
+// 131072-row lm_head with the norm folded in measured 76 us against 4 + 56 us
+// for the two launches) -- 6 launches per layer instead of 8.  x ping-pongs
+// between x and x2 where a fused producer writes the new x (it cannot update
+// x in place: every workgroup reads it).
 int bqb_chain(int steps, int warmup, int nlayers, const bq_weight* w, const bq_weight* lm_head, float* const* f,
               void* const* q, int K, int KO, int FF, int folded, float* x2, bq_stream_t st, double* out) {
     float *x = f[0], *proj = f[1], *yqkv = f[2], *aout = f[3], *yg = f[4], *yu = f[5], *logits = f[6];
@@ -250,10 +252,8 @@ int bqb_chain(int steps, int warmup, int nlayers, const bq_weight* w, const bq_w
             if (int r = bq_gemv(proj, &lw[4], tq, td, ts, s)) return r;
         }
         if (int r = bq_resid_q8(xc, proj, alpha2, 1, K, xq, xd, xs, s)) return r;
-        float* yl[1] = {logits};
-        const bq_weight* pl[1] = {lm_head};
-        return bq_gemv_norm_fused(yl, pl, 1, BQ_OP_NORM, nullptr, xc, nullptr, nullptr, nullptr, nullptr, nullptr,
-                                  nullptr, s);
+        if (int r = bq_norm_q8(nullptr, xc, 1, K, xq, xd, xs, s)) return r;
+        return bq_gemv(logits, lm_head, xq, xd, xs, s);
     };
     auto token_plain = [&](bq_stream_t s) -> int {
         for (int l = 0; l < nlayers; ++l) {

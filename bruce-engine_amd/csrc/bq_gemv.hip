@@ -702,7 +702,8 @@ constexpr int kPrioMaxBlocks = 4096;
 #endif
 // BQ_GEMV_LATE=0: the 9216-value fused rows also issue their weights before
 // the staging (measured slower: down 7.4 -> 8.0-8.2 us, with or without the
-// priority)
+// priority).  Issuing them once the wave's own fp32 row has landed, before
+// the quantization and the barrier, measured slower still (8.1 -> 9.2 us).
 #ifndef BQ_GEMV_LATE
 #define BQ_GEMV_LATE 1
 #endif
