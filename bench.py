@@ -451,7 +451,7 @@ def main():
             "shapes": gemm,
             "tail_rows_bq_gemm_b": {"what": "Q5_K 9216x3072 W144, bq_gemm_b: 8-row GEMV chunks below 44 rows, "
                                             "the 128-row MMQ tile from 44", **tail},
-            "q6k_down_M2048": {"what": "Q6_K 3072x9216 over W160 (k_mmq_q6k), M=2048", "ms": round(q6ms, 4),
+            "q6k_down_M2048": {"what": "Q6_K 3072x9216 over W160 (k_mmq_q6k_dma), M=2048", "ms": round(q6ms, 4),
                                "tops": round(q6tops, 1), "frac": round(q6tops / INT8_PEAK_TOPS, 4)},
         }
 

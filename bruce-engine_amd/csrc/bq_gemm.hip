@@ -675,6 +675,173 @@ k_mmq_q6k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
 }
 
 // ---------------------------------------------------------------------------
+// Q6_K over W160, DMA-staged (the staging of k_mmq_w144 for the W160 layout;
+// the arithmetic is k_mmq_q6k's, instruction for instruction, so the results
+// are bit-identical to it).
+//   * W160 is row-major ([N][K/128][160]), so a stage's 128 rows are 160 B
+//     apart only within a row: the codes (bytes 0..127 of a row's stage) land
+//     128 B apart with 16-byte slot p of row r at p ^ f(r), f(r) = (r >> 1) & 7
+//     (the 8-byte operand reads of 32 rows then hit each bank pair at most
+//     twice, as with the old 144-byte stride), and the eight d*sc floats
+//     (bytes 128..159) land [row][8].  Tokens as the codes, xd as [tok][4].
+//   * 16 + 4 + 16 + 2 direct-to-LDS instructions per stage, two stage buffers
+//     (2 x 38 KB: two workgroups per CU), one barrier per stage.
+// ---------------------------------------------------------------------------
+struct SmemQ6Stage {
+    uint8_t w[kTN * 128];  // 16384 B: codes, swizzled 16-byte slots
+    uint8_t x[kTM * 128];  // 16384 B: token codes, same swizzle
+    float ws[kTN * 8];     //  4096 B: d*sc [row][g16]
+    float xs[kTM * 4];     //  2048 B: xd [tok][q]
+};
+
+BQ_DEV int q6_swz(int r) { return (r >> 1) & 7; }
+
+struct Q6Dma {
+    uint32_t w_off;   // codes, per lane (a wave issues instructions c = wave + 4i: c & 1 = wave & 1)
+    uint32_t s_off;   // scales, per lane
+    uint32_t x_off;   // tokens, per lane
+    uint32_t xd_off;
+    int tok_hi;         // lane >> 3
+};
+
+BQ_DEV void q6_dma(SmemQ6Stage& sb, const uint8_t* wstage, uint32_t row_bytes, const int8_t* xq, const float* xd,
+                   const Q6Dma& o, int m0, int rows, int K, int nb, int s, int wave, int lane) {
+    // weight codes: instruction c = rows 8c..8c+7
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = wave + 4 * i;
+        dma16(wstage + (size_t)(8 * c) * row_bytes, o.w_off, sb.w + 1024 * c);
+    }
+    // weight scales: instruction c = rows 32c..32c+31 (one per wave)
+    dma16(wstage + (size_t)(32 * wave) * row_bytes, o.s_off, (uint8_t*)sb.ws + 1024 * wave);
+    // tokens: instruction c = tokens 8c..8c+7 (rows past `rows` skipped)
+    const int8_t* xs0 = xq + (size_t)m0 * K + 128 * s;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = wave + 4 * i;
+        if (m0 + 8 * c + o.tok_hi < rows) dma16(xs0 + (size_t)(8 * c) * K, o.x_off, sb.x + 1024 * c);
+    }
+    if (wave < 2 && m0 + 64 * wave + lane < rows)
+        dma16(xd + (size_t)(m0 + 64 * wave) * nb + 4 * s, o.xd_off, (uint8_t*)sb.xs + 1024 * wave);
+}
+
+// One stage: per 32-group q and tile, the two-block fp32 outer product of the
+// scales of the 16-groups 2q (lanes 0-31) and 2q+1 (lanes 32-63), the two
+// int8 K=16 dots, then one convert and one FMA per output and 16-group.
+BQ_DEV void q6_stage(const SmemQ6Stage& sb, f32x16 (&acc)[2][2], int wn, int wm, int l32, int lh) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        long a[2][2], b[2][2];  // [tile][16-group half]
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                const int r = wn * 64 + nt * 32 + l32;
+                a[nt][h] = *(const long*)(sb.w + r * 128 + 16 * ((2 * q + h) ^ q6_swz(r)) + 8 * lh);
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const int t = wm * 64 + mt * 32 + l32;
+                b[mt][h] = *(const long*)(sb.x + t * 128 + 16 * ((2 * q + h) ^ q6_swz(t)) + 8 * lh);
+            }
+        }
+        float wsv[2], xsv[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) wsv[nt] = sb.ws[8 * (wn * 64 + nt * 32 + l32) + 2 * q + lh];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) xsv[mt] = sb.xs[4 * (wm * 64 + mt * 32 + l32) + q];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const f32x32 zero32 = {0.f};
+                const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(wsv[nt], xsv[mt], zero32, 0, 0, 0);
+                const i32x16 zero = {0};
+                const i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a[nt][0], b[mt][0], zero, 0, 0, 0);
+                const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a[nt][1], b[mt][1], zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    acc[nt][mt][r] = __builtin_fmaf(sc[r], (float)d0[r], acc[nt][mt][r]);
+                    acc[nt][mt][r] = __builtin_fmaf(sc[16 + r], (float)d1[r], acc[nt][mt][r]);
+                }
+            }
+    }
+}
+
+__global__ void __launch_bounds__(256, 2)
+k_mmq_q6k_dma(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
+              const float* __restrict__ xd) {
+    __shared__ __attribute__((aligned(16))) SmemQ6Stage sm0;
+    __shared__ __attribute__((aligned(16))) SmemQ6Stage sm1;
+    TileMap tm;
+    if (!map_tile(blockIdx.x, ntm, ntn, tm)) return;
+    int nbase = tm.nt * kTN;
+    const int p = part_of_ntile(pt, nbase);
+    const int Nloc = pt.N[p];
+    const uint8_t* __restrict__ W = (const uint8_t*)pt.W[p];
+    const int m0 = tm.mt * kTM;
+    const int nb = K >> 5, nst = K >> 7;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave >> 1, wm = wave & 1;
+    const int l32 = lane & 31, lh = lane >> 5;
+    const uint32_t row_bytes = (uint32_t)nst * kW160;
+    auto wstage = [&](int s) { return W + (size_t)nbase * row_bytes + (size_t)s * kW160; };
+    Q6Dma o;
+    o.tok_hi = lane >> 3;
+    // codes: lane -> row (lane >> 3) of the instruction, LDS slot lane & 7,
+    // global slot (lane & 7) ^ f(8c + (lane >> 3)); f depends on c only via
+    // c & 1, which is wave & 1 for every instruction of this wave
+    {
+        const uint32_t sw = q6_swz(8 * (wave & 1) + (lane >> 3));
+        o.w_off = (uint32_t)(lane >> 3) * row_bytes + 16u * ((lane & 7) ^ sw);
+        o.x_off = (uint32_t)(lane >> 3) * (uint32_t)K + 16u * ((lane & 7) ^ sw);
+    }
+    o.s_off = (uint32_t)(lane >> 1) * row_bytes + 128u + 16u * (uint32_t)(lane & 1);
+    o.xd_off = (uint32_t)lane * (uint32_t)(nb * 4);
+
+    q6_dma(sm0, wstage(0), row_bytes, xq, xd, o, m0, rows, K, nb, 0, wave, lane);
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+    for (int s = 0; s < nst; s += 2) {
+        BQ_WAIT_VM(0);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (s + 1 < nst) q6_dma(sm1, wstage(s + 1), row_bytes, xq, xd, o, m0, rows, K, nb, s + 1, wave, lane);
+        q6_stage(sm0, acc, wn, wm, l32, lh);
+        if (s + 1 >= nst) break;
+        BQ_WAIT_VM(0);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (s + 2 < nst) q6_dma(sm0, wstage(s + 2), row_bytes, xq, xd, o, m0, rows, K, nb, s + 2, wave, lane);
+        q6_stage(sm1, acc, wn, wm, l32, lh);
+    }
+
+    float* __restrict__ Y = pt.Y[p];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int m = m0 + wm * 64 + mt * 32 + l32;
+        if (m >= rows) continue;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const int n = nbase + wn * 64 + nt * 32 + 8 * rg + 4 * lh;
+                const f32x4 v = {acc[nt][mt][4 * rg], acc[nt][mt][4 * rg + 1], acc[nt][mt][4 * rg + 2],
+                                 acc[nt][mt][4 * rg + 3]};
+                *(f32x4*)(Y + (size_t)m * Nloc + n) = v;
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
 static int ntile_count(const PartTable& pt) {
     int n = 0;
     for (int p = 0; p < pt.nparts; ++p) n += pt.N[p] / kTN;
@@ -724,7 +891,15 @@ hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const
                           hipStream_t st) {
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    launch_kernel(k_mmq_q6k, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd);
+    static int v = -1;  // BQ_MMQ_Q6_DMA=0: the register-staged kernel (dev A/B switch, read once)
+    if (v < 0) {
+        const char* e = getenv("BQ_MMQ_Q6_DMA");
+        v = e ? atoi(e) : 1;
+    }
+    if (v)
+        launch_kernel(k_mmq_q6k_dma, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd);
+    else
+        launch_kernel(k_mmq_q6k, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd);
     return hipGetLastError();
 }
 
