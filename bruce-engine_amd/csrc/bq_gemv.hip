@@ -792,7 +792,14 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     // q8 staging (DMA of a row the previous kernel just wrote) stays ahead of
     // the weight loads.
     constexpr bool kLate = QN != 0 && KC != 3072 && KC != 4096 && BQ_GEMV_LATE;
-    constexpr int kEarly = kLate ? 0 : SPS;  // steps whose loads go out before the staging wait
+// With the late weight issue, the first step's loads still go out before the
+// staging wait (down, 2 steps per wave: 8.18 -> 8.08 us in the decode step,
+// kernel-event medians 8.19 -> 7.97 over 6 interleaved pairs).
+#ifndef BQ_GEMV_LATE_EARLY
+#define BQ_GEMV_LATE_EARLY 1
+#endif
+    // steps whose loads go out before the staging wait (late: at least one step after it)
+    constexpr int kEarly = kLate ? (BQ_GEMV_LATE_EARLY < SPS - 1 ? BQ_GEMV_LATE_EARLY : SPS - 1) : SPS;
                                              // (issuing 1 or 2 of 3 early measured slower)
     auto issue_weights = [&](int s0, int s1) {
 #pragma unroll
