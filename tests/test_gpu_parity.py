@@ -405,11 +405,15 @@ def test_mmq_unsupported(bq):
     assert bq.try_mmq([y], [w], 64, xq, xd, xs) == bq.BQ_UNSUPPORTED  # rows < 96
 
 
-def test_mmq_q6k(bq, oracle):
+@pytest.mark.parametrize("K,N,M", [(1024, 256, 160), (256, 128, 1), (256, 384, 300), (9216, 128, 140),
+                                   (3072, 256, 257)])
+def test_mmq_q6k(bq, oracle, K, N, M):
+    """Q6_K GEMM over W160: the shortest K (one stage pair), a single token,
+    token counts that leave a partial tile, the down projection's K = 9216."""
     import torch
-    K, N, M = 1024, 256, 160
-    raw = weights(1200, N, K, "q6k")
-    _, (xq, xd, xs) = acts(1201, M, K)
+    print(f"mmq q6k K={K} N={N} M={M}", flush=True)
+    raw = weights(1200 + K // 128 + M, N, K, "q6k")
+    _, (xq, xd, xs) = acts(1201 + M, M, K)
     g = dev(raw)
     w = bq.make_weight(g, bq.TYPE_Q6_K, K, N, rep=bq.repack_q6k(g, K, N))
     y = torch.full((M, N), float("nan"), device="cuda")
