@@ -146,6 +146,11 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
     if r != 0:
         raise RuntimeError(f"bqb_chain (folded) failed: {r}")
     folded_ms = out[0] / steps
+    # and the FFN folded too: gate+up with the silu*mul epilogue, its norm + q8 in the down GEMV
+    r = B.bqb_chain(steps, warmup, LAYERS, ws, ctypes.byref(lmw), farr, qarr, K, KO, FF, 2, ptr(x2), sp, out)
+    if r != 0:
+        raise RuntimeError(f"bqb_chain (folded ffn) failed: {r}")
+    folded2_ms = out[0] / steps
     del fb, qb
     wbytes = LAYERS * sum(a.nbytes for a in (w_qkv, w_o, w_gate, w_up, w_down)) + lm.numel()
     act = LAYERS * (2 * (4 * K + q8_bytes(1, K)) + (4 * KO + q8_bytes(1, KO)) + (4 * FF + q8_bytes(1, FF))) \
@@ -167,7 +172,12 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
                                             "folded into them (bq_gemv_norm_fused): QKV+resid, O+gate norm; resid, "
                                             "gate+up, silu*mul norm, down as before; last resid, final norm -> q8, lm_head",
                                     "ms_per_token": round(folded_ms, 4), "GBps": round(gbs(tot, folded_ms), 1),
-                                    "launches_per_token": 6 * LAYERS + 3}}
+                                    "launches_per_token": 6 * LAYERS + 3},
+            "decode_chain_folded_ffn": {"what": "as decode_chain_folded, with gate+up and the silu*mul of its "
+                                                "outputs in one launch (bq_gate_up_silu) and the norm -> q8 of h "
+                                                "inside the down GEMV (bq_gemv_norm_fused)",
+                                        "ms_per_token": round(folded2_ms, 4), "GBps": round(gbs(tot, folded2_ms), 1),
+                                        "launches_per_token": 5 * LAYERS + 3}}
 
 
 def q8s_head(B, bq, torch, sp, ptr, steps=50):

@@ -40,7 +40,7 @@ EXPORTS = [
     "bq_quantize_q8s_host", "bq_gemv_q8s", "bq_norm_q8", "bq_add_norm_q8", "bq_resid_q8",
     "bq_gate_norm_q8", "bq_silu_mul_norm_q8", "bq_gguf_open", "bq_gguf_close", "bq_gguf_n_tensors",
     "bq_gguf_find", "bq_gguf_tensor_info", "bq_gguf_kv_num", "bq_gguf_kv_str", "bq_gguf_read", "bq_gguf_load",
-    "bq_gemv_norm_fused",
+    "bq_gemv_norm_fused", "bq_gate_up_silu",
 ]
 
 
@@ -102,6 +102,7 @@ def load(path=LIB_PATH):
         "bq_time_next_launch": (I, [P, P]),
         "bq_gemv_q8_fused": (I, [P, P, I, P, P, P, P, P]),
         "bq_gemv_norm_fused": (I, [P, P, I, I, P, P, P, P, P, P, P, P, P]),
+        "bq_gate_up_silu": (I, [P, WP, WP, P, P, P, P, P, P]),
         "bq_q8s_bytes": (S, [I, I]),
         "bq_quantize_q8s": (I, [P, I, I, P, P]),
         "bq_quantize_q8s_host": (I, [P, I, I, P]),
@@ -235,6 +236,14 @@ def gemv_norm_fused(ys, ws, op, a, b=None, c=None, d=None, out=None, q8=None):
     if r not in (BQ_OK, BQ_UNSUPPORTED):
         raise BqError(r, "bq_gemv_norm_fused")
     return r
+
+
+def gate_up_silu(h, wg, wu, sg, su, xq, xd, xsum=None):
+    """h = silu(g * sg) * u * su with g = wg x, u = wu x for one q8 row x, one launch."""
+    _need_gpu(h, sg, su, xq, xd, xsum)
+    _check(load().bq_gate_up_silu(_ptr(h), ctypes.byref(wg), ctypes.byref(wu), _ptr(sg), _ptr(su), _ptr(xq),
+                                  _ptr(xd), _ptr(xsum), _stream()), "bq_gate_up_silu")
+    return h
 
 
 def q6_verify_fused(ys, ws, rows, xq, xd, xoff=0):

@@ -294,6 +294,38 @@ int bq_gemv_norm_fused(float* const* ys, const bq_weight* const* ws, int nparts,
                                          xsum, (hipStream_t)st));
 }
 
+int bq_gate_up_silu(float* h, const bq_weight* wg, const bq_weight* wu, const float* sg, const float* su,
+                    const int8_t* xq, const float* xd, const int32_t* xsum, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (!h || !sg || !su || !xq || !xd || !weight_ok(wg) || !weight_ok(wu)) return BQ_EINVAL;
+    const int K = wg->K, N = wg->N;
+    const uint32_t type = wg->ggml_type;
+    if (wu->K != K || wu->N != N || wu->ggml_type != type) return BQ_UNSUPPORTED;
+    if (K % 256 != 0 || N % 16 != 0) return BQ_UNSUPPORTED;
+    PartTable pt;
+    memset(&pt, 0, sizeof(pt));
+    GemvKind kind;
+    if (type == BQ_TYPE_Q5_K) {
+        if (!wg->raw || !wu->raw) return BQ_UNSUPPORTED;
+        if (!xsum) return BQ_EINVAL;
+        kind = GemvKind::Q5K;
+        pt.W[0] = wg->raw;
+        pt.W[1] = wu->raw;
+    } else if (type == BQ_TYPE_Q6_K) {
+        const bool rep = wg->rep != nullptr;
+        if ((wu->rep != nullptr) != rep || (!rep && (!wg->raw || !wu->raw))) return BQ_UNSUPPORTED;
+        kind = rep ? GemvKind::Q6KRep : GemvKind::Q6KRaw;
+        pt.W[0] = rep ? wg->rep : wg->raw;
+        pt.W[1] = rep ? wu->rep : wu->raw;
+    } else {
+        return BQ_UNSUPPORTED;
+    }
+    pt.N[0] = pt.N[1] = N;
+    pt.Y[0] = pt.Y[1] = h;  // not written: the epilogue writes h
+    pt.nparts = 2;
+    return from_hip(launch_gemv_silu_pair(kind, pt, K, xq, xd, xsum, sg, su, h, (hipStream_t)st));
+}
+
 namespace {
 // The MMQ launch behind bq_try_mmq and the bq_gemm_b dispatchers.  min_w144 /
 // min_raw: the smallest row count taken by the prepacked / raw tier (below

@@ -214,7 +214,9 @@ int bqb_gemv_rows(int steps, int warmup, int nsets, const bq_weight* w, int rows
 // 131072-row lm_head with the norm folded in measured 76 us against 4 + 56 us
 // for the two launches) -- 6 launches per layer instead of 8.  x ping-pongs
 // between x and x2 where a fused producer writes the new x (it cannot update
-// x in place: every workgroup reads it).
+// x in place: every workgroup reads it).  folded == 2: also gate+up with the
+// silu*mul epilogue (bq_gate_up_silu) and the norm + q8 of h inside the down
+// GEMV (bq_gemv_norm_fused, BQ_OP_NORM) -- 5 launches per layer.
 int bqb_chain(int steps, int warmup, int nlayers, const bq_weight* w, const bq_weight* lm_head, float* const* f,
               void* const* q, int K, int KO, int FF, int folded, float* x2, bq_stream_t st, double* out) {
     float *x = f[0], *proj = f[1], *yqkv = f[2], *aout = f[3], *yg = f[4], *yu = f[5], *logits = f[6];
@@ -245,6 +247,16 @@ int bqb_chain(int steps, int warmup, int nlayers, const bq_weight* w, const bq_w
                                            nullptr, nullptr, s))
                 return r;
             if (int r = bq_resid_q8(xc, proj, alpha, 1, K, xq, xd, xs, s)) return r;
+            if (folded == 2) {
+                // gate+up with the silu*mul epilogue, its norm + q8 inside the down GEMV
+                if (int r = bq_gate_up_silu(yg, &lw[2], &lw[3], sg, su, xq, xd, xs, s)) return r;
+                float* yd[1] = {proj};
+                const bq_weight* pd[1] = {&lw[4]};
+                if (int r = bq_gemv_norm_fused(yd, pd, 1, BQ_OP_NORM, nullptr, yg, nullptr, nullptr, nullptr,
+                                               nullptr, nullptr, nullptr, s))
+                    return r;
+                continue;
+            }
             float* y2[2] = {yg, yu};
             const bq_weight* p2[2] = {&lw[2], &lw[3]};
             if (int r = bq_verify_fused(y2, p2, 2, 1, xq, xd, xs, 0, s)) return r;

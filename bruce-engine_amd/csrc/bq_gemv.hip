@@ -715,11 +715,17 @@ constexpr int kPrioMaxBlocks = 4096;
 // K slices of a row of K values (ceil(K/1024) steps, at most 3 per wave)
 __host__ __device__ constexpr int ks_for(int K) { return ((K + 1023) / 1024 + 2) / 3; }
 
-template <class F, int MR, int SPS, int QN, int LB, int KC = 0>
+// PAIR: gate and up rows of the same index in one wave (parts 0 and 1, equal
+// N): DPP rows 0, 1 take gate rows 2t, 2t+1 and rows 2, 3 the up rows of the
+// same indices; the epilogue writes h = silu(g * sg) * u * su (fq.out, with
+// sg = fq.c, su = fq.d) instead of the two outputs.  The sums of each row are
+// the plain kernel's, so h is bit-identical to silu_mul on its outputs.
+template <class F, int MR, int SPS, int QN, int LB, int KC = 0, bool PAIR = false>
 __global__ void __launch_bounds__(LB)
 k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float* __restrict__ xd,
        const int32_t* __restrict__ xsum, FusedQ8 fq) {
     static_assert(QN == 0 || MR == 1, "fused quantizer / producer: one activation row");
+    static_assert(!PAIR || (MR == 1 && QN == 0), "paired silu epilogue: one q8 activation row");
     // KC > 0: the row length (and so the K split and the 4-wave workgroup) is
     // a compile-time constant -- the decode shapes get their own instances
     const int K = KC ? KC : K_;
@@ -774,11 +780,12 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     const int tile = blockIdx.x * RT + wave / KS, ks = wave % KS;
     const bool active = wave < RT * KS && tile < pt.ntiles;
     const int tl = active ? tile : 0;
-    const int p = find_part(pt, tl);
+    const int p = PAIR ? 0 : find_part(pt, tl);
     const int Nloc = pt.N[p];
-    const int row = (tl - pt.tile0[p]) * kRowsPerTile + g;
+    const int row = PAIR ? 2 * tl + (g & 1) : (tl - pt.tile0[p]) * kRowsPerTile + g;
     const int tpr = K >> 6;
-    const uint8_t* rowp = (const uint8_t*)pt.W[p] + (size_t)min(row, Nloc - 1) * RowBytes<F>::of(K);
+    const void* wbase = PAIR ? ((g >> 1) ? pt.W[1] : pt.W[0]) : pt.W[p];
+    const uint8_t* rowp = (const uint8_t*)wbase + (size_t)min(row, Nloc - 1) * RowBytes<F>::of(K);
     typename F::Task w[SPS];
     // The fused quantizer's fp32 row comes from memory that the whole grid's
     // weight stream is also queueing on: issued together, the row lands only
@@ -799,7 +806,10 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
 #define BQ_GEMV_LATE_EARLY 1
 #endif
     // steps whose loads go out before the staging wait (late: at least one step after it)
-    constexpr int kEarly = kLate ? (BQ_GEMV_LATE_EARLY < SPS - 1 ? BQ_GEMV_LATE_EARLY : SPS - 1) : SPS;
+    // (fused quantizer only: with a producer the first step's loads held up
+    // its reductions -- down + norm 9.99 -> 16.9 us)
+    constexpr int kEarly =
+        kLate ? (QN > 0 ? (BQ_GEMV_LATE_EARLY < SPS - 1 ? BQ_GEMV_LATE_EARLY : SPS - 1) : 0) : SPS;
                                              // (issuing 1 or 2 of 3 early measured slower)
     auto issue_weights = [&](int s0, int s1) {
 #pragma unroll
@@ -871,6 +881,12 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     // ---- 5. row sums; K slices combined through LDS
     float* Y = pt.Y[p];
     if (KS == 1) {
+        if constexpr (PAIR) {
+            const float v = row16_sum(acc[0]);
+            const float u = __shfl(v, lane + 32, 64);  // DPP rows 0, 1 <- 2, 3
+            if (g < 2 && li == 15 && rowok) fq.out[row] = silu_mul(v, u, fq.c[row], fq.d[row]);
+            return;
+        }
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
             const float v = kMmLanes ? lane4_sum(acc[m], li) : row16_sum(acc[m]);
@@ -885,6 +901,17 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
         if (li == 15) part_sums[(wave * MR + m) * 4 + g] = v;
     }
     __syncthreads();
+    if constexpr (PAIR) {
+        if (ks == 0 && g < 2 && rowok && li == 15) {
+            float v = 0.f, u = 0.f;
+            for (int k = 0; k < KS; ++k) {
+                v += part_sums[(wave + k) * 4 + g];
+                u += part_sums[(wave + k) * 4 + g + 2];
+            }
+            fq.out[row] = silu_mul(v, u, fq.c[row], fq.d[row]);
+        }
+        return;
+    }
     if (ks == 0 && rowok && li == 15) {
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
@@ -979,7 +1006,7 @@ static int gemv_waves(int KS, int MR) {
     return std::max(w, KS);
 }
 
-template <class F, int MR, int SPS, int QN = 0>
+template <class F, int MR, int SPS, int QN = 0, bool PAIR = false>
 static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* xq, const float* xd,
                              const int32_t* xsum, hipStream_t st, FusedQ8 fq = {}) {
     int waves = gemv_waves(KS, MR);
@@ -995,33 +1022,33 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     // single-row decode shapes run compile-time-K instances
     if constexpr (SPS == 3 && (MR == 1 || QN == 0)) {
         if (waves == 4 && K == 3072 && KS == ks_for(K)) {
-            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
+            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
                           xsum, fq);
             return hipGetLastError();
         }
     }
     if constexpr (SPS == 3 && MR == 1) {
         if (waves == 4 && K == 9216 && KS == ks_for(K)) {
-            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 9216>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
+            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 9216, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
                           xsum, fq);
             return hipGetLastError();
         }
     }
     if constexpr (MR == 1 && SPS == 2) {
         if (waves == 4 && K == 4096 && KS == ks_for(K)) {
-            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 4096>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
+            launch_kernel((k_gemv<F, MR, SPS, QN, 256, 4096, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
                           xsum, fq);
             return hipGetLastError();
         }
     }
     if (waves <= 4)
-        launch_kernel((k_gemv<F, MR, SPS, QN, 256>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
+        launch_kernel((k_gemv<F, MR, SPS, QN, 256, 0, PAIR>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
                       xq, xd, xsum, fq);
     else if (waves <= 9 && MR == 1)
-        launch_kernel((k_gemv<F, MR, SPS, QN, 576>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
+        launch_kernel((k_gemv<F, MR, SPS, QN, 576, 0, PAIR>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
                       xq, xd, xsum, fq);
     else
-        launch_kernel((k_gemv<F, MR, SPS, QN, 1024>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
+        launch_kernel((k_gemv<F, MR, SPS, QN, 1024, 0, PAIR>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
                       xq, xd, xsum, fq);
     return hipGetLastError();
 }
@@ -1078,6 +1105,38 @@ hipError_t launch_gemv(GemvKind kind, PartTable pt, int rows, int K, const int8_
         case GemvKind::Q5K: return dispatch_rows<FmtQ5K>(rows, pt, K, xq, xd, xsum, st);
         case GemvKind::Q6KRaw: return dispatch_rows<FmtQ6KRaw>(rows, pt, K, xq, xd, xsum, st);
         default: return dispatch_rows<FmtQ6KRep>(rows, pt, K, xq, xd, xsum, st);
+    }
+}
+
+// gate and up of one q8 row with the silu*mul epilogue (PAIR): parts 0 and 1
+// of pt (equal N), h / sg / su in fq.out / fq.c / fq.d.  The K split is the
+// one launch_gemv picks for the two parts, so each row's sum is the same.
+template <class F>
+static hipError_t dispatch_pair(const PartTable& pt, int K, const int8_t* xq, const float* xd,
+                                const int32_t* xsum, const FusedQ8& fq, hipStream_t st) {
+    int KS, SPS;
+    k_split(K, sps_cap(KindOf<F>::v, K, (long long)pt.ntiles * kRowsPerTile, 1, false), KS, SPS);
+    if (KS > 16) return hipErrorInvalidValue;
+    switch (SPS) {
+        case 1: return launch_fmt<F, 1, 1, 0, true>(pt, K, KS, xq, xd, xsum, st, fq);
+        case 2: return launch_fmt<F, 1, 2, 0, true>(pt, K, KS, xq, xd, xsum, st, fq);
+        default: return launch_fmt<F, 1, 3, 0, true>(pt, K, KS, xq, xd, xsum, st, fq);
+    }
+}
+
+hipError_t launch_gemv_silu_pair(GemvKind kind, PartTable pt, int K, const int8_t* xq, const float* xd,
+                                 const int32_t* xsum, const float* sg, const float* su, float* h, hipStream_t st) {
+    if (pt.nparts != 2 || pt.N[0] != pt.N[1] || pt.N[0] % 4 != 0) return hipErrorInvalidValue;
+    build_tiles(pt);
+    if (pt.ntiles == 0) return hipSuccess;
+    FusedQ8 fq{};
+    fq.out = h;
+    fq.c = sg;
+    fq.d = su;
+    switch (kind) {
+        case GemvKind::Q5K: return dispatch_pair<FmtQ5K>(pt, K, xq, xd, xsum, fq, st);
+        case GemvKind::Q6KRaw: return dispatch_pair<FmtQ6KRaw>(pt, K, xq, xd, xsum, fq, st);
+        default: return dispatch_pair<FmtQ6KRep>(pt, K, xq, xd, xsum, fq, st);
     }
 }
 

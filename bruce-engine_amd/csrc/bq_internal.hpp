@@ -68,6 +68,8 @@ hipError_t launch_gemv_producer(GemvKind kind, PartTable pt, int K, int op, floa
                                 const float* b, const float* c, const float* d, int8_t* xq, float* xd,
                                 int32_t* xsum, hipStream_t st);
 size_t gemv_lds_bytes(GemvKind kind, int rows, int K);
+hipError_t launch_gemv_silu_pair(GemvKind kind, PartTable pt, int K, const int8_t* xq, const float* xd,
+                                 const int32_t* xsum, const float* sg, const float* su, float* h, hipStream_t st);
 hipError_t launch_gemv(GemvKind kind, PartTable pt, int rows, int K, const int8_t* xq,
                        const float* xd, const int32_t* xsum, hipStream_t st);
 

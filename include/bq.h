@@ -162,6 +162,20 @@ int bq_gemv_q8_fused(float* const* ys, const bq_weight* const* ws, int nparts, c
  * workgroups, since each one recomputes the producer).
  * K % 256 == 0 and K <= 16384, else BQ_UNSUPPORTED.  An extension of this
  * library: the reference has no fused form. */
+/* Gate and up projections of one q8 activation row with the elementwise
+ * silu*mul epilogue: h[n] = silu(g[n] * sg[n]) * u[n] * su[n] with g = Wg x,
+ * u = Wu x (silu(v) = v / (1 + exp(-v))), in one launch that reads both
+ * matrices once and writes only h.  Replaces the gate+up GEMV
+ * (launch_verify_fused, bruce.cu:7141) and the elementwise half of
+ * k_silu_mul_norm (:622); the norm + q8 half then runs inside the down
+ * projection's GEMV (bq_gemv_norm_fused with BQ_OP_NORM on h).  g and u are
+ * bit-identical to bq_verify_fused / bq_gemv on the same inputs, and h to
+ * silu_mul of them.  wg, wu: same type (Q5_K raw, or Q6_K raw / W160), K and
+ * N; K % 256 == 0, N % 16 == 0, else BQ_UNSUPPORTED; xsum required for Q5_K.
+ * An extension of this library: the reference has no fused form. */
+int bq_gate_up_silu(float* h, const bq_weight* wg, const bq_weight* wu, const float* sg, const float* su,
+                    const int8_t* xq, const float* xd, const int32_t* xsum, bq_stream_t st);
+
 #define BQ_OP_NORM 0
 #define BQ_OP_ADD 1
 #define BQ_OP_RESID 2
