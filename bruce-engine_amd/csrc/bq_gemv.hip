@@ -707,6 +707,13 @@ constexpr int kPrioMaxBlocks = 4096;
 #ifndef BQ_GEMV_LATE
 #define BQ_GEMV_LATE 1
 #endif
+// A compile-time-K instance for the fused / producer-fused 9216-value row over
+// 16-wave workgroups (the down projection; the launch's K split is kept):
+// fused down 8.0-8.4 -> 7.5-7.8 us, down + norm 10.1 -> 9.7-9.85 us, decode
+// FFN step 17.93 -> 17.50 us.  BQ_GEMV_DOWN_KC=0 builds without it.
+#ifndef BQ_GEMV_DOWN_KC
+#define BQ_GEMV_DOWN_KC 1
+#endif
 // BQ_GEMV_STEP_ORDER=0 builds the previous load order (a dev A/B switch)
 #ifndef BQ_GEMV_STEP_ORDER
 #define BQ_GEMV_STEP_ORDER 1
@@ -729,7 +736,8 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     // KC > 0: the row length (and so the K split and the 4-wave workgroup) is
     // a compile-time constant -- the decode shapes get their own instances
     const int K = KC ? KC : K_;
-    const int KS = KC ? ks_for(KC) : KS_;
+    // (the 16-wave compile-time-K instance keeps the launch's K split)
+    const int KS = (KC && LB == 256) ? ks_for(KC) : KS_;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // multi-row Q5_K from kQ5kMfmaMinRows rows: dot products on the matrix
     // cores, lane = 4 * task + row
@@ -739,7 +747,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     const int lane = threadIdx.x & 63;
     const int g = kMmLanes ? (lane & 3) : (lane >> 4), li = kMmLanes ? (lane >> 2) : (lane & 15);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
-    const int waves = KC ? 4 : blockDim.x >> 6;
+    const int waves = (KC && LB == 256) ? 4 : (KC ? LB / 64 : blockDim.x >> 6);
     const int nb = K >> 5;
     BQ_TS(0);
     // ---- 1. activations -> LDS (asynchronous), or this wave's fp32 chunks -> registers
@@ -1041,6 +1049,16 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
             return hipGetLastError();
         }
     }
+#if BQ_GEMV_DOWN_KC
+    // the fused / producer-fused 9216-value row over 16-wave workgroups (the down projection)
+    if constexpr (MR == 1 && SPS == 2 && QN != 0 && !PAIR) {
+        if (waves == 16 && K == 9216) {
+            launch_kernel((k_gemv<F, MR, SPS, QN, 1024, 9216, PAIR>), dim3(blocks), dim3(1024), lds, st, ptl, K, KS,
+                          xq, xd, xsum, fq);
+            return hipGetLastError();
+        }
+    }
+#endif
     if (waves <= 4)
         launch_kernel((k_gemv<F, MR, SPS, QN, 256, 0, PAIR>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
                       xq, xd, xsum, fq);
