@@ -719,8 +719,8 @@ constexpr int kPrioMaxBlocks = 4096;
 #define BQ_GEMV_STEP_ORDER 1
 #endif
 
-// K slices of a row of K values (ceil(K/1024) steps, at most 3 per wave)
-__host__ __device__ constexpr int ks_for(int K) { return ((K + 1023) / 1024 + 2) / 3; }
+// K slices of a compile-time-K instance with SPS steps per wave
+__host__ __device__ constexpr int kc_ks(int K, int sps) { return ((K + 1023) / 1024 + sps - 1) / sps; }
 
 // PAIR: gate and up rows of the same index in one wave (parts 0 and 1, equal
 // N): DPP rows 0, 1 take gate rows 2t, 2t+1 and rows 2, 3 the up rows of the
@@ -733,11 +733,11 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
        const int32_t* __restrict__ xsum, FusedQ8 fq) {
     static_assert(QN == 0 || MR == 1, "fused quantizer / producer: one activation row");
     static_assert(!PAIR || (MR == 1 && QN == 0), "paired silu epilogue: one q8 activation row");
-    // KC > 0: the row length (and so the K split and the 4-wave workgroup) is
-    // a compile-time constant -- the decode shapes get their own instances
+    // KC > 0: the row length, and with it the K split (kc_ks) and the workgroup
+    // (LB / 64 waves), is a compile-time constant -- the decode shapes get
+    // their own instances
     const int K = KC ? KC : K_;
-    // (the 16-wave compile-time-K instance keeps the launch's K split)
-    const int KS = (KC && LB == 256) ? ks_for(KC) : KS_;
+    const int KS = KC ? kc_ks(KC, SPS) : KS_;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // multi-row Q5_K from kQ5kMfmaMinRows rows: dot products on the matrix
     // cores, lane = 4 * task + row
@@ -747,7 +747,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     const int lane = threadIdx.x & 63;
     const int g = kMmLanes ? (lane & 3) : (lane >> 4), li = kMmLanes ? (lane >> 2) : (lane & 15);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
-    const int waves = (KC && LB == 256) ? 4 : (KC ? LB / 64 : blockDim.x >> 6);
+    const int waves = KC ? LB / 64 : blockDim.x >> 6;
     const int nb = K >> 5;
     BQ_TS(0);
     // ---- 1. activations -> LDS (asynchronous), or this wave's fp32 chunks -> registers
@@ -1029,30 +1029,42 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     // the launch-bounds class sets the compiler's occupancy target; the
     // single-row decode shapes run compile-time-K instances
     if constexpr (SPS == 3 && (MR == 1 || QN == 0)) {
-        if (waves == 4 && K == 3072 && KS == ks_for(K)) {
+        if (waves == 4 && K == 3072 && KS == kc_ks(K, SPS)) {
             launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
                           xsum, fq);
             return hipGetLastError();
         }
     }
     if constexpr (SPS == 3 && MR == 1) {
-        if (waves == 4 && K == 9216 && KS == ks_for(K)) {
+        if (waves == 4 && K == 9216 && KS == kc_ks(K, SPS)) {
             launch_kernel((k_gemv<F, MR, SPS, QN, 256, 9216, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
                           xsum, fq);
             return hipGetLastError();
         }
     }
     if constexpr (MR == 1 && SPS == 2) {
-        if (waves == 4 && K == 4096 && KS == ks_for(K)) {
+        if (waves == 4 && K == 4096 && KS == kc_ks(K, SPS)) {
             launch_kernel((k_gemv<F, MR, SPS, QN, 256, 4096, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
                           xsum, fq);
+            return hipGetLastError();
+        }
+    }
+    // one step per wave (the cap-1 K split of the small decode GEMVs: QKV, O)
+    if constexpr (MR == 1 && SPS == 1 && QN <= 1) {
+        if (waves == 4 && KS == kc_ks(K, SPS) && (K == 3072 || K == 4096)) {
+            if (K == 3072)
+                launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K,
+                              KS, xq, xd, xsum, fq);
+            else
+                launch_kernel((k_gemv<F, MR, SPS, QN, 256, 4096, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K,
+                              KS, xq, xd, xsum, fq);
             return hipGetLastError();
         }
     }
 #if BQ_GEMV_DOWN_KC
     // the fused / producer-fused 9216-value row over 16-wave workgroups (the down projection)
     if constexpr (MR == 1 && SPS == 2 && QN != 0 && !PAIR) {
-        if (waves == 16 && K == 9216) {
+        if (waves == 16 && K == 9216 && KS == kc_ks(K, SPS)) {
             launch_kernel((k_gemv<F, MR, SPS, QN, 1024, 9216, PAIR>), dim3(blocks), dim3(1024), lds, st, ptl, K, KS,
                           xq, xd, xsum, fq);
             return hipGetLastError();
