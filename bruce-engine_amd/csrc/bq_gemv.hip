@@ -1061,6 +1061,18 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
             return hipGetLastError();
         }
     }
+    // Q5_K verify rows 2..8 at K = 3072 / 4096 (cap-1 / cap-2 K splits)
+    if constexpr (QN == 0 && !PAIR && MR > 1 && SPS < 3 && std::is_same<F, FmtQ5K>::value) {
+        if (waves == 4 && KS == kc_ks(K, SPS) && (K == 3072 || K == 4096)) {
+            if (K == 3072)
+                launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K,
+                              KS, xq, xd, xsum, fq);
+            else
+                launch_kernel((k_gemv<F, MR, SPS, QN, 256, 4096, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K,
+                              KS, xq, xd, xsum, fq);
+            return hipGetLastError();
+        }
+    }
 #if BQ_GEMV_DOWN_KC
     // the fused / producer-fused 9216-value row over 16-wave workgroups (the down projection)
     if constexpr (MR == 1 && SPS == 2 && QN != 0 && !PAIR) {
