@@ -1073,6 +1073,30 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
             return hipGetLastError();
         }
     }
+    // Q6_K raw at the down (K = 9216, verify rows) and lm_head (K = 3072, one row) shapes
+    if constexpr (QN == 0 && !PAIR && std::is_same<F, FmtQ6KRaw>::value) {
+        if constexpr (SPS == 3 && MR > 1 && MR <= 5) {
+            if (waves == 4 && K == 9216 && KS == kc_ks(K, SPS)) {
+                launch_kernel((k_gemv<F, MR, SPS, QN, 256, 9216, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K,
+                              KS, xq, xd, xsum, fq);
+                return hipGetLastError();
+            }
+        }
+        if constexpr (SPS == 2 && MR == 1) {
+            if (waves == 4 && K == 3072 && KS == kc_ks(K, SPS)) {
+                launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K,
+                              KS, xq, xd, xsum, fq);
+                return hipGetLastError();
+            }
+        }
+        if constexpr (SPS == 2 && MR >= 6) {
+            if (waves == 16 && K == 9216 && KS == kc_ks(K, SPS)) {
+                launch_kernel((k_gemv<F, MR, SPS, QN, 1024, 9216, PAIR>), dim3(blocks), dim3(1024), lds, st, ptl, K,
+                              KS, xq, xd, xsum, fq);
+                return hipGetLastError();
+            }
+        }
+    }
 #if BQ_GEMV_DOWN_KC
     // the fused / producer-fused 9216-value row over 16-wave workgroups (the down projection)
     if constexpr (MR == 1 && SPS == 2 && QN != 0 && !PAIR) {
