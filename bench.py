@@ -525,7 +525,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for("gemv_q5k_gateup_fused"),
                      "kernel": "k_gemv<FmtQ5K, 1, 3, 1, 256, 3072> (quantize x + gate+up)", "bytes_per_launch": gu_bytes,
                      "avg_launch_us": round(gu_ms * 1e3, 3)},
-        "down_gemv": {"kernel": "k_gemv<FmtQ6KRaw, 1, 2, 1, 1024, 0> (quantize t + down)", "avg_launch_us": round(dn_ms * 1e3, 3),
+        "down_gemv": {"kernel": "k_gemv<FmtQ6KRaw, 1, 2, 1, 1024, 9216> (quantize t + down)", "avg_launch_us": round(dn_ms * 1e3, 3),
                       "GBps": round(gbs(dn_bytes, dn_ms), 1)},
         "decode_ffn_unfused": unfused,
         "gemv_config1_3072x3072": c1_obj,
