@@ -1073,9 +1073,10 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
             return hipGetLastError();
         }
     }
-    // Q6_K raw at the down (K = 9216, verify rows) and lm_head (K = 3072, one row) shapes
-    if constexpr (QN == 0 && !PAIR && std::is_same<F, FmtQ6KRaw>::value) {
-        if constexpr (SPS == 3 && MR > 1 && MR <= 5) {
+    // Q6_K (raw and W160) at the down (K = 9216, verify rows) and lm_head
+    // (K = 3072, one row) shapes
+    if constexpr (QN == 0 && !PAIR && !std::is_same<F, FmtQ5K>::value) {
+        if constexpr (SPS == 3 && MR > 1) {
             if (waves == 4 && K == 9216 && KS == kc_ks(K, SPS)) {
                 launch_kernel((k_gemv<F, MR, SPS, QN, 256, 9216, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K,
                               KS, xq, xd, xsum, fq);
@@ -1089,7 +1090,7 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
                 return hipGetLastError();
             }
         }
-        if constexpr (SPS == 2 && MR >= 6) {
+        if constexpr (SPS == 2 && MR > 1) {
             if (waves == 16 && K == 9216 && KS == kc_ks(K, SPS)) {
                 launch_kernel((k_gemv<F, MR, SPS, QN, 1024, 9216, PAIR>), dim3(blocks), dim3(1024), lds, st, ptl, K,
                               KS, xq, xd, xsum, fq);
