@@ -198,23 +198,24 @@ def test_q6k_gemv(bq, oracle, N, K, rows):
         assert oracle.normwise_err(host(y3), ref) < TOL
 
 
-@pytest.mark.parametrize("fmt", ["q5k", "q6k_raw", "q6k_rep"])
+@pytest.mark.parametrize("fmt", ["q5k", "q5k_k4096", "q5k_n6912", "q6k_raw", "q6k_rep"])
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_multirow_every_row_count(bq, oracle, fmt, rows):
     """Every multi-row instance (dot4 below, matrix-core dot products from 6
     rows for Q5_K and from 3 for Q6_K, partial last set of four rows
-    included) against the oracle."""
+    included) against the oracle.  The Q5_K shapes reach the compile-time-K
+    instances with one (small N), two (rows 5, N*K >= 20M) and three steps per
+    wave, at K = 3072 and 4096."""
     import torch
-    if fmt == "q5k":
-        K, N = 3072, 528
-    else:
-        K, N = 9216, 132
-    raw = weights(1000 + rows, N, K, "q5k" if fmt == "q5k" else "q6k")
+    print(f"multirow {fmt} rows={rows}", flush=True)
+    K, N = {"q5k": (3072, 528), "q5k_k4096": (4096, 528), "q5k_n6912": (3072, 6912)}.get(fmt, (9216, 132))
+    q5 = fmt.startswith("q5k")
+    raw = weights(1000 + rows, N, K, "q5k" if q5 else "q6k")
     _, (xq, xd, xs) = acts(1010 + rows, rows, K)
     g = dev(raw)
     gq, gd, gs = _xq_dev(xq, xd, xs)
     y = torch.full((rows, N), float("nan"), device="cuda")
-    if fmt == "q5k":
+    if q5:
         assert bq.verify_fused([y], [bq.make_weight(g, bq.TYPE_Q5_K, K, N)], rows, gq, gd, gs) == bq.BQ_OK
         ref = oracle.gemm_q5k(raw, xq, xd, xs)
     elif fmt == "q6k_raw":
