@@ -11,7 +11,9 @@
 
 #include <algorithm>
 #include <cmath>
+#include <map>
 #include <mutex>
+#include <utility>
 
 #include "../../include/bq.h"
 #include "bq_internal.hpp"
@@ -327,6 +329,31 @@ int bq_gate_up_silu(float* h, const bq_weight* wg, const bq_weight* wu, const fl
 }
 
 namespace {
+// K-split workspace of the single-token-tile W144 GEMM: 8M floats (32 MiB)
+// per (device, stream), allocated on the first split on that stream outside
+// graph capture (during a capture without one the GEMM runs unsplit).  One
+// per stream, so GEMMs on different streams never share it; calls on one
+// stream use it in stream order.
+constexpr size_t kSplitWsFloats = 8u << 20;
+float* splitk_ws(hipStream_t st) {
+    static std::mutex mu;
+    static std::map<std::pair<int, hipStream_t>, float*> ws;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = ws.find({dev, st});
+    if (it != ws.end()) return it->second;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    float* p = nullptr;
+    if (hipMalloc(&p, kSplitWsFloats * sizeof(float)) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    ws[{dev, st}] = p;
+    return p;
+}
+
 // The MMQ launch behind bq_try_mmq and the bq_gemm_b dispatchers.  min_w144 /
 // min_raw: the smallest row count taken by the prepacked / raw tier (below
 // it BQ_UNSUPPORTED, nothing enqueued).
@@ -359,18 +386,20 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
         }
         hipError_t e = launch_fill_xdh(xd, xsum, rows * (K / 32), xdh, s);
         if (e != hipSuccess) return from_hip(e);
-        return from_hip(launch_mmq_q5k_144(pt, rows, K, xq, xd, xdh, s));
+        float* sw = (rows <= 128 && nparts == 1) ? splitk_ws(s) : nullptr;
+        return from_hip(launch_mmq_q5k_144(pt, rows, K, xq, xd, xdh, s, sw, sw ? kSplitWsFloats : 0));
     }
     for (int p = 0; p < nparts; ++p) pt.W[p] = ws[p]->raw;
     return from_hip(launch_mmq_q5k_raw(pt, rows, K, xq, xd, xsum, s));
 }
 
-// bq_gemm_b / bq_gemm_b_fused: one 128-row MMQ tile costs the same for any
-// row count up to 128 (9216 x 3072: 53 us prepacked, 64 us raw), while the
-// 8-row GEMV chunks stream the weights once per chunk (48 rows 57 us, 95 rows
-// 108 us): the tile wins from 44 rows prepacked and 56 rows raw.  (The
-// reference sends rows 9..95 to its 64x64 MMA tile.)
-constexpr int kGemmBMmqW144 = 44;
+// bq_gemm_b / bq_gemm_b_fused: one 128-row MMQ tile costs about the same for
+// any row count up to 128 (9216 x 3072: 22-30 us prepacked with the K split
+// of a single token tile, 64 us raw), while the 8-row GEMV chunks stream the
+// weights once per chunk (16 rows 18 us, 24 rows 27 us, 48 rows 57 us): the
+// tile wins from 17 rows prepacked and 56 rows raw.  (The reference sends
+// rows 9..95 to its 64x64 MMA tile.)
+constexpr int kGemmBMmqW144 = 17;
 constexpr int kGemmBMmqRaw = 56;
 }  // namespace
 

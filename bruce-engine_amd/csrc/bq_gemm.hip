@@ -28,6 +28,8 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
+
 namespace bq {
 
 constexpr int kTM = 128;   // tokens per tile
@@ -451,7 +453,7 @@ BQ_DEV void mmq144_stage(const SmemStage& sb, f32x16 (&acc)[2][2], int wn, int w
 
 __global__ void __launch_bounds__(256, 2)
 k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
-           const float* __restrict__ xd, const uint16_t* __restrict__ xdh) {
+           const float* __restrict__ xd, const uint16_t* __restrict__ xdh, int ksplit, float* __restrict__ part) {
     __shared__ __attribute__((aligned(16))) SmemStage sm0;
     __shared__ __attribute__((aligned(16))) SmemStage sm1;
     TileMap tm;
@@ -467,13 +469,16 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
     const int wn = wave >> 1, wm = wave & 1;
     const int l32 = lane & 31, lh = lane >> 5;
     auto wsrc = [&](int s) { return W + ((size_t)s * Nloc + nbase) * kW144; };
+    // K split (blockIdx.y of ksplit): stage pairs [s0, s1) of this slice
+    const int kc = blockIdx.y;
+    const int s0 = 2 * (kc * (nst / 2) / ksplit), s1 = 2 * ((kc + 1) * (nst / 2) / ksplit);
     Mmq144Dma dof;
     dof.tok_hi = lane >> 3;
     dof.w_off = 16 * lane;
     dof.x_off = (uint32_t)(lane >> 3) * (uint32_t)K + 16u * (uint32_t)((lane & 7) ^ (lane >> 3));
     dof.xd_off = (uint32_t)lane * (uint32_t)(nb * 4);
 
-    mmq144_dma(sm0, wsrc(0), xq, xd, dof, m0, rows, K, nb, 0, wave, lane);
+    mmq144_dma(sm0, wsrc(s0), xq, xd, dof, m0, rows, K, nb, s0, wave, lane);
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -483,7 +488,8 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
     // min term: sum_g f16(Dm[n][g]) * f16(xdh[m][g]) on fp16 MFMA, K/32 % 16 == 0
-    {
+    // (the first K slice only)
+    if (kc == 0) {
         const uint16_t* __restrict__ Dm = (const uint16_t*)pt.aux[p];
         for (int g0 = 0; g0 < nb; g0 += 16) {
             f16x8 a[2], b[2];
@@ -505,21 +511,22 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
         }
     }
 
-    for (int s = 0; s < nst; s += 2) {
+    for (int s = s0; s < s1; s += 2) {
         BQ_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (s + 1 < nst) mmq144_dma(sm1, wsrc(s + 1), xq, xd, dof, m0, rows, K, nb, s + 1, wave, lane);
+        if (s + 1 < s1) mmq144_dma(sm1, wsrc(s + 1), xq, xd, dof, m0, rows, K, nb, s + 1, wave, lane);
         mmq144_stage(sm0, acc, wn, wm, l32, lh);
-        if (s + 1 >= nst) break;
+        if (s + 1 >= s1) break;
         BQ_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (s + 2 < nst) mmq144_dma(sm0, wsrc(s + 2), xq, xd, dof, m0, rows, K, nb, s + 2, wave, lane);
+        if (s + 2 < s1) mmq144_dma(sm0, wsrc(s + 2), xq, xd, dof, m0, rows, K, nb, s + 2, wave, lane);
         mmq144_stage(sm1, acc, wn, wm, l32, lh);
     }
 
-    float* __restrict__ Y = pt.Y[p];
+    // K split: slice kc's partial sums go to part[kc][rows][N] (one part only)
+    float* __restrict__ Y = ksplit > 1 ? part + (size_t)kc * rows * Nloc : pt.Y[p];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
         const int m = m0 + wm * 64 + mt * 32 + l32;
@@ -865,13 +872,44 @@ static dim3 mmq_grid(int ntm, int ntn) {
     return dim3(per * kXcds);
 }
 
+// y = sum over the K slices of part[k] (fixed order), 4 floats per thread
+__global__ void __launch_bounds__(256) k_sum_splits(const float* __restrict__ part, int ks, size_t n4,
+                                                   float* __restrict__ y) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    f32x4 v = ((const f32x4*)part)[i];
+    for (int k = 1; k < ks; ++k) v = v + ((const f32x4*)part)[(size_t)k * n4 + i];
+    ((f32x4*)y)[i] = v;
+}
+
+// A single token tile leaves most of the 512 workgroup slots (two per CU)
+// empty: it is split over K into up to kMaxKSplit slices when a workspace of
+// ws_floats floats is given, whose partial outputs one more launch sums in a
+// fixed order.
+#ifndef BQ_MMQ_MAX_KSPLIT
+#define BQ_MMQ_MAX_KSPLIT 8
+#endif
+constexpr int kMaxKSplit = BQ_MMQ_MAX_KSPLIT;
+
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                              const uint16_t* xdh, hipStream_t st) {
+                              const uint16_t* xdh, hipStream_t st, float* ws, size_t ws_floats) {
     const int ntm = (rows + kTM - 1) / kTM;
     const int ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    if (mmq_v2())
-        launch_kernel(k_mmq_w144, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xdh);
+    int ks = 1;
+    if (ws && mmq_v2() && pt.nparts == 1 && ntm == 1) {
+        ks = std::min(kMaxKSplit, std::max(1, 512 / ntn));
+        while (ks > 1 && ((size_t)ks * rows * pt.N[0] > ws_floats || (K >> 8) < ks)) --ks;
+    }
+    if (mmq_v2()) {
+        const dim3 grid(mmq_grid(ntm, ntn).x, ks);
+        launch_kernel(k_mmq_w144, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xdh, ks, ws);
+        if (ks > 1) {
+            const size_t n4 = (size_t)rows * pt.N[0] / 4;
+            launch_kernel(k_sum_splits, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (const float*)ws, ks,
+                          n4, pt.Y[0]);
+        }
+    }
     else
         launch_kernel((k_mmq_q5k<MmqMode::Q5W144>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
                       rows, K, xq, xd, (const int32_t*)nullptr, xdh);

@@ -454,11 +454,38 @@ def test_mmq_config4_full_slices(bq, oracle):
         assert oracle.normwise_err(yh[np.ix_(mi, ni)], ref) < TOL, prepacked
 
 
+@pytest.mark.parametrize("rows", [17, 100, 128])
+def test_mmq_w144_ksplit(bq, oracle, rows):
+    """The W144 GEMM over one token tile split into 8 K slices (3072 / 256 = 12
+    stage pairs; 8 weight-row tiles): against the oracle, and bit-identical
+    between two calls (the slices are summed in a fixed order)."""
+    import torch
+    K, N = 3072, 1024
+    print(f"mmq w144 k-split rows={rows}", flush=True)
+    raw = weights(1500 + rows, N, K, "q5k")
+    _, (xq, xd, xs) = acts(1501 + rows, rows, K)
+    gq, gd, gs = _xq_dev(xq, xd, xs)
+    xdh = torch.empty((rows, K // 32), dtype=torch.int16, device="cuda")
+    g = dev(raw)
+    w144, dm = bq.repack_q5k(g, K, N)
+    w = bq.make_weight(g, bq.TYPE_Q5_K, K, N, rep=w144, rep_min=dm)
+    y1 = torch.full((rows, N), float("nan"), device="cuda")
+    y2 = torch.full((rows, N), float("nan"), device="cuda")
+    bq.gemm_b(y1, w, rows, gq, gd, gs, xdh)
+    bq.gemm_b(y2, w, rows, gq, gd, gs, xdh)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(y1).view(np.uint32), host(y2).view(np.uint32))
+    r144, rdm = oracle.repack_q5k_144(raw, K)
+    ref = oracle.gemm_q5k_144(r144, rdm, xq, xd, oracle.fill_xdh(xd, xs), N)
+    assert oracle.normwise_err(host(y1), ref) < TOL
+
+
 # ---------------------------------------------------------------- dispatcher
-@pytest.mark.parametrize("rows", [3, 20, 43, 47, 60, 130])
+@pytest.mark.parametrize("rows", [3, 16, 17, 20, 43, 60, 130])
 def test_gemm_b_dispatch(bq, oracle, rows):
-    """bq_gemm_b: 8-row GEMV chunks below 44 rows (W144) / 56 rows (raw), the
-    MMQ tile from there; bq_try_mmq keeps the reference's rows >= 96."""
+    """bq_gemm_b: 8-row GEMV chunks below 17 rows (W144) / 56 rows (raw), the
+    MMQ tile from there (K-split for one token tile); bq_try_mmq keeps the
+    reference's rows >= 96."""
     import torch
     K, N = 1024, 256
     raw5 = weights(1400, N, K, "q5k")
@@ -471,12 +498,12 @@ def test_gemm_b_dispatch(bq, oracle, rows):
     bq.gemm_b(y, bq.make_weight(g5, bq.TYPE_Q5_K, K, N), rows, gq, gd, gs, xdh)
     torch.cuda.synchronize()
     assert oracle.normwise_err(host(y), oracle.gemm_q5k(raw5, xq, xd, xs)) < TOL
-    # prepacked: the W144 tile (fp16 min term) from 44 rows
+    # prepacked: the W144 tile (fp16 min term) from 17 rows
     w144, dm = bq.repack_q5k(g5, K, N)
     yp = torch.full((rows, N), float("nan"), device="cuda")
     bq.gemm_b(yp, bq.make_weight(g5, bq.TYPE_Q5_K, K, N, rep=w144, rep_min=dm), rows, gq, gd, gs, xdh)
     torch.cuda.synchronize()
-    if rows >= 44:
+    if rows >= 17:
         r144, rdm = oracle.repack_q5k_144(raw5, K)
         ref = oracle.gemm_q5k_144(r144, rdm, xq, xd, oracle.fill_xdh(xd, xs), N)
     else:
