@@ -415,7 +415,9 @@ int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, co
     if (int s = ensure_init()) return s;
     if (!weight_ok(w) || !y || !xq || !xd || rows < 1) return BQ_EINVAL;
     if (w->ggml_type != BQ_TYPE_Q6_K || !w->rep || (w->N % 128) != 0) return BQ_UNSUPPORTED;
-    return from_hip(launch_mmq_q6k(one_part(y, w->rep, w->N), rows, w->K, xq, xd, (hipStream_t)st));
+    float* sw = splitk_ws((hipStream_t)st);
+    return from_hip(launch_mmq_q6k(one_part(y, w->rep, w->N), rows, w->K, xq, xd, (hipStream_t)st, sw,
+                                   sw ? kSplitWsFloats : 0));
 }
 
 int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,

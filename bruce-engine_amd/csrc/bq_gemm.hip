@@ -777,7 +777,7 @@ BQ_DEV void q6_stage(const SmemQ6Stage& sb, f32x16 (&acc)[2][2], int wn, int wm,
 
 __global__ void __launch_bounds__(256, 2)
 k_mmq_q6k_dma(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
-              const float* __restrict__ xd) {
+              const float* __restrict__ xd, int ksplit, float* __restrict__ part) {
     __shared__ __attribute__((aligned(16))) SmemQ6Stage sm0;
     __shared__ __attribute__((aligned(16))) SmemQ6Stage sm1;
     TileMap tm;
@@ -807,7 +807,10 @@ k_mmq_q6k_dma(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
     o.s_off = (uint32_t)(lane >> 1) * row_bytes + 128u + 16u * (uint32_t)(lane & 1);
     o.xd_off = (uint32_t)lane * (uint32_t)(nb * 4);
 
-    q6_dma(sm0, wstage(0), row_bytes, xq, xd, o, m0, rows, K, nb, 0, wave, lane);
+    // K split (blockIdx.y of ksplit): stage pairs [s0, s1) of this slice
+    const int kc = blockIdx.y;
+    const int s0 = 2 * (kc * (nst / 2) / ksplit), s1 = 2 * ((kc + 1) * (nst / 2) / ksplit);
+    q6_dma(sm0, wstage(s0), row_bytes, xq, xd, o, m0, rows, K, nb, s0, wave, lane);
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -817,21 +820,22 @@ k_mmq_q6k_dma(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
-    for (int s = 0; s < nst; s += 2) {
+    for (int s = s0; s < s1; s += 2) {
         BQ_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (s + 1 < nst) q6_dma(sm1, wstage(s + 1), row_bytes, xq, xd, o, m0, rows, K, nb, s + 1, wave, lane);
+        if (s + 1 < s1) q6_dma(sm1, wstage(s + 1), row_bytes, xq, xd, o, m0, rows, K, nb, s + 1, wave, lane);
         q6_stage(sm0, acc, wn, wm, l32, lh);
-        if (s + 1 >= nst) break;
+        if (s + 1 >= s1) break;
         BQ_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (s + 2 < nst) q6_dma(sm0, wstage(s + 2), row_bytes, xq, xd, o, m0, rows, K, nb, s + 2, wave, lane);
+        if (s + 2 < s1) q6_dma(sm0, wstage(s + 2), row_bytes, xq, xd, o, m0, rows, K, nb, s + 2, wave, lane);
         q6_stage(sm1, acc, wn, wm, l32, lh);
     }
 
-    float* __restrict__ Y = pt.Y[p];
+    // K split: slice kc's partial sums go to part[kc][rows][N] (one part only)
+    float* __restrict__ Y = ksplit > 1 ? part + (size_t)kc * rows * Nloc : pt.Y[p];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
         const int m = m0 + wm * 64 + mt * 32 + l32;
@@ -926,7 +930,7 @@ hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, c
 }
 
 hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                          hipStream_t st) {
+                          hipStream_t st, float* ws, size_t ws_floats) {
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
     static int v = -1;  // BQ_MMQ_Q6_DMA=0: the register-staged kernel (dev A/B switch, read once)
@@ -934,9 +938,21 @@ hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const
         const char* e = getenv("BQ_MMQ_Q6_DMA");
         v = e ? atoi(e) : 1;
     }
-    if (v)
-        launch_kernel(k_mmq_q6k_dma, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd);
-    else
+    if (v) {
+        // the K split fills the 512 workgroup slots when the tiles do not
+        int ks = 1;
+        if (ws && pt.nparts == 1) {
+            ks = std::min(kMaxKSplit, std::max(1, 512 / (ntm * ntn)));
+            while (ks > 1 && ((size_t)ks * rows * pt.N[0] > ws_floats || (K >> 8) < ks)) --ks;
+        }
+        const dim3 grid(mmq_grid(ntm, ntn).x, ks);
+        launch_kernel(k_mmq_q6k_dma, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, ks, ws);
+        if (ks > 1) {
+            const size_t n4 = (size_t)rows * pt.N[0] / 4;
+            launch_kernel(k_sum_splits, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (const float*)ws, ks,
+                          n4, pt.Y[0]);
+        }
+    } else
         launch_kernel(k_mmq_q6k, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd);
     return hipGetLastError();
 }

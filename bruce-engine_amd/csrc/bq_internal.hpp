@@ -82,7 +82,7 @@ hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, c
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                               const uint16_t* xdh, hipStream_t st, float* ws = nullptr, size_t ws_floats = 0);
 hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                          hipStream_t st);
+                          hipStream_t st, float* ws = nullptr, size_t ws_floats = 0);
 
 // Q8_0 logits head (Q8S: 8 fp16 scales + 256 int8 per row and 256 values)
 constexpr int kQ8SMaxK = 4096;  // the GEMV keeps K/1024 activation chunks per lane in registers
