@@ -886,10 +886,10 @@ __global__ void __launch_bounds__(256) k_sum_splits(const float* __restrict__ pa
     ((f32x4*)y)[i] = v;
 }
 
-// A single token tile leaves most of the 512 workgroup slots (two per CU)
-// empty: it is split over K into up to kMaxKSplit slices when a workspace of
-// ws_floats floats is given, whose partial outputs one more launch sums in a
-// fixed order.
+// A launch with fewer tiles than the 512 workgroup slots (two per CU) leaves
+// CUs idle (one token tile of a 9216-row matrix: 72 tiles): it is split over
+// K into up to kMaxKSplit slices when a workspace of ws_floats floats is
+// given, whose partial outputs one more launch sums in a fixed order.
 #ifndef BQ_MMQ_MAX_KSPLIT
 #define BQ_MMQ_MAX_KSPLIT 8
 #endif
@@ -901,8 +901,8 @@ hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, c
     const int ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
     int ks = 1;
-    if (ws && mmq_v2() && pt.nparts == 1 && ntm == 1) {
-        ks = std::min(kMaxKSplit, std::max(1, 512 / ntn));
+    if (ws && mmq_v2() && pt.nparts == 1) {
+        ks = std::min(kMaxKSplit, std::max(1, 512 / (ntm * ntn)));
         while (ks > 1 && ((size_t)ks * rows * pt.N[0] > ws_floats || (K >> 8) < ks)) --ks;
     }
     if (mmq_v2()) {
