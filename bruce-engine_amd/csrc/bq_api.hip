@@ -390,17 +390,18 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
         return from_hip(launch_mmq_q5k_144(pt, rows, K, xq, xd, xdh, s, sw, sw ? kSplitWsFloats : 0));
     }
     for (int p = 0; p < nparts; ++p) pt.W[p] = ws[p]->raw;
-    return from_hip(launch_mmq_q5k_raw(pt, rows, K, xq, xd, xsum, s));
+    float* sw = nparts == 1 ? splitk_ws(s) : nullptr;
+    return from_hip(launch_mmq_q5k_raw(pt, rows, K, xq, xd, xsum, s, sw, sw ? kSplitWsFloats : 0));
 }
 
 // bq_gemm_b / bq_gemm_b_fused: one 128-row MMQ tile costs about the same for
-// any row count up to 128 (9216 x 3072: 22-30 us prepacked with the K split
-// of a single token tile, 64 us raw), while the 8-row GEMV chunks stream the
-// weights once per chunk (16 rows 18 us, 24 rows 27 us, 48 rows 57 us): the
-// tile wins from 17 rows prepacked and 56 rows raw.  (The reference sends
-// rows 9..95 to its 64x64 MMA tile.)
+// any row count up to 128 (9216 x 3072 with the K split of a single token
+// tile: 22-30 us prepacked, 30-34 us raw), while the 8-row GEMV chunks stream
+// the weights once per chunk (16 rows 18 us, 24 rows 27 us, 32 rows 36 us):
+// the tile wins from 17 rows prepacked and 28 rows raw.  (The reference
+// sends rows 9..95 to its 64x64 MMA tile.)
 constexpr int kGemmBMmqW144 = 17;
-constexpr int kGemmBMmqRaw = 56;
+constexpr int kGemmBMmqRaw = 28;
 }  // namespace
 
 int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int rows,

@@ -82,7 +82,7 @@ template <MmqMode MODE>
 __global__ void __launch_bounds__(256, 2)
 k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
           const float* __restrict__ xd, const int32_t* __restrict__ xsum,
-          const uint16_t* __restrict__ xdh) {
+          const uint16_t* __restrict__ xdh, int ksplit, float* __restrict__ part) {
     __shared__ __attribute__((aligned(16))) Smem sm;
     TileMap tm;
     if (!map_tile(blockIdx.x, ntm, ntn, tm)) return;
@@ -92,6 +92,9 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
     const uint8_t* __restrict__ W = (const uint8_t*)pt.W[p];
     const int m0 = tm.mt * kTM;
     const int nb = K >> 5, nst = K >> 7, nsb = K >> 8;
+    // K split (blockIdx.y of ksplit): stages [s0, s1) of this slice
+    const int kc = blockIdx.y;
+    const int s0 = kc * nst / ksplit, s1 = (kc + 1) * nst / ksplit;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wn = wave >> 1, wm = wave & 1;
@@ -105,8 +108,9 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
-    if constexpr (MODE == MmqMode::Q5W144) {
+    if (MODE == MmqMode::Q5W144 && kc == 0) {
         // min term: sum_g f16(Dm[n][g]) * f16(xdh[m][g]) on fp16 MFMA, K/32 % 16 == 0
+        // (the first K slice only)
         const uint16_t* __restrict__ Dm = (const uint16_t*)pt.aux[p];
         for (int g0 = 0; g0 < nb; g0 += 16) {
             f16x8 a[2], b[2];
@@ -234,8 +238,8 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
         }
     };
 
-    load_stage(0);
-    for (int s = 0; s < nst; ++s) {
+    load_stage(s0);
+    for (int s = s0; s < s1; ++s) {
         __syncthreads();  // everyone is done reading the previous stage
         store_stage(s);
         __syncthreads();
@@ -245,7 +249,7 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
             return;
         }
 #endif
-        if (s + 1 < nst) load_stage(s + 1);
+        if (s + 1 < s1) load_stage(s + 1);
 
         // Per group pair (q0, q0+1) and tile: the scale products ds[n] * xd[m]
         // of both groups come from one fp32 outer-product MFMA (32x32x1, two
@@ -305,7 +309,8 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
     }
 
     // ---- epilogue: Y[m][n], lane owns token column l32, rows 8*rg + 4*lh + 0..3
-    float* __restrict__ Y = pt.Y[p];
+    // K split: slice kc's partial sums go to part[kc][rows][N] (one part only)
+    float* __restrict__ Y = ksplit > 1 ? part + (size_t)kc * rows * Nloc : pt.Y[p];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
         const int m = m0 + wm * 64 + mt * 32 + l32;
@@ -916,16 +921,27 @@ hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, c
     }
     else
         launch_kernel((k_mmq_q5k<MmqMode::Q5W144>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
-                      rows, K, xq, xd, (const int32_t*)nullptr, xdh);
+                      rows, K, xq, xd, (const int32_t*)nullptr, xdh, 1, (float*)nullptr);
     return hipGetLastError();
 }
 
 hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                              const int32_t* xsum, hipStream_t st) {
+                              const int32_t* xsum, hipStream_t st, float* ws, size_t ws_floats) {
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    launch_kernel((k_mmq_q5k<MmqMode::Q5Raw>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
-                       rows, K, xq, xd, xsum, (const uint16_t*)nullptr);
+    int ks = 1;  // K split as in launch_mmq_q5k_144 (stage granularity)
+    if (ws && pt.nparts == 1) {
+        ks = std::min(kMaxKSplit, std::max(1, 512 / (ntm * ntn)));
+        while (ks > 1 && ((size_t)ks * rows * pt.N[0] > ws_floats || (K >> 7) < ks)) --ks;
+    }
+    const dim3 grid(mmq_grid(ntm, ntn).x, ks);
+    launch_kernel((k_mmq_q5k<MmqMode::Q5Raw>), grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xsum,
+                  (const uint16_t*)nullptr, ks, ws);
+    if (ks > 1) {
+        const size_t n4 = (size_t)rows * pt.N[0] / 4;
+        launch_kernel(k_sum_splits, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (const float*)ws, ks, n4,
+                      pt.Y[0]);
+    }
     return hipGetLastError();
 }
 

@@ -78,7 +78,7 @@ hipError_t launch_repack_q6k(const void* raw, int K, int N, void* w160, hipStrea
 
 // prefill GEMMs (128x128 tiles, int8 MFMA)
 hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                              const int32_t* xsum, hipStream_t st);
+                              const int32_t* xsum, hipStream_t st, float* ws = nullptr, size_t ws_floats = 0);
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                               const uint16_t* xdh, hipStream_t st, float* ws = nullptr, size_t ws_floats = 0);
 hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,

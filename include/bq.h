@@ -204,7 +204,7 @@ int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, co
 
 /* Prompt-batch dispatcher.  Replaces launch_gemm_b (bruce.cu:7428-7568): rows
  * <= 8 -> the verify / GEMV kernels above; Q5_K from 17 rows (W144 prepack)
- * or 56 rows (raw) and Q6_K W160 above 8 rows -> the MFMA GEMMs (one 128-row
+ * or 28 rows (raw) and Q6_K W160 above 8 rows -> the MFMA GEMMs (one 128-row
  * tile costs the same at any row count up to 128, the 8-row chunks stream the
  * weights once per chunk); otherwise 8-row chunks of the multi-row kernels.
  * (The reference sends rows 9..95 to a 64x64 MMA tile.)  Never returns

@@ -481,9 +481,9 @@ def test_mmq_w144_ksplit(bq, oracle, rows):
 
 
 # ---------------------------------------------------------------- dispatcher
-@pytest.mark.parametrize("rows", [3, 16, 17, 20, 43, 60, 130])
+@pytest.mark.parametrize("rows", [3, 16, 17, 20, 27, 28, 43, 60, 130])
 def test_gemm_b_dispatch(bq, oracle, rows):
-    """bq_gemm_b: 8-row GEMV chunks below 17 rows (W144) / 56 rows (raw), the
+    """bq_gemm_b: 8-row GEMV chunks below 17 rows (W144) / 28 rows (raw), the
     MMQ tile from there (K-split for one token tile); bq_try_mmq keeps the
     reference's rows >= 96."""
     import torch
