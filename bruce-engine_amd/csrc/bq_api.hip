@@ -386,11 +386,11 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
         }
         hipError_t e = launch_fill_xdh(xd, xsum, rows * (K / 32), xdh, s);
         if (e != hipSuccess) return from_hip(e);
-        float* sw = nparts == 1 ? splitk_ws(s) : nullptr;
+        float* sw = splitk_ws(s);
         return from_hip(launch_mmq_q5k_144(pt, rows, K, xq, xd, xdh, s, sw, sw ? kSplitWsFloats : 0));
     }
     for (int p = 0; p < nparts; ++p) pt.W[p] = ws[p]->raw;
-    float* sw = nparts == 1 ? splitk_ws(s) : nullptr;
+    float* sw = splitk_ws(s);
     return from_hip(launch_mmq_q5k_raw(pt, rows, K, xq, xd, xsum, s, sw, sw ? kSplitWsFloats : 0));
 }
 

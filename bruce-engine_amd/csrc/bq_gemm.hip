@@ -60,6 +60,17 @@ BQ_DEV bool map_tile(int b, int ntm, int ntn, TileMap& t) {
     return true;
 }
 
+// offset of slice kc, part p in the K-split workspace [slice][part][rows][N[part]]
+BQ_DEV size_t split_offset(const PartTable& pt, int p, int kc, int rows) {
+    size_t ntot = 0, off = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxParts; ++i) {
+        if (i < pt.nparts) ntot += pt.N[i];
+        if (i < p) off += pt.N[i];
+    }
+    return ((size_t)kc * ntot + off) * rows;
+}
+
 BQ_DEV int part_of_ntile(const PartTable& pt, int& nbase) {
     int p = 0;
 #pragma unroll
@@ -309,8 +320,8 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
     }
 
     // ---- epilogue: Y[m][n], lane owns token column l32, rows 8*rg + 4*lh + 0..3
-    // K split: slice kc's partial sums go to part[kc][rows][N] (one part only)
-    float* __restrict__ Y = ksplit > 1 ? part + (size_t)kc * rows * Nloc : pt.Y[p];
+    // K split: slice kc's partial sums go to part[kc][part p: rows x N[p]]
+    float* __restrict__ Y = ksplit > 1 ? part + split_offset(pt, p, kc, rows) : pt.Y[p];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
         const int m = m0 + wm * 64 + mt * 32 + l32;
@@ -530,8 +541,8 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
         mmq144_stage(sm1, acc, wn, wm, l32, lh);
     }
 
-    // K split: slice kc's partial sums go to part[kc][rows][N] (one part only)
-    float* __restrict__ Y = ksplit > 1 ? part + (size_t)kc * rows * Nloc : pt.Y[p];
+    // K split: slice kc's partial sums go to part[kc][part p: rows x N[p]]
+    float* __restrict__ Y = ksplit > 1 ? part + split_offset(pt, p, kc, rows) : pt.Y[p];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
         const int m = m0 + wm * 64 + mt * 32 + l32;
@@ -839,8 +850,8 @@ k_mmq_q6k_dma(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
         q6_stage(sm1, acc, wn, wm, l32, lh);
     }
 
-    // K split: slice kc's partial sums go to part[kc][rows][N] (one part only)
-    float* __restrict__ Y = ksplit > 1 ? part + (size_t)kc * rows * Nloc : pt.Y[p];
+    // K split: slice kc's partial sums go to part[kc][part p: rows x N[p]]
+    float* __restrict__ Y = ksplit > 1 ? part + split_offset(pt, p, kc, rows) : pt.Y[p];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
         const int m = m0 + wm * 64 + mt * 32 + l32;
@@ -883,13 +894,23 @@ static dim3 mmq_grid(int ntm, int ntn) {
 
 // y = sum over the K slices of part[k] (fixed order), 4 floats per thread
 __global__ void __launch_bounds__(256) k_sum_splits(const float* __restrict__ part, int ks, size_t n4,
-                                                   float* __restrict__ y) {
+                                                   size_t stride4, float* __restrict__ y) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n4) return;
     f32x4 v = ((const f32x4*)part)[i];
-    for (int k = 1; k < ks; ++k) v = v + ((const f32x4*)part)[(size_t)k * n4 + i];
+    for (int k = 1; k < ks; ++k) v = v + ((const f32x4*)part)[(size_t)k * stride4 + i];
     ((f32x4*)y)[i] = v;
 }
+
+static int ntotal(const PartTable& pt) {
+    int n = 0;
+    for (int p = 0; p < pt.nparts; ++p) n += pt.N[p];
+    return n;
+}
+
+// pick the K split of a launch of ntiles tiles (1 = none) and sum the slices afterwards
+static int pick_ksplit(const PartTable& pt, int ntiles, int rows, int pairs, float* ws, size_t ws_floats);
+static hipError_t sum_splits(const PartTable& pt, int ks, int rows, const float* ws, hipStream_t st);
 
 // A launch with fewer tiles than the 512 workgroup slots (two per CU) leaves
 // CUs idle (one token tile of a 9216-row matrix: 72 tiles): it is split over
@@ -905,19 +926,11 @@ hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, c
     const int ntm = (rows + kTM - 1) / kTM;
     const int ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    int ks = 1;
-    if (ws && mmq_v2() && pt.nparts == 1) {
-        ks = std::min(kMaxKSplit, std::max(1, 512 / (ntm * ntn)));
-        while (ks > 1 && ((size_t)ks * rows * pt.N[0] > ws_floats || (K >> 8) < ks)) --ks;
-    }
+    const int ks = mmq_v2() ? pick_ksplit(pt, ntm * ntn, rows, K >> 8, ws, ws_floats) : 1;
     if (mmq_v2()) {
         const dim3 grid(mmq_grid(ntm, ntn).x, ks);
         launch_kernel(k_mmq_w144, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xdh, ks, ws);
-        if (ks > 1) {
-            const size_t n4 = (size_t)rows * pt.N[0] / 4;
-            launch_kernel(k_sum_splits, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (const float*)ws, ks,
-                          n4, pt.Y[0]);
-        }
+        if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
     }
     else
         launch_kernel((k_mmq_q5k<MmqMode::Q5W144>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
@@ -929,19 +942,11 @@ hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, c
                               const int32_t* xsum, hipStream_t st, float* ws, size_t ws_floats) {
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    int ks = 1;  // K split as in launch_mmq_q5k_144 (stage granularity)
-    if (ws && pt.nparts == 1) {
-        ks = std::min(kMaxKSplit, std::max(1, 512 / (ntm * ntn)));
-        while (ks > 1 && ((size_t)ks * rows * pt.N[0] > ws_floats || (K >> 7) < ks)) --ks;
-    }
+    const int ks = pick_ksplit(pt, ntm * ntn, rows, K >> 7, ws, ws_floats);  // stage granularity
     const dim3 grid(mmq_grid(ntm, ntn).x, ks);
     launch_kernel((k_mmq_q5k<MmqMode::Q5Raw>), grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xsum,
                   (const uint16_t*)nullptr, ks, ws);
-    if (ks > 1) {
-        const size_t n4 = (size_t)rows * pt.N[0] / 4;
-        launch_kernel(k_sum_splits, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (const float*)ws, ks, n4,
-                      pt.Y[0]);
-    }
+    if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
     return hipGetLastError();
 }
 
@@ -956,20 +961,31 @@ hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const
     }
     if (v) {
         // the K split fills the 512 workgroup slots when the tiles do not
-        int ks = 1;
-        if (ws && pt.nparts == 1) {
-            ks = std::min(kMaxKSplit, std::max(1, 512 / (ntm * ntn)));
-            while (ks > 1 && ((size_t)ks * rows * pt.N[0] > ws_floats || (K >> 8) < ks)) --ks;
-        }
+        const int ks = pick_ksplit(pt, ntm * ntn, rows, K >> 8, ws, ws_floats);
         const dim3 grid(mmq_grid(ntm, ntn).x, ks);
         launch_kernel(k_mmq_q6k_dma, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, ks, ws);
-        if (ks > 1) {
-            const size_t n4 = (size_t)rows * pt.N[0] / 4;
-            launch_kernel(k_sum_splits, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (const float*)ws, ks,
-                          n4, pt.Y[0]);
-        }
+        if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
     } else
         launch_kernel(k_mmq_q6k, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd);
+    return hipGetLastError();
+}
+
+static int pick_ksplit(const PartTable& pt, int ntiles, int rows, int pairs, float* ws, size_t ws_floats) {
+    if (!ws) return 1;
+    int ks = std::min(kMaxKSplit, std::max(1, 512 / ntiles));
+    while (ks > 1 && ((size_t)ks * rows * ntotal(pt) > ws_floats || pairs < ks)) --ks;
+    return ks;
+}
+
+static hipError_t sum_splits(const PartTable& pt, int ks, int rows, const float* ws, hipStream_t st) {
+    const size_t stride4 = (size_t)rows * ntotal(pt) / 4;
+    size_t off = 0;
+    for (int p = 0; p < pt.nparts; ++p) {
+        const size_t n4 = (size_t)rows * pt.N[p] / 4;
+        launch_kernel(k_sum_splits, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, ws + off, ks, n4, stride4,
+                      pt.Y[p]);
+        off += (size_t)rows * pt.N[p];
+    }
     return hipGetLastError();
 }
 
