@@ -40,7 +40,7 @@ EXPORTS = [
     "bq_quantize_q8s_host", "bq_gemv_q8s", "bq_norm_q8", "bq_add_norm_q8", "bq_resid_q8",
     "bq_gate_norm_q8", "bq_silu_mul_norm_q8", "bq_gguf_open", "bq_gguf_close", "bq_gguf_n_tensors",
     "bq_gguf_find", "bq_gguf_tensor_info", "bq_gguf_kv_num", "bq_gguf_kv_str", "bq_gguf_read", "bq_gguf_load",
-    "bq_gemv_norm_fused", "bq_gate_up_silu",
+    "bq_gemv_norm_fused", "bq_gate_up_silu", "bq_gemm_workspace_bytes",
 ]
 
 
@@ -89,10 +89,11 @@ def load(path=LIB_PATH):
         "bq_q6_verify_fused": (I, [P, P, I, I, P, P, I, P]),
         "bq_gemm_q6k_dp": (I, [P, WP, I, P, P, I, P]),
         "bq_gemm_q6k_raw": (I, [P, WP, I, P, P, I, P]),
-        "bq_try_mmq": (I, [P, P, I, I, P, P, P, P, P]),
-        "bq_gemm_q6k_mma": (I, [P, WP, I, P, P, P]),
-        "bq_gemm_b": (I, [P, WP, I, P, P, P, P, P]),
-        "bq_gemm_b_fused": (I, [P, P, I, I, P, P, P, P, P]),
+        "bq_gemm_workspace_bytes": (S, [I, I, I]),
+        "bq_try_mmq": (I, [P, P, I, I, P, P, P, P, P, S, P]),
+        "bq_gemm_q6k_mma": (I, [P, WP, I, P, P, P, S, P]),
+        "bq_gemm_b": (I, [P, WP, I, P, P, P, P, P, S, P]),
+        "bq_gemm_b_fused": (I, [P, P, I, I, P, P, P, P, P, S, P]),
         "bq_repack_q5k": (I, [P, I, I, P, P, P]),
         "bq_repack_q5k_bytes": (S, [I, I]),
         "bq_repack_q5k_min_bytes": (S, [I, I]),
@@ -265,28 +266,58 @@ def gemm_q6k_raw(y, w, rows, xq, xd, xoff=0):
 
 
 # ---------------------------------------------------------------- prefill GEMM
-def try_mmq(ys, ws, rows, xq, xd, xsum, xdh=None):
+def workspace_bytes(rows, K, n_total):
+    """bq_gemm_workspace_bytes: K-split workspace that allows the full split."""
+    return int(load().bq_gemm_workspace_bytes(rows, K, n_total))
+
+
+def workspace(rows, K, n_total, device="cuda"):
+    """A K-split workspace for GEMMs of rows x (n_total = sum N) x K (None if
+    such a launch never splits).  Allocated by torch: libbq itself allocates
+    nothing."""
+    import torch
+    n = workspace_bytes(rows, K, n_total)
+    return torch.empty(n // 4, dtype=torch.float32, device=device) if n else None
+
+
+def _work(work, rows, K, n_total):
+    """work="auto": a fresh workspace sized for the full split (torch's
+    caching allocator keeps it stream-ordered); None: no split; a tensor: used
+    as given.  Returns (pointer, bytes, tensor kept alive by the caller)."""
+    if isinstance(work, str):
+        assert work == "auto"
+        work = workspace(rows, K, n_total)
+    if work is None:
+        return None, 0, None
+    return _ptr(work), work.numel() * work.element_size(), work
+
+
+def try_mmq(ys, ws, rows, xq, xd, xsum, xdh=None, work="auto"):
+    wp, wb, keep = _work(work, rows, ws[0].K, sum(w.N for w in ws))
     yarr, warr = _arrays(ys, ws)
-    r = load().bq_try_mmq(yarr, warr, len(ws), rows, _ptr(xq), _ptr(xd), _ptr(xsum), _ptr(xdh), _stream())
+    r = load().bq_try_mmq(yarr, warr, len(ws), rows, _ptr(xq), _ptr(xd), _ptr(xsum), _ptr(xdh), wp, wb, _stream())
     if r not in (BQ_OK, BQ_UNSUPPORTED):
         raise BqError(r, "bq_try_mmq")
     return r
 
 
-def gemm_q6k_mma(y, w, rows, xq, xd):
-    return _check(load().bq_gemm_q6k_mma(_ptr(y), ctypes.byref(w), rows, _ptr(xq), _ptr(xd), _stream()),
+def gemm_q6k_mma(y, w, rows, xq, xd, work="auto"):
+    wp, wb, keep = _work(work, rows, w.K, w.N)
+    return _check(load().bq_gemm_q6k_mma(_ptr(y), ctypes.byref(w), rows, _ptr(xq), _ptr(xd), wp, wb, _stream()),
                   "bq_gemm_q6k_mma")
 
 
-def gemm_b(y, w, rows, xq, xd, xsum, xdh=None):
+def gemm_b(y, w, rows, xq, xd, xsum, xdh=None, work="auto"):
+    wp, wb, keep = _work(work, rows, w.K, w.N)
     return _check(load().bq_gemm_b(_ptr(y), ctypes.byref(w), rows, _ptr(xq), _ptr(xd), _ptr(xsum),
-                                   _ptr(xdh), _stream()), "bq_gemm_b")
+                                   _ptr(xdh), wp, wb, _stream()), "bq_gemm_b")
 
 
-def gemm_b_fused(ys, ws, rows, xq, xd, xsum, xdh=None):
+def gemm_b_fused(ys, ws, rows, xq, xd, xsum, xdh=None, work="auto"):
+    wp, wb, keep = _work(work, rows, ws[0].K, sum(w.N for w in ws))
     yarr, warr = _arrays(ys, ws)
     return _check(load().bq_gemm_b_fused(yarr, warr, len(ws), rows, _ptr(xq), _ptr(xd), _ptr(xsum),
-                                         _ptr(xdh), _stream()), "bq_gemm_b_fused")
+                                         _ptr(xdh), wp, wb, _stream()), "bq_gemm_b_fused")
 
 
 # ---------------------------------------------------------------- repacks

@@ -11,9 +11,7 @@
 
 #include <algorithm>
 #include <cmath>
-#include <map>
 #include <mutex>
-#include <utility>
 
 #include "../../include/bq.h"
 #include "bq_internal.hpp"
@@ -41,22 +39,13 @@ int ensure_init() {
         if (hipGetDeviceProperties(&prop, dev) != hipSuccess) { g_init_status = -(int)hipErrorNoDevice; return; }
         g_dev.lds_per_block = prop.sharedMemPerBlock;
         g_dev.cus = prop.multiProcessorCount;
-        gemv_set_cus(g_dev.cus);
         q8s_set_cus(g_dev.cus);
     });
     return g_init_status;
 }
 
-// try_launch_mmq's row threshold (bruce.cu:7369: rows >= 96); BQ_MMQ_MIN_ROWS
-// overrides it (a dev A/B switch, read once)
-int mmq_min_rows() {
-    static int v = -1;
-    if (v < 0) {
-        const char* e = getenv("BQ_MMQ_MIN_ROWS");
-        v = e ? std::max(9, atoi(e)) : 96;
-    }
-    return v;
-}
+// try_launch_mmq's row threshold (bruce.cu:7369: rows >= 96)
+constexpr int kMmqMinRows = 96;
 
 bool weight_ok(const bq_weight* w) { return w && w->K > 0 && w->N > 0 && (w->K % 256) == 0; }
 
@@ -329,39 +318,18 @@ int bq_gate_up_silu(float* h, const bq_weight* wg, const bq_weight* wu, const fl
 }
 
 namespace {
-// K-split workspace of the single-token-tile W144 GEMM: 8M floats (32 MiB)
-// per (device, stream), allocated on the first split on that stream outside
-// graph capture (during a capture without one the GEMM runs unsplit).  One
-// per stream, so GEMMs on different streams never share it; calls on one
-// stream use it in stream order.
-constexpr size_t kSplitWsFloats = 8u << 20;
-float* splitk_ws(hipStream_t st) {
-    static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, float*> ws;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> lk(mu);
-    auto it = ws.find({dev, st});
-    if (it != ws.end()) return it->second;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-    float* p = nullptr;
-    if (hipMalloc(&p, kSplitWsFloats * sizeof(float)) != hipSuccess) {
-        (void)hipGetLastError();
-        return nullptr;
-    }
-    ws[{dev, st}] = p;
-    return p;
-}
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // The MMQ launch behind bq_try_mmq and the bq_gemm_b dispatchers.  min_w144 /
 // min_raw: the smallest row count taken by the prepacked / raw tier (below
-// it BQ_UNSUPPORTED, nothing enqueued).
+// it BQ_UNSUPPORTED, nothing enqueued).  work / work_bytes: the caller's K-split
+// workspace (NULL / 0: no split).
 int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int rows, const int8_t* xq,
-                 const float* xd, const int32_t* xsum, uint16_t* xdh, bq_stream_t st, int min_w144,
-                 int min_raw) {
+                 const float* xd, const int32_t* xsum, uint16_t* xdh, void* work, size_t work_bytes,
+                 bq_stream_t st, int min_w144, int min_raw) {
     if (nparts < 1 || nparts > BQ_MAX_PARTS || rows < std::min(min_w144, min_raw)) return BQ_UNSUPPORTED;
     if (!ys || !ws || !ws[0] || !xq || !xd || !xsum) return BQ_EINVAL;
+    if (!al16(work) || !al16(xq)) return BQ_EINVAL;
     const int K = ws[0]->K;
     PartTable pt;
     memset(&pt, 0, sizeof(pt));
@@ -370,6 +338,7 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
         const bq_weight* w = ws[p];
         if (!w || !w->raw || !ys[p] || w->ggml_type != BQ_TYPE_Q5_K) return BQ_UNSUPPORTED;
         if (w->K != K || w->N <= 0 || (w->N % 128) != 0) return BQ_UNSUPPORTED;
+        if (!al16(ys[p])) return BQ_EINVAL;  // the tiles store 16-byte vectors
         if (!w->rep || !w->rep_min || (K % 512) != 0) prepacked = false;
         pt.Y[p] = ys[p];
         pt.N[p] = w->N;
@@ -379,6 +348,8 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
     if (rows < (prepacked ? min_w144 : min_raw)) return BQ_UNSUPPORTED;
     pt.nparts = nparts;
     hipStream_t s = (hipStream_t)st;
+    float* wf = (float*)work;
+    const size_t wn = work ? work_bytes / sizeof(float) : 0;
     if (prepacked) {
         for (int p = 0; p < nparts; ++p) {
             pt.W[p] = ws[p]->rep;
@@ -386,12 +357,10 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
         }
         hipError_t e = launch_fill_xdh(xd, xsum, rows * (K / 32), xdh, s);
         if (e != hipSuccess) return from_hip(e);
-        float* sw = splitk_ws(s);
-        return from_hip(launch_mmq_q5k_144(pt, rows, K, xq, xd, xdh, s, sw, sw ? kSplitWsFloats : 0));
+        return from_hip(launch_mmq_q5k_144(pt, rows, K, xq, xd, xdh, s, wf, wn));
     }
     for (int p = 0; p < nparts; ++p) pt.W[p] = ws[p]->raw;
-    float* sw = splitk_ws(s);
-    return from_hip(launch_mmq_q5k_raw(pt, rows, K, xq, xd, xsum, s, sw, sw ? kSplitWsFloats : 0));
+    return from_hip(launch_mmq_q5k_raw(pt, rows, K, xq, xd, xsum, s, wf, wn));
 }
 
 // bq_gemm_b / bq_gemm_b_fused: one 128-row MMQ tile costs about the same for
@@ -404,25 +373,31 @@ constexpr int kGemmBMmqW144 = 17;
 constexpr int kGemmBMmqRaw = 28;
 }  // namespace
 
+size_t bq_gemm_workspace_bytes(int rows, int K, int n_total) {
+    if (rows <= 0 || K <= 0 || n_total <= 0) return 0;
+    const int ks = mmq_ksplit(rows, K, n_total, true, (size_t)-1);
+    return ks > 1 ? (size_t)ks * rows * n_total * sizeof(float) : 0;
+}
+
 int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
                const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
-               bq_stream_t st) {
+               void* work, size_t work_bytes, bq_stream_t st) {
     if (int s = ensure_init()) return s;
-    return try_mmq_impl(ys, ws, nparts, rows, xq, xd, xsum, xdh, st, mmq_min_rows(), mmq_min_rows());
+    return try_mmq_impl(ys, ws, nparts, rows, xq, xd, xsum, xdh, work, work_bytes, st, kMmqMinRows, kMmqMinRows);
 }
 
 int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
-                    bq_stream_t st) {
+                    void* work, size_t work_bytes, bq_stream_t st) {
     if (int s = ensure_init()) return s;
     if (!weight_ok(w) || !y || !xq || !xd || rows < 1) return BQ_EINVAL;
+    if (!al16(y) || !al16(xq) || !al16(work)) return BQ_EINVAL;
     if (w->ggml_type != BQ_TYPE_Q6_K || !w->rep || (w->N % 128) != 0) return BQ_UNSUPPORTED;
-    float* sw = splitk_ws((hipStream_t)st);
-    return from_hip(launch_mmq_q6k(one_part(y, w->rep, w->N), rows, w->K, xq, xd, (hipStream_t)st, sw,
-                                   sw ? kSplitWsFloats : 0));
+    return from_hip(launch_mmq_q6k(one_part(y, w->rep, w->N), rows, w->K, xq, xd, (hipStream_t)st, (float*)work,
+                                   work ? work_bytes / sizeof(float) : 0));
 }
 
 int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
-              const int32_t* xsum, uint16_t* xdh, bq_stream_t st) {
+              const int32_t* xsum, uint16_t* xdh, void* work, size_t work_bytes, bq_stream_t st) {
     if (int s = ensure_init()) return s;
     if (!weight_ok(w) || !y || !xq || !xd || rows < 0) return BQ_EINVAL;
     if (rows == 0) return BQ_OK;
@@ -433,11 +408,11 @@ int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const fl
         if (q5) {
             float* ys[1] = {y};
             const bq_weight* wsp[1] = {w};
-            const int r = try_mmq_impl(ys, wsp, 1, rows, xq, xd, xsum, xdh, st, std::min(kGemmBMmqW144, mmq_min_rows()),
-                                       std::min(kGemmBMmqRaw, mmq_min_rows()));
+            const int r = try_mmq_impl(ys, wsp, 1, rows, xq, xd, xsum, xdh, work, work_bytes, st, kGemmBMmqW144,
+                                       kGemmBMmqRaw);
             if (r != BQ_UNSUPPORTED) return r;
         } else if (w->rep && (w->N % 128) == 0) {
-            return bq_gemm_q6k_mma(y, w, rows, xq, xd, st);
+            return bq_gemm_q6k_mma(y, w, rows, xq, xd, work, work_bytes, st);
         }
     }
     // 1..8-row kernels, in 8-row chunks
@@ -460,16 +435,16 @@ int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const fl
 
 int bq_gemm_b_fused(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
                     const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
-                    bq_stream_t st) {
+                    void* work, size_t work_bytes, bq_stream_t st) {
     if (int s = ensure_init()) return s;
     if (!ys || !ws || nparts < 1 || nparts > BQ_MAX_PARTS) return BQ_EINVAL;
     if (rows > BQ_MAX_ROWS) {
-        const int r = try_mmq_impl(ys, ws, nparts, rows, xq, xd, xsum, xdh, st,
-                                   std::min(kGemmBMmqW144, mmq_min_rows()), std::min(kGemmBMmqRaw, mmq_min_rows()));
+        const int r = try_mmq_impl(ys, ws, nparts, rows, xq, xd, xsum, xdh, work, work_bytes, st,
+                                   kGemmBMmqW144, kGemmBMmqRaw);
         if (r != BQ_UNSUPPORTED) return r;
     }
     for (int p = 0; p < nparts; ++p) {
-        const int r = bq_gemm_b(ys[p], ws[p], rows, xq, xd, xsum, xdh, st);
+        const int r = bq_gemm_b(ys[p], ws[p], rows, xq, xd, xsum, xdh, work, work_bytes, st);
         if (r != BQ_OK) return r;
     }
     return BQ_OK;
@@ -532,8 +507,6 @@ int bq_repack_q6k_host(const void* rawv, int K, int N, void* dstv) {
 // ---- q8 producers (norm + quantize) -----------------------------------------
 
 namespace {
-bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
-
 int norm_q8(int op, float* out, const float* a, const float* b, const float* c, const float* d, int rows,
             int n, int8_t* xq, float* xd, int32_t* xsum, bq_stream_t st) {
     if (int s = ensure_init()) return s;
@@ -613,8 +586,8 @@ uint16_t host_f2h_rn(float f) {
 }  // namespace
 
 // q8k_quant_host (bruce.cu:4843-4867): the same bytes as bq_quantize_q8s,
-// including groups with 0 < amax < 127/FLT_MAX (id = inf), where the device
-// kernels saturate to +-127.
+// including groups with 0 < amax < 127 * 2^-128 (id = inf), where the device
+// kernels follow __float2int_rn: zeros -> 0, other values -> +-127.
 int bq_quantize_q8s_host(const uint16_t* bf16, int K, int N, void* dstv) {
     if (K <= 0 || N < 0 || (K % 256) != 0) return BQ_EINVAL;
     if (N == 0) return BQ_OK;
@@ -637,10 +610,11 @@ int bq_quantize_q8s_host(const uint16_t* bf16, int K, int N, void* dstv) {
                 const uint16_t h = host_f2h_rn(d);
                 memcpy(blk + 2 * g, &h, 2);
                 for (int i = 0; i < 32; ++i) {
-                    // clamp before rounding: equal to round-then-clamp for finite v*id,
-                    // and saturating like the device kernel when id overflows to inf
-                    const float t = std::min(127.f, std::max(-127.f, v[i] * id));
-                    blk[16 + 32 * g + i] = (uint8_t)(int8_t)std::lrint(t);
+                    // __float2int_rn semantics (PTX cvt.rni): NaN (0 * inf, when id
+                    // overflows to inf) -> 0, +-inf saturates; then the clamp
+                    const float t = v[i] * id;
+                    const float c = t != t ? 0.f : std::min(127.f, std::max(-127.f, t));
+                    blk[16 + 32 * g + i] = (uint8_t)(int8_t)std::lrint(c);
                 }
             }
         }

@@ -140,14 +140,15 @@ int bqb_decode_ffn(int mode, int steps, int warmup, int nsets, const bq_weight* 
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// Prefill GEMM: `steps` launches of try_launch_mmq over the same inputs.
+// Prefill GEMM: `steps` launches of try_launch_mmq over the same inputs (no
+// K-split workspace: the config 4 launches fill the GPU unsplit).
 //   out[0] = timed region (ms), out[1] = sum of per-launch event times (ms).
 int bqb_gemm(int steps, int warmup, const bq_weight* w, int M, const int8_t* xq, const float* xd,
              const int32_t* xs, uint16_t* xdh, float* y, bq_stream_t st, double* out) {
     float* ys[1] = {y};
     const bq_weight* ws[1] = {w};
     for (int i = 0; i < warmup; ++i)
-        if (int r = bq_try_mmq(ys, ws, 1, M, xq, xd, xs, xdh, st)) return r;
+        if (int r = bq_try_mmq(ys, ws, 1, M, xq, xd, xs, xdh, nullptr, 0, st)) return r;
     EventPool pool((size_t)steps * 2 + 2);
     hipDeviceSynchronize();
     hipEventRecord(pool.ev[0], (hipStream_t)st);
@@ -155,7 +156,7 @@ int bqb_gemm(int steps, int warmup, const bq_weight* w, int M, const int8_t* xq,
         // the fill_xdh pre-pass of the W144 path is not timed: the event pair
         // brackets the GEMM kernel itself
         bq_time_next_launch(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
-        if (int r = bq_try_mmq(ys, ws, 1, M, xq, xd, xs, xdh, st)) return r;
+        if (int r = bq_try_mmq(ys, ws, 1, M, xq, xd, xs, xdh, nullptr, 0, st)) return r;
     }
     hipEventRecord(pool.ev[1], (hipStream_t)st);
     hipDeviceSynchronize();

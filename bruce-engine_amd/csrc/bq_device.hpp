@@ -42,14 +42,7 @@ BQ_DEV float as_float(uint32_t u) { return __builtin_bit_cast(float, u); }
 BQ_DEV int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 // 16-byte load of read-once weight data
-#ifdef BQ_EXP_NT
-BQ_DEV u32x4 ld16(const void* p) { return __builtin_nontemporal_load((const u32x4*)p); }
-#else
 BQ_DEV u32x4 ld16(const void* p) { return *(const u32x4*)p; }
-#endif
-BQ_DEV u32x4 ld16_stream(const void* p) {
-    return __builtin_nontemporal_load((const u32x4*)p);
-}
 
 // 16 bytes starting at a 2-byte aligned address, built from dword-aligned loads
 // (v_alignbyte_b32 funnel shift).  Reads only [p & ~3, p + 18) when p % 4 == 2,
@@ -101,6 +94,10 @@ BQ_DEV int wave_sum_i(int v) {
 // even) and the low byte of the sum's bit pattern is that integer in two's
 // complement.  The codes of the lane's 16 values are returned in q[0..3]
 // (little-endian bytes, value order).
+// A group with 0 < amax < 127 * 2^-128 has a denormal d and id = 1/d = inf.
+// The reference's __float2int_rn (PTX cvt.rni.s32.f32) turns v * id = NaN
+// (v = 0) into 0 and +-inf into +-INT_MAX, clamped to +-127; that group-wide
+// case is redone explicitly after the fast path (never taken otherwise).
 BQ_DEV void q8_quant16(const f32x4 (&v)[4], uint32_t (&q)[4], float& d, int& s) {
     float amax = 0.f;
 #pragma unroll
@@ -121,8 +118,22 @@ BQ_DEV void q8_quant16(const f32x4 (&v)[4], uint32_t (&q)[4], float& d, int& s) 
         const uint32_t lo = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, c1), __builtin_bit_cast(uint32_t, c0), 0x0C0C0400u);
         const uint32_t hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, c3), __builtin_bit_cast(uint32_t, c2), 0x0C0C0400u);
         q[i] = lo | (hi << 16);
-        acc = __builtin_amdgcn_sdot4((int)q[i], 0x01010101, acc, false);
     }
+    if (__builtin_expect(id > 3.402823466e38f, 0)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float x = v[i][e];
+                const uint32_t c = x > 0.f ? 0x7Fu : (x < 0.f ? 0x81u : 0u);
+                w |= c << (8 * e);
+            }
+            q[i] = w;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_sdot4((int)q[i], 0x01010101, acc, false);
     s = acc + __builtin_amdgcn_mov_dpp(acc, 0xB1, 0xF, 0xF, false);
 }
 

@@ -9,10 +9,11 @@
 //   * Workgroup = 4 waves, tile = 128 weight rows x 128 tokens, each wave a
 //     64x64 sub-tile of 2x2 v_mfma_i32_32x32x32_i8 (K = 32 = one Q5_K scale
 //     group per instruction, so the per-group scale is applied once per MFMA).
-//   * K advances in 128-value stages.  Weights and activations of a stage are
-//     staged in LDS with a 144-byte row stride (128 codes + 16 B pad: 4-dword
-//     bank offset per row, conflict-free 128-bit reads); the next stage is
-//     prefetched into registers while the current one is computed.
+//   * K advances in 128-value stages.  The raw tier stages a stage in LDS
+//     with a 144-byte row stride (128 codes + 16 B pad: 4-dword bank offset
+//     per row, conflict-free 128-bit reads) and prefetches the next stage into
+//     registers while the current one is computed; the W144 and Q6_K kernels
+//     copy stages with direct-to-LDS loads (below).
 //   * The k order inside an MFMA operand is irrelevant to the sum as long as A
 //     and B use the same order, so each lane simply loads 16 contiguous bytes.
 //   * Scales are staged q-major (sWs[q][row]) so a lane's 4 consecutive
@@ -38,13 +39,6 @@ constexpr int kRS = 144;   // LDS row stride (bytes)
 constexpr int kXcds = 8;
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-enum class MmqMode { Q5W144, Q5Raw };
-
-#ifdef BQ_MMQ_DEBUG
-__device__ uint8_t g_dbg[65536];
-extern "C" int bq_dbg_copy(void* dst) { return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_dbg), 65536); }
-#endif
 
 struct TileMap {
     int mt, nt;  // token tile, weight-row tile (over concatenated parts)
@@ -89,11 +83,10 @@ struct Smem {
     float xm[4 * kTM];         // raw: -(xd*xsum)  [q][tok]
 };
 
-template <MmqMode MODE>
 __global__ void __launch_bounds__(256, 2)
-k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
-          const float* __restrict__ xd, const int32_t* __restrict__ xsum,
-          const uint16_t* __restrict__ xdh, int ksplit, float* __restrict__ part) {
+k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
+              const float* __restrict__ xd, const int32_t* __restrict__ xsum, int ksplit,
+              float* __restrict__ part) {
     __shared__ __attribute__((aligned(16))) Smem sm;
     TileMap tm;
     if (!map_tile(blockIdx.x, ntm, ntn, tm)) return;
@@ -119,39 +112,12 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
-    if (MODE == MmqMode::Q5W144 && kc == 0) {
-        // min term: sum_g f16(Dm[n][g]) * f16(xdh[m][g]) on fp16 MFMA, K/32 % 16 == 0
-        // (the first K slice only)
-        const uint16_t* __restrict__ Dm = (const uint16_t*)pt.aux[p];
-        for (int g0 = 0; g0 < nb; g0 += 16) {
-            f16x8 a[2], b[2];
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const int n = nbase + wn * 64 + nt * 32 + l32;
-                a[nt] = *(const f16x8*)(Dm + (size_t)n * nb + g0 + 8 * lh);
-            }
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                const int m = m0 + wm * 64 + mt * 32 + l32;
-                if (m < rows) b[mt] = *(const f16x8*)(xdh + (size_t)m * nb + g0 + 8 * lh);
-                else b[mt] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-            }
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
-                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[nt], b[mt], acc[nt][mt], 0, 0, 0);
-        }
-    }
-
     // ---- register prefetch of one stage -------------------------------------
     // tokens: 1024 chunks of 16 B (tok = c >> 3, part = c & 7), 4 per thread;
     // token scales: threads 0..127 load xd[tok][4s..4s+3] (+ xsum for raw).
     u32x4 px[4];
     f32x4 pxd;
     i32x4 pxs;
-    // weights, W144: 1152 chunks of 16 B (row = c / 9, part = c % 9), <= 5 per thread
-    u32x4 pw[5];
     // weights, raw: thread -> (row = tid >> 1, 64-value half hv = tid & 1)
     u32x4 rqs0, rqs1, rqh0, rqh1, rhdr;
 
@@ -167,20 +133,13 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
             const int m = m0 + tid;
             if (m < rows) {
                 pxd = *(const f32x4*)(xd + (size_t)m * nb + 4 * s);
-                if constexpr (MODE == MmqMode::Q5Raw) pxs = *(const i32x4*)(xsum + (size_t)m * nb + 4 * s);
+                pxs = *(const i32x4*)(xsum + (size_t)m * nb + 4 * s);
             } else {
                 pxd = (f32x4){0.f, 0.f, 0.f, 0.f};
                 pxs = (i32x4){0, 0, 0, 0};
             }
         }
-        if constexpr (MODE == MmqMode::Q5W144) {
-            const uint8_t* src = W + ((size_t)s * Nloc + nbase) * kW144;
-#pragma unroll
-            for (int i = 0; i < 5; ++i) {
-                const int c = tid + 256 * i;
-                if (c < kTN * 9) pw[i] = ld16(src + 16 * c);
-            }
-        } else {
+        {
             const int row = tid >> 1, hv = tid & 1;
             const uint8_t* blk = W + ((size_t)(nbase + row) * nsb + (s >> 1)) * kQ5Bytes;
             const int j0 = 4 * (s & 1) + 2 * hv;  // sub-blocks j0, j0 + 1
@@ -201,26 +160,10 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
         if (tid < kTM) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) sm.xs[q * kTM + tid] = pxd[q];
-            if constexpr (MODE == MmqMode::Q5Raw) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) sm.xm[q * kTM + tid] = -(pxd[q] * (float)pxs[q]);
-            }
+            for (int q = 0; q < 4; ++q) sm.xm[q * kTM + tid] = -(pxd[q] * (float)pxs[q]);
         }
-        if constexpr (MODE == MmqMode::Q5W144) {
-#pragma unroll
-            for (int i = 0; i < 5; ++i) {
-                const int c = tid + 256 * i;
-                if (c < kTN * 9) {
-                    const int row = c / 9, part = c - 9 * row;
-                    if (part < 8) {
-                        *(u32x4*)(sm.w + row * kRS + 16 * part) = pw[i];
-                    } else {
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) sm.ws[q * kTN + row] = as_float(pw[i][q]);
-                    }
-                }
-            }
-        } else {
+        {
             const int row = tid >> 1, hv = tid & 1;
             const int j0 = 4 * (s & 1) + 2 * hv;
             // codes of sub-blocks j0 (low nibbles) and j0+1 (high nibbles), 32 each
@@ -254,12 +197,6 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
         __syncthreads();  // everyone is done reading the previous stage
         store_stage(s);
         __syncthreads();
-#ifdef BQ_MMQ_DEBUG
-        if (s == 0 && blockIdx.x == 0) {
-            for (int i = tid; i < (int)sizeof(Smem); i += 256) g_dbg[i] = ((const uint8_t*)&sm)[i];
-            return;
-        }
-#endif
         if (s + 1 < s1) load_stage(s + 1);
 
         // Per group pair (q0, q0+1) and tile: the scale products ds[n] * xd[m]
@@ -300,7 +237,7 @@ k_mmq_q5k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restr
                     }
                 }
         }
-        if constexpr (MODE == MmqMode::Q5Raw) {
+        {
             // exact fp32 min term of the stage's four groups: two K=2 MFMAs per tile
 #pragma unroll
             for (int qp = 0; qp < 2; ++qp) {
@@ -560,147 +497,8 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
 }
 
 // ---------------------------------------------------------------------------
-// Q6_K over the W160 repack: K = 16 MFMA per 16-value scale group.
-// ---------------------------------------------------------------------------
-struct SmemQ6 {
-    uint8_t w[kTN * kRS];
-    uint8_t x[kTM * kRS];
-    float ws[8 * kTN];  // d*sc per 16-group [g16][row]
-    float xs[4 * kTM];  // xd [q][tok]
-};
-
-__global__ void __launch_bounds__(256, 2)
-k_mmq_q6k(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
-          const float* __restrict__ xd) {
-    __shared__ __attribute__((aligned(16))) SmemQ6 sm;
-    TileMap tm;
-    if (!map_tile(blockIdx.x, ntm, ntn, tm)) return;
-    int nbase = tm.nt * kTN;
-    const int p = part_of_ntile(pt, nbase);
-    const int Nloc = pt.N[p];
-    const uint8_t* __restrict__ W = (const uint8_t*)pt.W[p];
-    const int m0 = tm.mt * kTM;
-    const int nb = K >> 5, nst = K >> 7;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wn = wave >> 1, wm = wave & 1;
-    const int l32 = lane & 31, lh = lane >> 5;
-
-    f32x16 acc[2][2];
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
-
-    u32x4 px[4], pw[5];
-    f32x4 pxd;
-    auto load_stage = [&](int s) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + 256 * i, tok = c >> 3, part = c & 7;
-            const int m = m0 + tok;
-            if (m < rows) px[i] = ld16(xq + (size_t)m * K + 128 * s + 16 * part);
-            else px[i] = (u32x4){0, 0, 0, 0};
-        }
-        if (tid < kTM) {
-            const int m = m0 + tid;
-            pxd = (m < rows) ? *(const f32x4*)(xd + (size_t)m * nb + 4 * s) : (f32x4){0.f, 0.f, 0.f, 0.f};
-        }
-        // 128 rows x 10 chunks: row = c / 10, part = c % 10
-#pragma unroll
-        for (int i = 0; i < 5; ++i) {
-            const int c = tid + 256 * i, row = c / 10, part = c - 10 * row;
-            pw[i] = ld16(W + ((size_t)(nbase + row) * nst + s) * kW160 + 16 * part);
-        }
-    };
-    auto store_stage = [&]() {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + 256 * i, tok = c >> 3, part = c & 7;
-            *(u32x4*)(sm.x + tok * kRS + 16 * part) = px[i];
-        }
-        if (tid < kTM) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) sm.xs[q * kTM + tid] = pxd[q];
-        }
-#pragma unroll
-        for (int i = 0; i < 5; ++i) {
-            const int c = tid + 256 * i, row = c / 10, part = c - 10 * row;
-            if (part < 8) {
-                *(u32x4*)(sm.w + row * kRS + 16 * part) = pw[i];
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    sm.ws[(4 * (part - 8) + e) * kTN + row] = as_float(pw[i][e]);
-            }
-        }
-    };
-
-    load_stage(0);
-    for (int s = 0; s < nst; ++s) {
-        __syncthreads();
-        store_stage();
-        __syncthreads();
-        if (s + 1 < nst) load_stage(s + 1);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            long a[2][2], b[2][2];  // [tile][16-group half]
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-                    a[nt][h] = *(const long*)(sm.w + (wn * 64 + nt * 32 + l32) * kRS + 32 * q + 16 * h + 8 * lh);
-#pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
-                    b[mt][h] = *(const long*)(sm.x + (wm * 64 + mt * 32 + l32) * kRS + 32 * q + 16 * h + 8 * lh);
-            }
-            // scale products of the two 16-value groups (2q, 2q+1) of this
-            // 32-group: one two-block fp32 outer-product MFMA per tile
-            float wsv[2], xsv[2];
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) wsv[nt] = sm.ws[(2 * q + lh) * kTN + wn * 64 + nt * 32 + l32];
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) xsv[mt] = sm.xs[q * kTM + wm * 64 + mt * 32 + l32];
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-                for (int mt = 0; mt < 2; ++mt) {
-                    const f32x32 zero32 = {0.f};
-                    const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(wsv[nt], xsv[mt], zero32, 0, 0, 0);
-                    const i32x16 zero = {0};
-                    const i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a[nt][0], b[mt][0], zero, 0, 0, 0);
-                    const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x16_i8(a[nt][1], b[mt][1], zero, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        acc[nt][mt][r] = __builtin_fmaf(sc[r], (float)d0[r], acc[nt][mt][r]);
-                        acc[nt][mt][r] = __builtin_fmaf(sc[16 + r], (float)d1[r], acc[nt][mt][r]);
-                    }
-                }
-        }
-    }
-
-    float* __restrict__ Y = pt.Y[p];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-        const int m = m0 + wm * 64 + mt * 32 + l32;
-        if (m >= rows) continue;
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int rg = 0; rg < 4; ++rg) {
-                const int n = nbase + wn * 64 + nt * 32 + 8 * rg + 4 * lh;
-                const f32x4 v = {acc[nt][mt][4 * rg], acc[nt][mt][4 * rg + 1], acc[nt][mt][4 * rg + 2],
-                                 acc[nt][mt][4 * rg + 3]};
-                *(f32x4*)(Y + (size_t)m * Nloc + n) = v;
-            }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Q6_K over W160, DMA-staged (the staging of k_mmq_w144 for the W160 layout;
-// the arithmetic is k_mmq_q6k's, instruction for instruction, so the results
-// are bit-identical to it).
+// Q6_K over W160 (k_gemm_mma_q6k_128 semantics: one K = 16 MFMA per 16-value
+// scale group), DMA-staged like k_mmq_w144.
 //   * W160 is row-major ([N][K/128][160]), so a stage's 128 rows are 160 B
 //     apart only within a row: the codes (bytes 0..127 of a row's stage) land
 //     128 B apart with 16-byte slot p of row r at p ^ f(r), f(r) = (r >> 1) & 7
@@ -869,37 +667,12 @@ k_mmq_q6k_dma(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
 }
 
 // ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
 static int ntile_count(const PartTable& pt) {
     int n = 0;
     for (int p = 0; p < pt.nparts; ++p) n += pt.N[p] / kTN;
     return n;
-}
-
-// W144 kernel choice (BQ_MMQ_V2 dev A/B switch, read once): 1 = k_mmq_w144,
-// 0 = the register-staged k_mmq_q5k<Q5W144>
-static int mmq_v2() {
-    static int v = -1;
-    if (v < 0) {
-        const char* e = getenv("BQ_MMQ_V2");
-        v = e ? atoi(e) : 1;
-    }
-    return v;
-}
-
-static dim3 mmq_grid(int ntm, int ntn) {
-    const int ntiles = ntm * ntn;
-    const int per = (ntiles + kXcds - 1) / kXcds;
-    return dim3(per * kXcds);
-}
-
-// y = sum over the K slices of part[k] (fixed order), 4 floats per thread
-__global__ void __launch_bounds__(256) k_sum_splits(const float* __restrict__ part, int ks, size_t n4,
-                                                   size_t stride4, float* __restrict__ y) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n4) return;
-    f32x4 v = ((const f32x4*)part)[i];
-    for (int k = 1; k < ks; ++k) v = v + ((const f32x4*)part)[(size_t)k * stride4 + i];
-    ((f32x4*)y)[i] = v;
 }
 
 static int ntotal(const PartTable& pt) {
@@ -908,33 +681,73 @@ static int ntotal(const PartTable& pt) {
     return n;
 }
 
-// pick the K split of a launch of ntiles tiles (1 = none) and sum the slices afterwards
-static int pick_ksplit(const PartTable& pt, int ntiles, int rows, int pairs, float* ws, size_t ws_floats);
-static hipError_t sum_splits(const PartTable& pt, int ks, int rows, const float* ws, hipStream_t st);
+static dim3 mmq_grid(int ntm, int ntn) {
+    const int ntiles = ntm * ntn;
+    const int per = (ntiles + kXcds - 1) / kXcds;
+    return dim3(per * kXcds);
+}
 
-// A launch with fewer tiles than the 512 workgroup slots (two per CU) leaves
-// CUs idle (one token tile of a 9216-row matrix: 72 tiles): it is split over
-// K into up to kMaxKSplit slices when a workspace of ws_floats floats is
-// given, whose partial outputs one more launch sums in a fixed order.
-#ifndef BQ_MMQ_MAX_KSPLIT
-#define BQ_MMQ_MAX_KSPLIT 8
-#endif
-constexpr int kMaxKSplit = BQ_MMQ_MAX_KSPLIT;
+// K split.  A launch with fewer tiles than the 512 workgroup slots (two per
+// CU) leaves CUs idle (one token tile of a 9216-row matrix: 72 tiles), so it
+// is split over K into up to kMaxKSplit slices of whole K units (stage pairs
+// for the DMA-staged kernels, stages for the raw tier) when the caller's
+// workspace holds the slices' partial outputs [slice][part][rows][N[part]];
+// one more launch sums them in a fixed order.  The choice depends only on the
+// shape and the workspace size, so equal calls take equal paths (eager or
+// captured in a graph) and give equal bits.
+constexpr int kMaxKSplit = 8;
+
+int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats) {
+    const int ntiles = ((rows + kTM - 1) / kTM) * (ntot / kTN);
+    if (ntiles <= 0) return 1;
+    const int units = stage_units ? (K >> 7) : (K >> 8);
+    int ks = std::min(kMaxKSplit, std::max(1, 512 / ntiles));
+    while (ks > 1 && ((size_t)ks * rows * ntot > ws_floats || units < ks)) --ks;
+    return ks;
+}
+
+// y_p = sum over the K slices of the workspace (fixed order), 4 floats per
+// thread over all parts of one launch: element i (in float4 units) of the
+// slice belongs to part p when off4[p] <= i < off4[p + 1]
+struct SumParts {
+    float* Y[kMaxParts];
+    size_t off4[kMaxParts + 1];
+};
+__global__ void __launch_bounds__(256) k_sum_splits(const float* __restrict__ ws, int ks, SumParts sp) {
+    const size_t n4 = sp.off4[kMaxParts];
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    f32x4 v = ((const f32x4*)ws)[i];
+    for (int k = 1; k < ks; ++k) v = v + ((const f32x4*)ws)[(size_t)k * n4 + i];
+    int p = 0;
+#pragma unroll
+    for (int q = 1; q < kMaxParts; ++q)
+        if (i >= sp.off4[q]) p = q;
+    ((f32x4*)sp.Y[p])[i - sp.off4[p]] = v;
+}
+
+static hipError_t sum_splits(const PartTable& pt, int ks, int rows, const float* ws, hipStream_t st) {
+    SumParts sp;
+    size_t off = 0;
+    for (int p = 0; p < kMaxParts; ++p) {
+        sp.off4[p] = off;
+        sp.Y[p] = p < pt.nparts ? pt.Y[p] : nullptr;
+        if (p < pt.nparts) off += (size_t)rows * pt.N[p] / 4;
+    }
+    sp.off4[kMaxParts] = off;
+    launch_kernel(k_sum_splits, dim3((unsigned)((off + 255) / 256)), dim3(256), 0, st, ws, ks, sp);
+    return hipGetLastError();
+}
 
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                               const uint16_t* xdh, hipStream_t st, float* ws, size_t ws_floats) {
     const int ntm = (rows + kTM - 1) / kTM;
     const int ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    const int ks = mmq_v2() ? pick_ksplit(pt, ntm * ntn, rows, K >> 8, ws, ws_floats) : 1;
-    if (mmq_v2()) {
-        const dim3 grid(mmq_grid(ntm, ntn).x, ks);
-        launch_kernel(k_mmq_w144, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xdh, ks, ws);
-        if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
-    }
-    else
-        launch_kernel((k_mmq_q5k<MmqMode::Q5W144>), mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn,
-                      rows, K, xq, xd, (const int32_t*)nullptr, xdh, 1, (float*)nullptr);
+    const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0);
+    const dim3 grid(mmq_grid(ntm, ntn).x, ks);
+    launch_kernel(k_mmq_w144, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xdh, ks, ws);
+    if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
     return hipGetLastError();
 }
 
@@ -942,10 +755,9 @@ hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, c
                               const int32_t* xsum, hipStream_t st, float* ws, size_t ws_floats) {
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    const int ks = pick_ksplit(pt, ntm * ntn, rows, K >> 7, ws, ws_floats);  // stage granularity
+    const int ks = mmq_ksplit(rows, K, ntotal(pt), true, ws ? ws_floats : 0);
     const dim3 grid(mmq_grid(ntm, ntn).x, ks);
-    launch_kernel((k_mmq_q5k<MmqMode::Q5Raw>), grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xsum,
-                  (const uint16_t*)nullptr, ks, ws);
+    launch_kernel(k_mmq_q5k_raw, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xsum, ks, ws);
     if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
     return hipGetLastError();
 }
@@ -954,38 +766,10 @@ hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const
                           hipStream_t st, float* ws, size_t ws_floats) {
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    static int v = -1;  // BQ_MMQ_Q6_DMA=0: the register-staged kernel (dev A/B switch, read once)
-    if (v < 0) {
-        const char* e = getenv("BQ_MMQ_Q6_DMA");
-        v = e ? atoi(e) : 1;
-    }
-    if (v) {
-        // the K split fills the 512 workgroup slots when the tiles do not
-        const int ks = pick_ksplit(pt, ntm * ntn, rows, K >> 8, ws, ws_floats);
-        const dim3 grid(mmq_grid(ntm, ntn).x, ks);
-        launch_kernel(k_mmq_q6k_dma, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, ks, ws);
-        if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
-    } else
-        launch_kernel(k_mmq_q6k, mmq_grid(ntm, ntn), dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd);
-    return hipGetLastError();
-}
-
-static int pick_ksplit(const PartTable& pt, int ntiles, int rows, int pairs, float* ws, size_t ws_floats) {
-    if (!ws) return 1;
-    int ks = std::min(kMaxKSplit, std::max(1, 512 / ntiles));
-    while (ks > 1 && ((size_t)ks * rows * ntotal(pt) > ws_floats || pairs < ks)) --ks;
-    return ks;
-}
-
-static hipError_t sum_splits(const PartTable& pt, int ks, int rows, const float* ws, hipStream_t st) {
-    const size_t stride4 = (size_t)rows * ntotal(pt) / 4;
-    size_t off = 0;
-    for (int p = 0; p < pt.nparts; ++p) {
-        const size_t n4 = (size_t)rows * pt.N[p] / 4;
-        launch_kernel(k_sum_splits, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, ws + off, ks, n4, stride4,
-                      pt.Y[p]);
-        off += (size_t)rows * pt.N[p];
-    }
+    const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0);
+    const dim3 grid(mmq_grid(ntm, ntn).x, ks);
+    launch_kernel(k_mmq_q6k_dma, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, ks, ws);
+    if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
     return hipGetLastError();
 }
 

@@ -45,14 +45,8 @@ constexpr int kQ5kMfmaMinRows = 6;
 // rows 3 / 4 / 8: W160 11.5 / 12.7 / 17.1 -> 11.0 / 11.7 / 14.8 us, raw
 // 10.0 / 11.2 / 16.1 -> 9.8 / 10.5 / 13.9 us; at 2 rows equal (W160) or
 // slower (raw 8.7 -> 9.2).
-#ifndef BQ_Q6REP_MFMA_MIN_ROWS
-#define BQ_Q6REP_MFMA_MIN_ROWS 3
-#endif
-constexpr int kQ6RepMfmaMinRows = BQ_Q6REP_MFMA_MIN_ROWS;
-#ifndef BQ_Q6RAW_MFMA_MIN_ROWS
-#define BQ_Q6RAW_MFMA_MIN_ROWS 3
-#endif
-constexpr int kQ6RawMfmaMinRows = BQ_Q6RAW_MFMA_MIN_ROWS;
+constexpr int kQ6RepMfmaMinRows = 3;
+constexpr int kQ6RawMfmaMinRows = 3;
 constexpr int kTasksPerStep = 16;  // tasks of one row per step
 
 BQ_DEV int find_part(const PartTable& pt, int tile) {
@@ -655,23 +649,6 @@ BQ_DEV void fp_produce(const f32x4 (&in)[4][4], uint8_t* smem, float* red, int K
     BQ_WAIT_LGKM0();
 }
 
-#ifdef BQ_EXP_TIMING
-// timing experiment: s_memrealtime stamps per wave of the last launch
-__device__ uint64_t g_tstamp[1 << 17];
-extern "C" int bq_tstamp_copy(void* dst, size_t bytes) {
-    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_tstamp), bytes);
-}
-#define BQ_TS(i)                                                                       \
-    do {                                                                               \
-        const uint64_t t_ = __builtin_amdgcn_s_memrealtime();                          \
-        if (lane == 0) g_tstamp[((size_t)blockIdx.x * waves + wave) * 8 + (i)] = t_;   \
-    } while (0)
-#else
-#define BQ_TS(i) \
-    do {         \
-    } while (0)
-#endif
-
 // ---------------------------------------------------------------------------
 // The kernel: blockDim.x / 64 = KS * RT waves per workgroup, a wave owns (tile
 // of 4 rows, K slice ks of KS), SPS steps of 16 tasks per row; MR activation
@@ -695,29 +672,8 @@ extern "C" int bq_tstamp_copy(void* dst, size_t bytes) {
 // 17.12 us.  Raising it only around the loads (1) gained about half of that.
 // Large grids (several rounds of workgroups: the 131072-row lm_head at 2..8
 // rows) lose with it (54.9 -> 58.0 us at 2 rows), so the launch sets it only
-// up to kPrioMaxBlocks workgroups.  BQ_GEMV_PRIO=0|1|2 is a dev A/B switch.
+// up to kPrioMaxBlocks workgroups.
 constexpr int kPrioMaxBlocks = 4096;
-#ifndef BQ_GEMV_PRIO
-#define BQ_GEMV_PRIO 2
-#endif
-// BQ_GEMV_LATE=0: the 9216-value fused rows also issue their weights before
-// the staging (measured slower: down 7.4 -> 8.0-8.2 us, with or without the
-// priority).  Issuing them once the wave's own fp32 row has landed, before
-// the quantization and the barrier, measured slower still (8.1 -> 9.2 us).
-#ifndef BQ_GEMV_LATE
-#define BQ_GEMV_LATE 1
-#endif
-// A compile-time-K instance for the fused / producer-fused 9216-value row over
-// 16-wave workgroups (the down projection; the launch's K split is kept):
-// fused down 8.0-8.4 -> 7.5-7.8 us, down + norm 10.1 -> 9.7-9.85 us, decode
-// FFN step 17.93 -> 17.50 us.  BQ_GEMV_DOWN_KC=0 builds without it.
-#ifndef BQ_GEMV_DOWN_KC
-#define BQ_GEMV_DOWN_KC 1
-#endif
-// BQ_GEMV_STEP_ORDER=0 builds the previous load order (a dev A/B switch)
-#ifndef BQ_GEMV_STEP_ORDER
-#define BQ_GEMV_STEP_ORDER 1
-#endif
 
 // K slices of a compile-time-K instance with SPS steps per wave
 __host__ __device__ constexpr int kc_ks(int K, int sps) { return ((K + 1023) / 1024 + sps - 1) / sps; }
@@ -749,7 +705,6 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
     const int waves = KC ? LB / 64 : blockDim.x >> 6;
     const int nb = K >> 5;
-    BQ_TS(0);
     // ---- 1. activations -> LDS (asynchronous), or this wave's fp32 chunks -> registers
     ActLds act;
     act.x = (const int8_t*)smem;
@@ -759,12 +714,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     constexpr int QA = QN > 0 ? QN : 1;
     f32x4 xv[QA][4];
     [[maybe_unused]] f32x4 pin[QN < 0 ? 4 : 1][4];
-    // (BQ_EXP_NOSTAGE / BQ_EXP_NOCOMPUTE: timing experiments that skip the
-    // activation staging / the dot products; results are meaningless)
-#if BQ_GEMV_PRIO
     if (pt.prio) __builtin_amdgcn_s_setprio(3);
-#endif
-#ifndef BQ_EXP_NOSTAGE
     if constexpr (QN > 0) {
         fq_load<QA>(xv, fq.x, K, wave, waves, lane);
     } else if constexpr (QN < 0) {
@@ -775,12 +725,8 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
         if constexpr (std::is_same<F, FmtQ5K>::value)
             dma_to_lds(smem + MR * K + MR * nb * 4, xsum, MR * nb * 4, wave, waves, lane);
     }
-#endif
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-#if BQ_GEMV_PRIO == 1
-    __builtin_amdgcn_s_setprio(0);
-#endif
 
     // ---- 2. this wave's weight loads, all issued now (addresses clamped so the
     //         instruction count is fixed; results of clamped lanes are unused)
@@ -805,31 +751,23 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     // a third of that and issuing the weights first measured faster (gate+up
     // 10.3 -> 9.8 us, whole stack 1.008 -> 0.998 ms/token, interleaved A/B).
     // q8 staging (DMA of a row the previous kernel just wrote) stays ahead of
-    // the weight loads.
-    constexpr bool kLate = QN != 0 && KC != 3072 && KC != 4096 && BQ_GEMV_LATE;
-// With the late weight issue, the first step's loads still go out before the
-// staging wait (down, 2 steps per wave: 8.18 -> 8.08 us in the decode step,
-// kernel-event medians 8.19 -> 7.97 over 6 interleaved pairs).
-#ifndef BQ_GEMV_LATE_EARLY
-#define BQ_GEMV_LATE_EARLY 1
-#endif
-    // steps whose loads go out before the staging wait (late: at least one step after it)
-    // (fused quantizer only: with a producer the first step's loads held up
-    // its reductions -- down + norm 9.99 -> 16.9 us)
-    constexpr int kEarly =
-        kLate ? (QN > 0 ? (BQ_GEMV_LATE_EARLY < SPS - 1 ? BQ_GEMV_LATE_EARLY : SPS - 1) : 0) : SPS;
-                                             // (issuing 1 or 2 of 3 early measured slower)
+    // the weight loads.  (Issuing all of them early for the 9216-value row
+    // measured slower: down 7.4 -> 8.0-8.2 us.)
+    constexpr bool kLate = QN != 0 && KC != 3072 && KC != 4096;
+    // Steps whose loads go out before the staging wait.  With the late issue
+    // the first step's loads still go out before it for the fused quantizer
+    // (down, 2 steps per wave: kernel-event medians 8.19 -> 7.97 us); with a
+    // producer they held up its reductions (down + norm 9.99 -> 16.9 us).
+    constexpr int kEarly = kLate ? (QN > 0 ? (1 < SPS - 1 ? 1 : SPS - 1) : 0) : SPS;
     auto issue_weights = [&](int s0, int s1) {
 #pragma unroll
         for (int s = 0; s < SPS; ++s) {
             if (s < s0 || s >= s1) continue;
             const int t = (ks * SPS + s) * kTasksPerStep + li;
             F::load(w[s], rowp, min(t, tpr - 1));
-#if BQ_GEMV_STEP_ORDER
             // keep the steps' loads in step order, so that step s waits only
             // for its own loads (left alone, the scheduler interleaves them)
             __builtin_amdgcn_sched_barrier(0);
-#endif
         }
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
@@ -838,19 +776,12 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
 
     // ---- 3. own DMA / fp32 loads done (only the weight loads may still be outstanding)
     BQ_WAIT_VM(F::kLoads * kEarly);
-    BQ_TS(1);
-#ifndef BQ_EXP_NOSTAGE
     if constexpr (QN > 0) fq_quantize<QA, std::is_same<F, FmtQ5K>::value>(xv, smem, K, wave, waves, lane, fq);
     if constexpr (QN < 0)
         fp_produce<std::is_same<F, FmtQ5K>::value>(pin, smem, part_sums + waves * MR * 4, K, wave, lane, fq);
-#endif
-    BQ_TS(2);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-#if BQ_GEMV_PRIO == 2
     __builtin_amdgcn_s_setprio(0);
-#endif
-    BQ_TS(3);
     if constexpr (kEarly < SPS) issue_weights(kEarly, SPS);
 
     // ---- 4. compute, step by step as the loads return
@@ -861,9 +792,6 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
 #pragma unroll
     for (int s = 0; s < SPS; ++s) {
         const int t = (ks * SPS + s) * kTasksPerStep + li;
-#ifdef BQ_EXP_NOCOMPUTE
-        if (rowok && t < tpr) acc[0] += as_float(((const uint32_t*)&w[s])[0] & 0x3F800000u);
-#else
         if constexpr (kMmLanes) {
             // every lane of the block takes part in the matrix instruction;
             // the lane's own contribution is dropped afterwards if not valid
@@ -881,11 +809,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
         } else {
             if (rowok && t < tpr) F::template dot<MR>(w[s], rowp, t, act, K, acc);
         }
-#endif
-        if (s == 0) BQ_TS(6);
-        if (s == 1) BQ_TS(7);
     }
-    BQ_TS(4);
     // ---- 5. row sums; K slices combined through LDS
     float* Y = pt.Y[p];
     if (KS == 1) {
@@ -900,7 +824,6 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
             const float v = kMmLanes ? lane4_sum(acc[m], li) : row16_sum(acc[m]);
             if (li == 15 && rowok) Y[(size_t)m * Nloc + row] = v;
         }
-        BQ_TS(5);
         return;
     }
 #pragma unroll
@@ -928,14 +851,11 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
             Y[(size_t)m * Nloc + row] = v;
         }
     }
-    BQ_TS(5);
 }
 
 // ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
-void gemv_set_cus(int) {}
-
 static void build_tiles(PartTable& pt, int rows_per_tile = kRowsPerTile) {
     int acc = 0;
     for (int p = 0; p < pt.nparts; ++p) {
@@ -967,14 +887,7 @@ static void build_tiles(PartTable& pt, int rows_per_tile = kRowsPerTile) {
 //       3 for 2..8 rows (8 rows 115 -> 85), 1 row 2 (60.0 -> 57.5)
 //     W160 3072 x 9216: 3 up to 2 rows (2 rows 10.2 -> 9.7), else 2 (rows * K
 //       >= 27K); 131072 x 3072: 3 for all rows (8 rows 121.6 -> 99)
-// BQ_GEMV_SPS=1|2|3 overrides the cap (a dev A/B switch, read once).
 int sps_cap(GemvKind kind, int K, long long N, int MR, bool fused) {
-    static int env = -1;
-    if (env < 0) {
-        const char* e = getenv("BQ_GEMV_SPS");
-        env = e ? std::max(1, std::min(3, atoi(e))) : 0;
-    }
-    if (env) return env;
     if (fused) return K > 4096 ? 2 : (N * K >= (20ll << 20) ? 3 : 1);
     // Q6_K: the staged activation bytes per workgroup (rows * K) decide
     if (kind == GemvKind::Q6KRaw) return MR == 1 ? (K <= 4096 ? 2 : 3) : (MR * K >= 48 * 1024 ? 2 : 3);
@@ -996,28 +909,13 @@ void k_split(int K, int cap, int& KS, int& SPS) {
 
 // Workgroup size: 4 waves while K needs at most 4 slices, else 16; the
 // workgroup holds RT = waves / KS row tiles and any remaining waves only share
-// the activation staging.  Dev A/B switches, read once: BQ_GEMV_WAVES sets the
-// wave count (0 = exactly KS * RT with the default RT), BQ_GEMV_RT sets RT for
-// single-row launches with KS > 1.
-static int gemv_waves(int KS, int MR) {
-    static int w = -1, rt = -1;
-    if (w < 0) {
-        const char* e = getenv("BQ_GEMV_WAVES");
-        w = e ? std::max(0, std::min(16, atoi(e))) : -2;
-        const char* r = getenv("BQ_GEMV_RT");
-        rt = r ? std::max(1, atoi(r)) : 0;
-    }
-    if (rt && MR == 1 && KS > 1) return std::min(16 / KS, rt) * KS;
-    const int def = KS <= 4 ? 4 : 16;
-    if (w == -2) return def;
-    if (w == 0) return KS * (def / KS);
-    return std::max(w, KS);
-}
+// the activation staging.
+static int gemv_waves(int KS) { return KS <= 4 ? 4 : 16; }
 
 template <class F, int MR, int SPS, int QN = 0, bool PAIR = false>
 static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* xq, const float* xd,
                              const int32_t* xsum, hipStream_t st, FusedQ8 fq = {}) {
-    int waves = gemv_waves(KS, MR);
+    int waves = gemv_waves(KS);
     // the producer needs a wave per 1024-value chunk
     if (QN < 0 && waves < (K + kChunk - 1) / kChunk) waves = 16;
     const int RT = waves / KS;  // the kernel derives the same from blockDim
@@ -1098,7 +996,6 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
             }
         }
     }
-#if BQ_GEMV_DOWN_KC
     // the fused / producer-fused 9216-value row over 16-wave workgroups (the down projection)
     if constexpr (MR == 1 && SPS == 2 && QN != 0 && !PAIR) {
         if (waves == 16 && K == 9216 && KS == kc_ks(K, SPS)) {
@@ -1107,12 +1004,8 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
             return hipGetLastError();
         }
     }
-#endif
     if (waves <= 4)
         launch_kernel((k_gemv<F, MR, SPS, QN, 256, 0, PAIR>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
-                      xq, xd, xsum, fq);
-    else if (waves <= 9 && MR == 1)
-        launch_kernel((k_gemv<F, MR, SPS, QN, 576, 0, PAIR>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
                       xq, xd, xsum, fq);
     else
         launch_kernel((k_gemv<F, MR, SPS, QN, 1024, 0, PAIR>), dim3(blocks), dim3(64 * waves), lds, st, ptl, K, KS,
@@ -1211,7 +1104,7 @@ hipError_t launch_gemv_silu_pair(GemvKind kind, PartTable pt, int K, const int8_
 // K split gives KS >= chunks / 3 and waves >= KS)
 template <class F, int SPS>
 static hipError_t dispatch_fused_qn(const PartTable& pt, int K, int KS, const FusedQ8& fq, hipStream_t st) {
-    const int waves = gemv_waves(KS, 1);
+    const int waves = gemv_waves(KS);
     const int qn = (K / kChunk + waves - 1) / waves;
     switch (qn) {
         case 0:

@@ -2,9 +2,12 @@
  * bq.h -- C ABI of the MI355X k-quant matmul path (libbq.so).
  *
  * Drop-in replacement for the quantized-matmul launchers of the reference
- * engine (engine/src/bruce.cu).  Every entry point is stream-ordered, allocates
- * nothing, never synchronises and never exits; all buffers are caller-owned
- * device memory (weights, q8 activations, outputs, repack targets).
+ * engine (engine/src/bruce.cu).  Every compute entry point is stream-ordered,
+ * allocates nothing, never synchronises and never exits; all buffers are
+ * caller-owned device memory (weights, q8 activations, outputs, repack
+ * targets, and the prefill GEMMs' scratch: xdh and the K-split workspace), as
+ * the reference preallocates its scratch once (alloc_buffers, bruce.cu:5525-5547).
+ * The GGUF loader (host file I/O) is the one exception, see below.
  *
  * Return codes: BQ_OK (0); BQ_UNSUPPORTED (1) = shape/type not handled, nothing
  * was enqueued and the caller should fall back (the reference's `return false`,
@@ -186,21 +189,36 @@ int bq_gemv_norm_fused(float* const* ys, const bq_weight* const* ws, int nparts,
                        float* xd, int32_t* xsum, bq_stream_t st);
 
 /* ---- prefill GEMM ----------------------------------------------------------
- * Y_p[M][N_p] for nparts (1..4) Q5_K matrices, 128x128 tiles on int8 MFMA.
+ * K-split workspace.  A GEMM whose 128x128 tiles leave the GPU's workgroup
+ * slots unfilled (e.g. one 128-token tile of a 9216-row matrix) is split over
+ * K; the slices' partial outputs go to a caller-owned workspace and one more
+ * launch sums them in a fixed order.  The split is chosen from the shape and
+ * work_bytes alone, so equal calls (eager or captured in a graph) take equal
+ * paths and give equal bits.  work = NULL (or too small) means a smaller or no
+ * split.  bq_gemm_workspace_bytes gives the size that allows the full split of
+ * a launch of `rows` activation rows over matrices of n_total = sum N_p rows
+ * (0: that launch never splits); it is at most 32 MiB for any shape.  work
+ * must be 16-byte aligned.  Calls that share a workspace must be ordered
+ * (one stream, or events): the workspace holds one call's partials at a time.
+ * No counterpart in the reference (its 128x128 GEMM never splits K). */
+size_t bq_gemm_workspace_bytes(int rows, int K, int n_total);
+
+/* Y_p[M][N_p] for nparts (1..4) Q5_K matrices, 128x128 tiles on int8 MFMA.
  * Replaces try_launch_mmq (bruce.cu:7366-7419).  rows >= 96 (the reference's
  * rule), N_p % 128 == 0, K % 256 == 0, else BQ_UNSUPPORTED.  If every part has
  * rep/rep_min and K % 512 == 0 the W144 kernel runs (k_gemm_mmq_q5k_144
  * :6604-6792, fp16 min term from Dm and xdh; xdh scratch [M][K/32] must be
  * given and is written first, as k_fill_xdh does); otherwise the raw-Q5_K
- * kernel runs (k_gemm_mmq_q5k :6367-6593, fp32 min term) and xdh is unused. */
+ * kernel runs (k_gemm_mmq_q5k :6367-6593, fp32 min term) and xdh is unused.
+ * ys and xq 16-byte aligned. */
 int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
                const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
-               bq_stream_t st);
+               void* work, size_t work_bytes, bq_stream_t st);
 
 /* Q6_K prefill GEMM over W160, rows >= 1, N % 128 == 0.  Replaces the
  * k_gemm_mma_q6k_128 arm of launch_gemm_b (bruce.cu:7475-7521; kernel :6943-7063). */
 int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
-                    bq_stream_t st);
+                    void* work, size_t work_bytes, bq_stream_t st);
 
 /* Prompt-batch dispatcher.  Replaces launch_gemm_b (bruce.cu:7428-7568): rows
  * <= 8 -> the verify / GEMV kernels above; Q5_K from 17 rows (W144 prepack)
@@ -210,12 +228,12 @@ int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, co
  * (The reference sends rows 9..95 to a 64x64 MMA tile.)  Never returns
  * BQ_UNSUPPORTED for a Q5_K/Q6_K weight with K % 256 == 0. */
 int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
-              const int32_t* xsum, uint16_t* xdh, bq_stream_t st);
+              const int32_t* xsum, uint16_t* xdh, void* work, size_t work_bytes, bq_stream_t st);
 /* launch_gemm_b_fused (bruce.cu:7421-7426): one MMQ launch over the parts if
  * possible (row thresholds of bq_gemm_b), otherwise bq_gemm_b per part. */
 int bq_gemm_b_fused(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
                     const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
-                    bq_stream_t st);
+                    void* work, size_t work_bytes, bq_stream_t st);
 
 /* ---- load-time repacks -----------------------------------------------------
  * Q5_K raw -> W144 + Dm (k_q5k_prepack144, bruce.cu:5747-5789, launched by

@@ -83,6 +83,18 @@ uint16_t orc_f2h_rn(float f) {
 /* ------------------------------------------------------------------------- */
 /* activation quantizer: bruce.cu:518-539 (k_q8_quant), :1081-1108 (k_q8_rows) */
 /* ------------------------------------------------------------------------- */
+/* __float2int_rn as the PTX ISA defines cvt.rni.s32.f32: round to nearest
+ * even, NaN -> 0, out-of-range values (infinities included) saturate to
+ * INT_MIN / INT_MAX.  The quantizer needs it when 0 < amax < 127 * 2^-128:
+ * d is then denormal and id = 1/d = inf, so v * id is NaN for v = 0 and
+ * +-inf otherwise. */
+static int cvt_rni(float f) {
+    if (f != f) return 0;
+    if (f >= 2147483648.f) return 2147483647;
+    if (f <= -2147483648.f) return -2147483647 - 1;
+    return (int)rintf(f);
+}
+
 void orc_q8_rows(const float* x, int M, int K, int8_t* xq, float* xd, int32_t* xsum) {
     const int nb = K / 32;
     for (int r = 0; r < M; ++r) {
@@ -94,7 +106,7 @@ void orc_q8_rows(const float* x, int M, int K, int8_t* xq, float* xd, int32_t* x
             const float id = d > 0.f ? 1.f / d : 0.f;
             int s = 0;
             for (int i = 0; i < 32; ++i) {
-                int v = (int)rintf(p[i] * id);
+                int v = cvt_rni(p[i] * id);
                 v = v < -127 ? -127 : (v > 127 ? 127 : v);
                 xq[(size_t)r * K + (size_t)b * 32 + i] = (int8_t)v;
                 s += v;
@@ -493,13 +505,12 @@ void orc_quantize_q8s(const uint16_t* bf16, int K, int N, uint8_t* dst) {
                 const uint16_t h = orc_f2h_rn(d);
                 memcpy(blk + 2 * g, &h, 2);
                 for (int i = 0; i < 32; ++i) {
-                    /* clamp, then round: the same as the reference's round-then-clamp
-                     * for every finite v*id; when 0 < amax < 127/FLT_MAX, id = inf and
-                     * the device kernel's __float2int_rn saturates (+-127) where the
-                     * host loop's lrintf(inf) is undefined -- the device result is kept. */
-                    float t = bf16_to_f32(p[i]) * id;
-                    t = t < -127.f ? -127.f : (t > 127.f ? 127.f : t);
-                    blk[16 + 32 * g + i] = (uint8_t)(int8_t)lrintf(t);
+                    /* the device kernel's __float2int_rn, then the clamp (the host
+                     * loop's lrintf(v*id) is undefined when id overflows to inf:
+                     * the device result is kept) */
+                    int v = cvt_rni(bf16_to_f32(p[i]) * id);
+                    v = v < -127 ? -127 : (v > 127 ? 127 : v);
+                    blk[16 + 32 * g + i] = (uint8_t)(int8_t)v;
                 }
             }
         }

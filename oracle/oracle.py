@@ -265,3 +265,18 @@ def normwise_err(y, ref):
     num = np.abs(y - ref).max(axis=-1)
     den = np.maximum(np.abs(ref).max(axis=-1), 1e-30)
     return float((num / den).max())
+
+
+def elementwise_err(y, ref, floor=1e-2):
+    """max over elements of |y - ref| / max(|ref|, floor * max |ref| of its row):
+    the relative error of each output, with outputs smaller than `floor` times
+    the row's largest measured against that floor (an output near zero is a
+    cancellation of large terms, whose fp32 rounding scales with the terms,
+    not with the output)."""
+    y = np.asarray(y, np.float64).reshape(np.shape(ref))
+    ref = np.asarray(ref, np.float64)
+    if ref.ndim == 1:
+        ref = ref[None]
+        y = y[None]
+    fl = np.maximum(floor * np.abs(ref).max(axis=-1, keepdims=True), 1e-30)
+    return float((np.abs(y - ref) / np.maximum(np.abs(ref), fl)).max())

@@ -71,6 +71,7 @@ def test_quantize_q8s_host_matches_oracle(oracle):
         w = oracle.f32_to_bf16(oracle.gaussian(500 + N, N * K, 0.0, 0.02).reshape(N, K))
         w[0, :32] = 0
         w[0, 32:64] = oracle.f32_to_bf16(np.full(32, 1e-38, np.float32))   # tiny (denormal half scale)
+        w[0, [33, 60]] = 0                                                  # id = inf: zeros stay 0
         w[1, 64:96] = oracle.f32_to_bf16(np.linspace(-3e4, 3e4, 32).astype(np.float32))
         got = bq.quantize_q8s_host(w, K, N)
         assert np.array_equal(got, oracle.quantize_q8s(w))
@@ -84,3 +85,16 @@ def test_q8s_sizes_and_rejects():
     buf = (ctypes.c_uint8 * 1024)()
     assert L.bq_quantize_q8s_host(buf, 100, 1, buf) == bq.BQ_EINVAL
     assert L.bq_quantize_q8s_host(None, 256, 1, buf) == bq.BQ_EINVAL
+
+
+def test_workspace_bytes():
+    """bq_gemm_workspace_bytes (host arithmetic only): the K-split workspace
+    of the prefill GEMMs, at most 32 MiB for any shape."""
+    import bq
+    L = bq.load()
+    # one token tile of a 9216-row matrix: 72 tiles -> 7 slices of rows x 9216
+    assert L.bq_gemm_workspace_bytes(64, 3072, 9216) == 7 * 64 * 9216 * 4
+    assert L.bq_gemm_workspace_bytes(2048, 3072, 9216) == 0      # 1152 tiles fill the GPU
+    assert L.bq_gemm_workspace_bytes(0, 3072, 9216) == 0
+    worst = max(L.bq_gemm_workspace_bytes(r, 3072, n) for r in range(1, 600, 7) for n in (128, 1024, 9216, 36864))
+    assert worst <= 32 << 20

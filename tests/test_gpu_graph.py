@@ -12,7 +12,7 @@ record no memset nodes, so each replay starts from the state the test sets up.
 import numpy as np
 import pytest
 
-from helpers import dev, host, weights
+from helpers import check, dev, host, weights
 
 pytestmark = pytest.mark.gpu
 
@@ -40,8 +40,15 @@ def test_decode_chain_graph_replay(bq, oracle):
     yg, yu = torch.empty((1, FF), device="cuda"), torch.empty((1, FF), device="cuda")
     proj = torch.empty((1, K), device="cuda")
 
+    xq_first = torch.empty_like(xq)
+    xd_first = torch.empty_like(xd)
+    xs_first = torch.empty_like(xs)
+
     def chain():
         assert bq.norm_q8("resid", 1, K, a=x, b=upd, c=alpha, q8=(xq, xd, xs))[0] == bq.BQ_OK
+        xq_first.copy_(xq)
+        xd_first.copy_(xd)
+        xs_first.copy_(xs)
         assert bq.verify_fused([yg, yu], [Wg, Wu], 1, xq, xd, xs) == bq.BQ_OK
         assert bq.norm_q8("silu", 1, FF, out=None, a=yg, b=yu, c=sg, d=su, q8=(tq, td, ts))[0] == bq.BQ_OK
         bq.gemv(proj, Wd, tq, td, ts)
@@ -73,6 +80,21 @@ def test_decode_chain_graph_replay(bq, oracle):
         for a, b in zip(got, ref):
             assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"replay {rep}"
         del scratch
+    # Each stage of the chain against the oracle, on the inputs the chain
+    # produced: the GEMVs within 1e-4 (normwise and elementwise, helpers.check),
+    # the resid producer's q8 row bit-exact with the oracle quantizer of its
+    # fp32 row.
+    x1 = oracle.norm_rows("resid", host(x0), host(upd), host(alpha)).astype(np.float32)
+    q1 = oracle.q8_rows(x1)
+    assert np.mean(q1[0] == host(xq_first)) > 0.999
+    check(oracle, ref[7], oracle.gemm_q5k(host(wg), *[host(t) for t in (xq_first, xd_first, xs_first)]),
+          what="gate")
+    check(oracle, ref[8], oracle.gemm_q5k(host(wu), *[host(t) for t in (xq_first, xd_first, xs_first)]),
+          what="up")
+    check(oracle, ref[9], oracle.gemm_q6k(host(wd), ref[4], ref[5]), what="down")
+    x2 = oracle.norm_rows("resid", x1, ref[9], host(alpha2))
+    assert oracle.normwise_err(ref[0], x2) < 1e-5
+    assert np.array_equal(oracle.q8_rows(ref[0])[0], ref[1])
     # the q8 row of t is the oracle's silu*mul norm of the GEMV outputs (fp32
     # rounding of the norm may move a code that sits on a rounding boundary)
     t_ref = oracle.norm_rows("silu", ref[7], ref[8], host(sg), host(su)).astype(np.float32)

@@ -27,6 +27,12 @@ def test_quantizer_bitexact(bq, oracle, M, K):
     if K > 64:
         x[0, 32:64] = 0.0
         x[0, 40] = 1e-30                  # a lone tiny value
+    if K > 96:
+        # 0 < amax < 127 * 2^-128: d denormal, id = inf; zeros -> 0 (NaN under
+        # cvt.rni), every other value -> +-127
+        x[-1, 64:96] = 1e-38
+        x[-1, [66, 70, 95]] = 0.0
+        x[-1, 80] = -3e-39
     xq, xd, xs = oracle.q8_rows(x)
     gq, gd, gs, gh = bq.quantize_q8(dev(x), with_xdh=True)
     torch.cuda.synchronize()

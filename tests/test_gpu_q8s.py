@@ -19,6 +19,7 @@ def bf16_weights(oracle, seed, N, K, std=0.02):
     w[0, :32] = 0                                                             # all-zero group
     if K >= 128:
         w[0, 32:64] = oracle.f32_to_bf16(np.full(32, 1e-38, np.float32))     # denormal half scale
+        w[0, [40, 47]] = 0                     # id = inf there: 0 * inf = NaN -> code 0 (cvt.rni)
         w[-1, 64:96] = oracle.f32_to_bf16(np.linspace(-3e4, 3e4, 32).astype(np.float32))
     return w
 

@@ -9,7 +9,7 @@ dots, linearity, and the repack index maps rebuilt with numpy.
 import numpy as np
 import pytest
 
-from helpers import acts, weights
+from helpers import acts, kat_q5k as kat_weights, kat_q6k, np_codes_q5k, np_codes_q6k, weights
 
 
 # ---------------------------------------------------------------- fp16
@@ -70,6 +70,20 @@ def test_q8_special_cases(oracle):
     assert xq[0, 39] == -127 and xs[0, 1] == -127 and np.count_nonzero(xq[0, 32:64]) == 1
     assert np.all(xq[0, 64:96] == 127) and xs[0, 2] == 127 * 32
     assert xq[0, 96] == 127 and xd[0, 3] > 0
+    # 0 < amax < 127 * 2^-128: d is denormal, id = 1/d = inf.  The
+    # reference's __float2int_rn (PTX cvt.rni: NaN -> 0, +-inf saturates)
+    # gives 0 for v = 0 (0 * inf = NaN) and +-127 for every other value.
+    x = np.zeros((1, 64), np.float32)
+    x[0, :32] = 1e-38
+    x[0, [3, 9, 31]] = 0.0
+    x[0, 5] = -1e-38
+    x[0, 7] = -0.0
+    x[0, 40] = 2e-39                         # alone: d denormal as well
+    xq, xd, xs = oracle.q8_rows(x)
+    assert 0 < xd[0, 0] < np.float32(2.0 ** -126) and np.isinf(np.float32(1) / xd[0, 0])
+    want = np.where(x[0, :32] > 0, 127, np.where(x[0, :32] < 0, -127, 0))
+    assert np.array_equal(xq[0, :32], want) and xs[0, 0] == want.sum()
+    assert xq[0, 40] == 127 and np.count_nonzero(xq[0, 32:]) == 1 and xs[0, 1] == 127
     # ties round half to even: amax = 127 -> d = 1 exactly, v = k + 0.5
     x = np.zeros((1, 32), np.float32)
     x[0, 0] = 127.0
@@ -132,31 +146,6 @@ def test_encoder_roundtrip(oracle, qtype, tol):
     assert np.array_equal(raw, raw2)
 
 
-# independent numpy decoders of the GGUF layouts (vectorised, written from the spec)
-def np_codes_q5k(raw, K):
-    N = raw.shape[0]
-    b = raw.reshape(N, K // 256, 176)
-    qh = b[:, :, 16:48]
-    qs = b[:, :, 48:176].reshape(N, K // 256, 4, 32)
-    out = np.empty((N, K // 256, 8, 32), np.int32)
-    for j in range(8):
-        nib = (qs[:, :, j // 2, :] >> (4 * (j % 2))) & 0xF
-        out[:, :, j, :] = nib | (((qh >> j) & 1) << 4)
-    return out.reshape(N, K)
-
-
-def np_codes_q6k(raw, K):
-    N = raw.shape[0]
-    b = raw.reshape(N, K // 256, 210)
-    ql = b[:, :, :128].reshape(N, K // 256, 2, 2, 32)   # [half][u&1][l]
-    qh = b[:, :, 128:192].reshape(N, K // 256, 2, 32)
-    out = np.empty((N, K // 256, 2, 4, 32), np.int32)
-    for u in range(4):
-        lo = (ql[:, :, :, u % 2, :] >> (4 * (u // 2))) & 0xF
-        out[:, :, :, u, :] = lo | (((qh >> (2 * u)) & 3) << 4)
-    return out.reshape(N, K)
-
-
 def test_dots_vs_numpy(oracle):
     raw5 = weights(21, 24, 512, "q5k")
     raw6 = weights(22, 24, 512, "q6k")
@@ -186,16 +175,6 @@ def test_gemm_vs_dequant_matmul(oracle):
     assert oracle.normwise_err(oracle.gemm_q6k_f32(raw6, xq, xd), oracle.gemm_q6k(raw6, xq, xd)) < 1e-5
 
 
-def kat_weights(N, K):
-    """mmq_test.cu simple==3 blocks: d = 1, dmin = 0, sc = 1 everywhere, all codes 1."""
-    raw = np.zeros((N, K // 256, 176), np.uint8)
-    raw[:, :, 0:2] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)
-    raw[:, :, 4:8] = 0x01
-    raw[:, :, 12:16] = 0x11
-    raw[:, :, 48:176] = 0x11
-    return raw.reshape(N, -1)
-
-
 def test_kat_y_equals_K(oracle):
     K, N, M = 1024, 8, 2
     raw = kat_weights(N, K)
@@ -204,6 +183,17 @@ def test_kat_y_equals_K(oracle):
     xs = np.zeros((M, K // 32), np.int32)
     assert np.all(oracle.gemm_q5k(raw, xq, xd, xs) == K)
     assert np.all(oracle.gemm_q5k_f32(raw, xq, xd, xs) == K)
+
+
+def test_kat_q6k_y_equals_K(oracle):
+    K, N, M = 512, 4, 2
+    raw = kat_q6k(N, K)
+    assert np.all(np_codes_q6k(raw, K) == 33)
+    xq = np.ones((M, K), np.int8)
+    xd = np.ones((M, K // 32), np.float32)
+    assert np.all(oracle.gemm_q6k(raw, xq, xd) == K)
+    assert np.all(oracle.gemm_q6k_f32(raw, xq, xd) == K)
+    assert np.all(np_codes_q5k(kat_weights(N, K), K) == 1)
 
 
 def test_linearity_and_min_term(oracle):

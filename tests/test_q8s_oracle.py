@@ -115,18 +115,21 @@ def test_gemv_q8s_kat_y_equals_K(oracle):
 
 def test_q8s_tiny_groups(oracle):
     """amax = 1e-38 (an fp32 denormal): d = amax/127 underflows the half scale
-    to 0 and 1/d overflows to inf, so every code saturates to +-127 -- what the
-    reference's device conversion (__float2int_rn) produces.  amax = 1e-30:
+    to 0 and 1/d overflows to inf, so every nonzero code saturates to +-127 and
+    zeros stay 0 (0 * inf = NaN -> 0) -- what the reference's device conversion
+    (__float2int_rn, PTX cvt.rni) produces.  amax = 1e-30:
     finite id, ordinary codes, half scale 0."""
     K = 256
     w = np.zeros((1, K), np.float32)
     w[0, :32] = 1e-38
     w[0, 5] = -1e-38
+    w[0, 11] = 0.0                               # 0 * inf = NaN -> 0 (cvt.rni)
     w[0, 32:64] = np.linspace(-1e-30, 1e-30, 32)
     b = oracle.f32_to_bf16(w)
     sc, codes = split_q8s(oracle, oracle.quantize_q8s(b), K)
     assert sc[0, 0] == 0 and sc[0, 1] == 0
-    assert np.all(codes[0, :32] == np.where(np.arange(32) == 5, -127, 127))
+    i = np.arange(32)
+    assert np.all(codes[0, :32] == np.where(i == 5, -127, np.where(i == 11, 0, 127)))
     assert codes[0, 32] == -127 and codes[0, 63] == 127
     xq, _, _ = oracle.q8_rows(oracle.bf16_to_f32(b)[:, 32:64])
     assert np.array_equal(codes[0, 32:64], xq[0])
