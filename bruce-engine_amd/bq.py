@@ -26,7 +26,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libbq.so")
 
-BQ_OK, BQ_UNSUPPORTED, BQ_EINVAL = 0, 1, 2
+BQ_OK, BQ_UNSUPPORTED, BQ_EINVAL, BQ_ETOOBIG = 0, 1, 2, 3
 TYPE_Q5_K, TYPE_Q6_K = 13, 14
 Q5K_BYTES, Q6K_BYTES = 176, 210
 Q8S_BYTES = 272  # Q8_0 logits head: 8 fp16 scales + 256 int8 per (row, 256 values)
@@ -40,7 +40,8 @@ EXPORTS = [
     "bq_quantize_q8s_host", "bq_gemv_q8s", "bq_norm_q8", "bq_add_norm_q8", "bq_resid_q8",
     "bq_gate_norm_q8", "bq_silu_mul_norm_q8", "bq_gguf_open", "bq_gguf_close", "bq_gguf_n_tensors",
     "bq_gguf_find", "bq_gguf_tensor_info", "bq_gguf_kv_num", "bq_gguf_kv_str", "bq_gguf_read", "bq_gguf_load",
-    "bq_gemv_norm_fused", "bq_gate_up_silu", "bq_gemm_workspace_bytes",
+    "bq_gemv_norm_fused", "bq_gate_up_silu", "bq_gemm_workspace_bytes", "bq_gemm_b_fused_noalloc",
+    "bq_noalloc_scratch_bytes",
 ]
 
 
@@ -94,6 +95,8 @@ def load(path=LIB_PATH):
         "bq_gemm_q6k_mma": (I, [P, WP, I, P, P, P, S, P]),
         "bq_gemm_b": (I, [P, WP, I, P, P, P, P, P, S, P]),
         "bq_gemm_b_fused": (I, [P, P, I, I, P, P, P, P, P, S, P]),
+        "bq_gemm_b_fused_noalloc": (I, [P, P, I, I, P, P, P, P]),
+        "bq_noalloc_scratch_bytes": (S, []),
         "bq_repack_q5k": (I, [P, I, I, P, P, P]),
         "bq_repack_q5k_bytes": (S, [I, I]),
         "bq_repack_q5k_min_bytes": (S, [I, I]),

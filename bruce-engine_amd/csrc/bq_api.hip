@@ -30,6 +30,7 @@ DevInfo g_dev;
 int g_init_status = BQ_OK;
 
 int from_hip(hipError_t e) { return e == hipSuccess ? BQ_OK : -(int)e; }
+int scratch_ptr(void** out);  // bq_gemm_b_fused_noalloc's scratch (below)
 
 int ensure_init() {
     std::call_once(g_once, [] {
@@ -97,7 +98,11 @@ int bq_time_next_launch(void* start_event, void* stop_event) {
     return BQ_OK;
 }
 
-int bq_init(void) { return ensure_init(); }
+int bq_init(void) {
+    if (int s = ensure_init()) return s;
+    void* p = nullptr;
+    return scratch_ptr(&p);  // the current device's allocation-free scratch
+}
 
 const char* bq_version(void) { return "bq 0.1 gfx950"; }
 
@@ -105,6 +110,7 @@ const char* bq_strerror(int code) {
     if (code == BQ_OK) return "ok";
     if (code == BQ_UNSUPPORTED) return "unsupported shape or type (nothing enqueued)";
     if (code == BQ_EINVAL) return "invalid argument";
+    if (code == BQ_ETOOBIG) return "input larger than the allocation-free entry point's static scratch";
     if (code < 0) return hipGetErrorString((hipError_t)(-code));
     return "unknown bq error";
 }
@@ -433,6 +439,39 @@ int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const fl
     return BQ_OK;
 }
 
+namespace {
+// Allocation-free scratch of bq_gemm_b_fused_noalloc: one file-scope device
+// array, so each GPU the library runs on holds its own copy until the process
+// ends.  [0, kScratchXdh): the W144 tier's xdh rows; the rest: the K-split
+// workspace.  Host code never passes `scratch` itself to a kernel (in host
+// code the name is a stand-in, not a device address): the address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+constexpr size_t kScratchBytes = 16u << 20;
+constexpr size_t kScratchXdh = 4u << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// the current device's scratch address (looked up on its first use)
+int scratch_ptr(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return from_hip(e);
+    if (dev < 0 || dev >= kMaxDevices) return BQ_UNSUPPORTED;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return from_hip(e);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return BQ_OK;
+}
+}  // namespace
+
 int bq_gemm_b_fused(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
                     const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
                     void* work, size_t work_bytes, bq_stream_t st) {
@@ -448,6 +487,24 @@ int bq_gemm_b_fused(float* const* ys, const bq_weight* const* ws, int nparts, in
         if (r != BQ_OK) return r;
     }
     return BQ_OK;
+}
+
+size_t bq_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int bq_gemm_b_fused_noalloc(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
+                            const int8_t* xq, const float* xd, const int32_t* xsum, bq_stream_t st) {
+    if (int s = ensure_init()) return s;
+    if (!ys || !ws || !ws[0] || nparts < 1 || nparts > BQ_MAX_PARTS || rows < 0) return BQ_EINVAL;
+    if (rows == 0) return BQ_OK;
+    const int K = ws[0]->K;
+    if (K <= 0 || (K % 32) != 0) return BQ_EINVAL;
+    // xdh [rows][K/32] fp16 must fit its region
+    if ((size_t)rows * (size_t)(K / 32) * 2 > kScratchXdh) return BQ_ETOOBIG;
+    void* base = nullptr;
+    if (int r = scratch_ptr(&base)) return r;
+    uint16_t* xdh = (uint16_t*)base;
+    void* work = (uint8_t*)base + kScratchXdh;
+    return bq_gemm_b_fused(ys, ws, nparts, rows, xq, xd, xsum, xdh, work, kScratchBytes - kScratchXdh, st);
 }
 
 size_t bq_repack_q5k_bytes(int K, int N) { return (size_t)(K / 128) * N * 144; }

@@ -12,7 +12,8 @@
  * Return codes: BQ_OK (0); BQ_UNSUPPORTED (1) = shape/type not handled, nothing
  * was enqueued and the caller should fall back (the reference's `return false`,
  * bruce.cu:7147-7161, :7366-7390); BQ_EINVAL (2) = bad argument (null pointer,
- * K not a multiple of 256, ...); a negative value = -(hipError_t) of a failed
+ * K not a multiple of 256, ...); BQ_ETOOBIG (3) = larger than the static
+ * scratch of the allocation-free entry point; a negative value = -(hipError_t) of a failed
  * launch.  bq_strerror() names each code.
  *
  * Layouts (GGUF blocks are read unchanged):
@@ -38,7 +39,7 @@ extern "C" {
 
 typedef struct ihipStream_t* bq_stream_t; /* == hipStream_t; NULL = default stream */
 
-enum { BQ_OK = 0, BQ_UNSUPPORTED = 1, BQ_EINVAL = 2 };
+enum { BQ_OK = 0, BQ_UNSUPPORTED = 1, BQ_EINVAL = 2, BQ_ETOOBIG = 3 };
 enum { BQ_TYPE_Q5_K = 13, BQ_TYPE_Q6_K = 14 }; /* GGML type ids (gguf.h:29-30) */
 enum { BQ_MAX_PARTS = 4, BQ_MAX_ROWS = 8 };
 
@@ -234,6 +235,22 @@ int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const fl
 int bq_gemm_b_fused(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
                     const int8_t* xq, const float* xd, const int32_t* xsum, uint16_t* xdh,
                     void* work, size_t work_bytes, bq_stream_t st);
+
+/* Allocation-free variant of bq_gemm_b_fused, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation).  No counterpart in the reference.  The W144 tier's xdh
+ * rows and the K-split workspace live in a 16 MiB static device array of the
+ * library (4 MiB for xdh, 12 MiB of workspace), which each GPU the library
+ * runs on holds until the process ends; the caller passes only inputs and
+ * outputs.  Results equal bq_gemm_b_fused given its own xdh and a 12 MiB
+ * workspace, bit for bit.  rows * (K/32) * 2 > 4 MiB returns BQ_ETOOBIG
+ * (nothing enqueued).  Every call on one GPU shares that GPU's array and it
+ * keeps the last call's contents (nothing in it needs clearing: each call
+ * writes what it reads): calls that overlap on one GPU (other streams, other
+ * host threads, graphs replayed concurrently) race, so order them. */
+int bq_gemm_b_fused_noalloc(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
+                            const int8_t* xq, const float* xd, const int32_t* xsum, bq_stream_t st);
+size_t bq_noalloc_scratch_bytes(void);  /* 16 MiB */
 
 /* ---- load-time repacks -----------------------------------------------------
  * Q5_K raw -> W144 + Dm (k_q5k_prepack144, bruce.cu:5747-5789, launched by
