@@ -85,6 +85,71 @@ def cpu_baseline(gate, up, down, x, t, threads, budget_s=12.0):
     return steps, el
 
 
+def cpu_rate(parts, threads, budget_s):
+    """Time full passes of `parts` [(fn, w, args)] -- the oracle's scalar fp32
+    restatement of the reference's host loop -- with each weight matrix's rows
+    split over `threads` host threads (the C calls release the GIL).  Returns
+    passes per second."""
+    from concurrent.futures import ThreadPoolExecutor
+    jobs = []
+    for fn, w, args in parts:
+        n = w.shape[0]
+        for i in range(threads):
+            lo, hi = n * i // threads, n * (i + 1) // threads
+            if hi > lo:
+                jobs.append((fn, np.ascontiguousarray(w[lo:hi]), args))
+    calls, t0 = 0, time.perf_counter()
+    with ThreadPoolExecutor(threads) as ex:
+        while True:
+            list(ex.map(lambda j: j[0](j[1], *j[2]), jobs))
+            calls += 1
+            el = time.perf_counter() - t0
+            if el > budget_s or calls >= 5000:
+                break
+    return calls / el
+
+
+def cpu_configs(synth, w_gate, w_down, threads, budget_s=1.2):
+    """The CPU baseline (oracle/bq_oracle.c: the reference's scalar host loop,
+    tools/mmq_test.cu:269-294, and the Q6_K formula of bruce.cu:4330-4345) on
+    BASELINE configs 1, 3, 4 and 5, on `threads` host threads.  Config 4 times
+    a slice of token rows and scales linearly to M (the loop is row-major in
+    M); config 5 times one layer's four matrices and an 8192-row block of the
+    131072-row lm_head and scales to 32 layers + the whole head."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    res = {}
+    x8 = synth.gaussian(SEED + 20, (8, FF))
+    q = {k: O.q8_rows(np.ascontiguousarray(x8[:, :k])) for k in (K, KO, FF)}
+    g5, g6 = O.gemm_q5k_f32, O.gemm_q6k_f32
+    a5 = lambda k, r=1: tuple(np.ascontiguousarray(t[:r]) for t in q[k])
+    a6 = lambda k, r=1: tuple(np.ascontiguousarray(t[:r]) for t in q[k][:2])
+    c1 = synth.quantize_q5k(synth.gaussian(SEED + 8, (K, K), 0.02))
+    r = cpu_rate([(g5, c1, a5(K))], threads, budget_s)
+    res["config1_3072x3072"] = {"GBps": round((c1.nbytes + q8_bytes(1, K) + 4 * K) * r / 1e9, 3)}
+    for rows in (1, 8):
+        r = cpu_rate([(g5, w_gate, a5(K, rows))], threads, budget_s)
+        res[f"config3_rows{rows}"] = {"GBps": round((w_gate.nbytes + q8_bytes(rows, K) + 4 * rows * FF) * r / 1e9, 3),
+                                      "ms_per_call": round(1e3 / r, 2)}
+    S = 16 * threads                                   # token-row slice of the config 4 GEMM
+    xs_ = synth.gaussian(SEED + 21, (S, K))
+    r = cpu_rate([(g5, w_gate, O.q8_rows(xs_))], threads, budget_s)
+    tops = 2.0 * S * FF * K * r / 1e12
+    res["config4_gemm"] = {"tops": round(tops, 5), "slice_rows": S,
+                           "ms_M2048": round(2.0 * 2048 * FF * K / (tops * 1e12) * 1e3, 1),
+                           "ms_M8192": round(2.0 * 8192 * FF * K / (tops * 1e12) * 1e3, 1)}
+    qkv = synth.quantize_q5k(synth.gaussian(SEED + 30, (NQKV, K), 0.02))
+    wo = synth.quantize_q5k(synth.gaussian(SEED + 31, (K, KO), 0.02))
+    head = synth.quantize_q6k(synth.gaussian(SEED + 32, (8192, K), 0.02))
+    r_layer = cpu_rate([(g5, qkv, a5(K)), (g5, wo, a5(KO)), (g5, w_gate, a5(K)), (g5, w_gate, a5(K)),
+                        (g6, w_down, a6(FF))], threads, budget_s)
+    r_head = cpu_rate([(g6, head, a6(K))], threads, budget_s)
+    tok_s = LAYERS / r_layer + (VOCAB // 8192) / r_head
+    res["config5_whole_stack"] = {"ms_per_token": round(tok_s * 1e3, 1),
+                                  "GBps": round(2942042112 / tok_s / 1e9, 3)}
+    return res
+
+
 LAYERS, KO, NQKV, VOCAB = 32, 4096, 5120, 131072
 
 
@@ -124,33 +189,51 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
         raise RuntimeError(f"bqb_stack failed: {r}")
     ms = out[0] / steps
     # the same weights in the reference's dependent decode sequence, with the
-    # q8 producers (gate norm, resid, silu*mul norm, final norm) between GEMVs
+    # q8 producers (gate norm, resid, silu*mul norm) between GEMVs, as the
+    # library's captured decode step (bq_decode_graph_*, one graph per token)
     g = torch.Generator(device="cuda").manual_seed(SEED + 15)
-    fb = [torch.randn(n, generator=g, device="cuda") for n in (K, K, NQKV, KO, FF, FF, VOCAB)]
-    fb += [torch.rand(n, generator=g, device="cuda") * 0.5 + 0.25 for n in (K, K, KO, FF, FF)]
-    qb = []
-    for n in (K, KO, FF):
-        qb += [torch.empty(n, dtype=torch.int8, device="cuda"), torch.empty(n // 32, device="cuda"),
-               torch.empty(n // 32, dtype=torch.int32, device="cuda")]
-    xq0, xd0, xs0 = bq.quantize_q8(fb[0].view(1, K))
-    qb[0].copy_(xq0.view(-1)); qb[1].copy_(xd0.view(-1)); qb[2].copy_(xs0.view(-1))
-    farr = (ctypes.c_void_p * len(fb))(*[t.data_ptr() for t in fb])
-    qarr = (ctypes.c_void_p * len(qb))(*[t.data_ptr() for t in qb])
-    r = B.bqb_chain(steps, warmup, LAYERS, ws, ctypes.byref(lmw), farr, qarr, K, KO, FF, 0, None, sp, out)
-    if r != 0:
-        raise RuntimeError(f"bqb_chain failed: {r}")
-    chain_ms = out[0] / steps
-    # the same sequence with every q8 producer folded into its consuming GEMV
-    x2 = torch.empty(K, device="cuda")
-    r = B.bqb_chain(steps, warmup, LAYERS, ws, ctypes.byref(lmw), farr, qarr, K, KO, FF, 1, ptr(x2), sp, out)
-    if r != 0:
-        raise RuntimeError(f"bqb_chain (folded) failed: {r}")
-    folded_ms = out[0] / steps
-    # and the FFN folded too: gate+up with the silu*mul epilogue, its norm + q8 in the down GEMV
-    r = B.bqb_chain(steps, warmup, LAYERS, ws, ctypes.byref(lmw), farr, qarr, K, KO, FF, 2, ptr(x2), sp, out)
-    if r != 0:
-        raise RuntimeError(f"bqb_chain (folded ffn) failed: {r}")
-    folded2_ms = out[0] / steps
+    vec = lambda n: torch.rand(n, generator=g, device="cuda") * 0.5 + 0.25
+    fb = {"x": torch.randn(K, generator=g, device="cuda"), "aout": torch.randn(KO, generator=g, device="cuda"),
+          "qkv": torch.empty(NQKV, device="cuda"), "proj": torch.empty(K, device="cuda"),
+          "fg": torch.empty(FF, device="cuda"), "fu": torch.empty(FF, device="cuda"),
+          "logits": torch.empty(VOCAB, device="cuda"), "alpha": vec(K), "alpha2": vec(K), "sgate": vec(KO),
+          "sg": vec(FF), "su": vec(FF)}
+    qb = [torch.empty(FF, dtype=torch.int8, device="cuda"), torch.empty(FF // 32, device="cuda"),
+          torch.empty(FF // 32, dtype=torch.int32, device="cuda")]
+    xq0, xd0, xs0 = bq.quantize_q8(fb["x"].view(1, K))
+    qb[0][:K].copy_(xq0.view(-1)); qb[1][:K // 32].copy_(xd0.view(-1)); qb[2][:K // 32].copy_(xs0.view(-1))
+    qout = (ctypes.c_void_p * 1)(fb["qkv"].data_ptr())
+    blocks = (bq.DecodeBlock * (2 * LAYERS))()
+    for l in range(LAYERS):
+        a, f = blocks[2 * l], blocks[2 * l + 1]
+        a.kind, a.alpha = bq.BLOCK_ATTN, fb["alpha"].data_ptr()
+        a.qkv, a.n_qkv, a.qkv_out = ctypes.pointer(ws[5 * l]), 1, qout
+        a.attn_out, a.attn_gate, a.sgate, a.n_attn = fb["aout"].data_ptr(), fb["qkv"].data_ptr(), fb["sgate"].data_ptr(), KO
+        a.o = ctypes.pointer(ws[5 * l + 1])
+        f.kind, f.alpha = bq.BLOCK_FFN, fb["alpha2"].data_ptr()
+        f.gate, f.up, f.down = ctypes.pointer(ws[5 * l + 2]), ctypes.pointer(ws[5 * l + 3]), ctypes.pointer(ws[5 * l + 4])
+        f.s_gate, f.s_up, f.n_ff = fb["sg"].data_ptr(), fb["su"].data_ptr(), FF
+    blocks[2 * LAYERS - 1].norm_after = 1
+    chain = {}
+    for fold in (0, 1):
+        stp = bq.DecodeStep()
+        stp.n_blocks, stp.blocks, stp.n_embd, stp.fold = 2 * LAYERS, blocks, K, fold
+        stp.x, stp.xq, stp.xd, stp.xsum = fb["x"].data_ptr(), qb[0].data_ptr(), qb[1].data_ptr(), qb[2].data_ptr()
+        stp.proj, stp.ffn_g, stp.ffn_u = fb["proj"].data_ptr(), fb["fg"].data_ptr(), fb["fu"].data_ptr()
+        stp.head, stp.logits = ctypes.pointer(lmw), fb["logits"].data_ptr()
+        dg = bq.DecodeGraph(stp)
+        for _ in range(warmup):
+            dg.launch()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            dg.launch()
+        e1.record()
+        torch.cuda.synchronize()
+        chain[fold] = e0.elapsed_time(e1) / steps
+        dg.close()
+    chain_ms, folded_ms = chain[0], chain[1]
     del fb, qb
     wbytes = LAYERS * sum(a.nbytes for a in (w_qkv, w_o, w_gate, w_up, w_down)) + lm.numel()
     act = LAYERS * (2 * (4 * K + q8_bytes(1, K)) + (4 * KO + q8_bytes(1, KO)) + (4 * FF + q8_bytes(1, FF))) \
@@ -163,21 +246,17 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
             "weight_bytes_per_token": wbytes, "bytes_per_token": tot, "ms_per_token": round(ms, 4),
             "GBps": round(gbs(tot, ms), 1), "hbm_frac": round(gbs(tot, ms) / HBM_PEAK_GBS, 4),
             "launches_per_token": 4 * LAYERS + 1,
-            "decode_chain": {"what": "the reference's dependent decode sequence per layer: QKV GEMV, gate norm -> q8, "
+            "decode_chain": {"what": "the reference's dependent decode sequence per layer through the library's "
+                                     "captured decode step (bq_decode_graph, fold = 0): QKV GEMV, gate norm -> q8, "
                                      "O GEMV, resid -> q8, gate+up GEMV, silu*mul norm -> q8, down GEMV, resid -> q8; "
                                      "final norm -> q8, lm_head (attention excluded; aout a fixed input)",
                              "ms_per_token": round(chain_ms, 4), "GBps": round(gbs(tot, chain_ms), 1),
                              "launches_per_token": 8 * LAYERS + 2},
-            "decode_chain_folded": {"what": "the same dependent sequence with the q8 producers of the small GEMVs "
-                                            "folded into them (bq_gemv_norm_fused): QKV+resid, O+gate norm; resid, "
-                                            "gate+up, silu*mul norm, down as before; last resid, final norm -> q8, lm_head",
+            "decode_chain_folded": {"what": "the same step with fold = 1: the gate norm inside the O GEMV, the "
+                                            "silu*mul in the gate+up epilogue (bq_gate_up_silu) and its norm -> q8 "
+                                            "inside the down GEMV (bq_gemv_norm_fused)",
                                     "ms_per_token": round(folded_ms, 4), "GBps": round(gbs(tot, folded_ms), 1),
-                                    "launches_per_token": 6 * LAYERS + 3},
-            "decode_chain_folded_ffn": {"what": "as decode_chain_folded, with gate+up and the silu*mul of its "
-                                                "outputs in one launch (bq_gate_up_silu) and the norm -> q8 of h "
-                                                "inside the down GEMV (bq_gemv_norm_fused)",
-                                        "ms_per_token": round(folded2_ms, 4), "GBps": round(gbs(tot, folded2_ms), 1),
-                                        "launches_per_token": 5 * LAYERS + 3}}
+                                    "launches_per_token": 6 * LAYERS + 2}}
 
 
 def q8s_head(B, bq, torch, sp, ptr, steps=50):
@@ -298,6 +377,76 @@ def gguf_load(bq, torch):
         os.unlink(path)
 
 
+def gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out):
+    """Config 4 (Q5_K 9216 x 3072 GEMM at M = 2048 / 512 / 8192, both tiers),
+    the prompt-batch tail through bq_gemm_b and the Q6_K GEMM (down projection
+    over W160, M = 2048)."""
+    gemm = {}
+    gw144, gdm = bq.repack_q5k(g_gate, K, FF)
+    for M in (2048, 512, 8192):
+        xm = torch.from_numpy(synth.gaussian(SEED + 6, (M, K))).cuda()
+        mq, md, ms_, mh = bq.quantize_q8(xm, with_xdh=True)
+        ym = torch.empty((M, FF), device="cuda")
+        res = {}
+        for name, w in (("w144", bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF, rep=gw144, rep_min=gdm)),
+                        ("raw", bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF))):
+            gsteps = 20 if M == 8192 else 50
+            r = B.bqb_gemm(gsteps, 5, ctypes.byref(w), M, ptr(mq), ptr(md), ptr(ms_), ptr(mh), ptr(ym), sp, out)
+            if r != 0:
+                raise RuntimeError(f"bqb_gemm failed: {r}")
+            kms = out[1] / gsteps
+            tops = 2.0 * M * FF * K / (kms * 1e-3) / 1e12
+            res[name] = {"ms": round(kms, 4), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)}
+        gemm[f"M{M}"] = res
+        del xm, mq, md, ms_, mh, ym
+    # prompt-batch tail (rows 9..95, bq_gemm_b: 8-row GEMV chunks or the
+    # MMQ tile) and the Q6_K GEMM (down projection over W160, M = 2048)
+    def ev_time(fn, n=20):
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+    wp = bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF, rep=gw144, rep_min=gdm)
+    xt = torch.from_numpy(synth.gaussian(SEED + 9, (96, K))).cuda()
+    tq, td_, ts_, th = bq.quantize_q8(xt, with_xdh=True)
+    yt = torch.empty((96, FF), device="cuda")
+    tail = {}
+    tw = torch.empty(8 << 20, device="cuda")      # K-split workspace: 32 MiB covers any split
+    for rows in (16, 32, 48, 64, 95):
+        tms = ev_time(lambda: bq.gemm_b(yt, wp, rows, tq, td_, ts_, th, work=tw))
+        tail[f"rows{rows}"] = {"us": round(tms * 1e3, 1),
+                               "tops": round(2.0 * rows * FF * K / (tms * 1e-3) / 1e12, 1)}
+    del xt, tq, td_, ts_, th, yt
+    w160 = bq.repack_q6k(g_down, FF, K)
+    wd6 = bq.make_weight(g_down, bq.TYPE_Q6_K, FF, K, rep=w160)
+    x6 = torch.from_numpy(synth.gaussian(SEED + 10, (2048, FF))).cuda()
+    q6q, q6d, _ = bq.quantize_q8(x6)
+    y6 = torch.empty((2048, K), device="cuda")
+    q6ms = ev_time(lambda: bq.gemm_q6k_mma(y6, wd6, 2048, q6q, q6d, work=None), n=10)
+    q6tops = 2.0 * 2048 * K * FF / (q6ms * 1e-3) / 1e12
+    del w160, x6, q6q, q6d, y6
+    g = gemm["M2048"]["w144"]
+    gemm_obj = {
+        "config": "prefill GEMM Q5_K 9216x3072 (W144 repack, fp16 min term), M=2048 q8 tokens, fp32 out",
+        "value": g["tops"], "unit": "TOPS", "ms": g["ms"],
+        "roofline": {"bound": "mfma", "achieved": g["tops"], "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                     "frac": g["frac"], "traffic": traffic_for("mmq_w144_M2048"),
+                     "kernel": "k_mmq_w144", "ops_per_launch": 2 * 2048 * FF * K},
+        "shapes": gemm,
+        "tail_rows_bq_gemm_b": {"what": "Q5_K 9216x3072 W144, bq_gemm_b: 8-row GEMV chunks below 17 rows, "
+                                        "the K-split 128-row MMQ tile from 17", **tail},
+        "q6k_down_M2048": {"what": "Q6_K 3072x9216 over W160 (k_mmq_q6k_dma), M=2048", "ms": round(q6ms, 4),
+                           "tops": round(q6tops, 1), "frac": round(q6tops / INT8_PEAK_TOPS, 4)},
+    }
+    return gemm_obj
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -306,6 +455,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode FFN step (for kernel traces); implies --no-cpu")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the prefill GEMMs of config 4 and the Q6_K GEMM (for counter profiles); "
+                         "prints their JSON object")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the k-quant matmul path has no multi-GPU mode in this "
@@ -330,7 +482,6 @@ def main():
     B.bqb_stack.argtypes = [I, I, I, WP, WP, P, P, P, P, P, P, P, P, P, P]
     B.bqb_q8s.argtypes = [I, I, I, P, I, I, I, P, P, P, P, P, P]
     B.bqb_norm.argtypes = [I, I, I, P, P, P, P, P, I, I, P, P, P, P, P]
-    B.bqb_chain.argtypes = [I, I, I, WP, WP, P, P, I, I, I, I, P, P, P]
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
     ptr = lambda t: ctypes.c_void_p(t.data_ptr())
@@ -371,8 +522,12 @@ def main():
     del calib_src, calib_dst
     torch.cuda.synchronize()
 
-    # ---------------------------------------------------------------- decode FFN step
     out = D4()
+    if args.gemm_only:
+        print(json.dumps({"gemm": gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out)}), flush=True)
+        return
+
+    # ---------------------------------------------------------------- decode FFN step
     step_bytes = wbytes + q8_bytes(1, K) + q8_bytes(1, FF) + 4 * (2 * FF + K)
 
     def decode(mode, warmup):
@@ -401,69 +556,7 @@ def main():
 
     gemm_obj, rows_res, c1_obj, stack_obj, q8s_obj, norm_obj, load_obj = None, None, None, None, None, None, None
     if not args.decode_only:
-        # ---------------------------------------------------------------- prefill GEMM (config 4)
-        gemm = {}
-        gw144, gdm = bq.repack_q5k(g_gate, K, FF)
-        for M in (2048, 512, 8192):
-            xm = torch.from_numpy(synth.gaussian(SEED + 6, (M, K))).cuda()
-            mq, md, ms_, mh = bq.quantize_q8(xm, with_xdh=True)
-            ym = torch.empty((M, FF), device="cuda")
-            res = {}
-            for name, w in (("w144", bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF, rep=gw144, rep_min=gdm)),
-                            ("raw", bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF))):
-                gsteps = 20 if M == 8192 else 50
-                r = B.bqb_gemm(gsteps, 5, ctypes.byref(w), M, ptr(mq), ptr(md), ptr(ms_), ptr(mh), ptr(ym), sp, out)
-                if r != 0:
-                    raise RuntimeError(f"bqb_gemm failed: {r}")
-                kms = out[1] / gsteps
-                tops = 2.0 * M * FF * K / (kms * 1e-3) / 1e12
-                res[name] = {"ms": round(kms, 4), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)}
-            gemm[f"M{M}"] = res
-            del xm, mq, md, ms_, mh, ym
-        # prompt-batch tail (rows 9..95, bq_gemm_b: 8-row GEMV chunks or the
-        # MMQ tile) and the Q6_K GEMM (down projection over W160, M = 2048)
-        def ev_time(fn, n=20):
-            for _ in range(3):
-                fn()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            e0.record()
-            for _ in range(n):
-                fn()
-            e1.record()
-            torch.cuda.synchronize()
-            return e0.elapsed_time(e1) / n
-        wp = bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF, rep=gw144, rep_min=gdm)
-        xt = torch.from_numpy(synth.gaussian(SEED + 9, (96, K))).cuda()
-        tq, td_, ts_, th = bq.quantize_q8(xt, with_xdh=True)
-        yt = torch.empty((96, FF), device="cuda")
-        tail = {}
-        for rows in (16, 32, 48, 64, 95):
-            tms = ev_time(lambda: bq.gemm_b(yt, wp, rows, tq, td_, ts_, th))
-            tail[f"rows{rows}"] = {"us": round(tms * 1e3, 1),
-                                   "tops": round(2.0 * rows * FF * K / (tms * 1e-3) / 1e12, 1)}
-        del xt, tq, td_, ts_, th, yt
-        w160 = bq.repack_q6k(g_down, FF, K)
-        wd6 = bq.make_weight(g_down, bq.TYPE_Q6_K, FF, K, rep=w160)
-        x6 = torch.from_numpy(synth.gaussian(SEED + 10, (2048, FF))).cuda()
-        q6q, q6d, _ = bq.quantize_q8(x6)
-        y6 = torch.empty((2048, K), device="cuda")
-        q6ms = ev_time(lambda: bq.gemm_q6k_mma(y6, wd6, 2048, q6q, q6d), n=10)
-        q6tops = 2.0 * 2048 * K * FF / (q6ms * 1e-3) / 1e12
-        del w160, x6, q6q, q6d, y6
-        g = gemm["M2048"]["w144"]
-        gemm_obj = {
-            "config": "prefill GEMM Q5_K 9216x3072 (W144 repack, fp16 min term), M=2048 q8 tokens, fp32 out",
-            "value": g["tops"], "unit": "TOPS", "ms": g["ms"],
-            "roofline": {"bound": "mfma", "achieved": g["tops"], "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                         "frac": g["frac"], "traffic": traffic_for("mmq_w144_M2048"),
-                         "kernel": "k_mmq_w144", "ops_per_launch": 2 * 2048 * FF * K},
-            "shapes": gemm,
-            "tail_rows_bq_gemm_b": {"what": "Q5_K 9216x3072 W144, bq_gemm_b: 8-row GEMV chunks below 17 rows, "
-                                            "the K-split 128-row MMQ tile from 17", **tail},
-            "q6k_down_M2048": {"what": "Q6_K 3072x9216 over W160 (k_mmq_q6k_dma), M=2048", "ms": round(q6ms, 4),
-                               "tops": round(q6tops, 1), "frac": round(q6tops / INT8_PEAK_TOPS, 4)},
-        }
+        gemm_obj = gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out)
 
         # ---------------------------------------------------------------- config 3 / config 1 GEMV
         rows_res = {}
@@ -510,7 +603,12 @@ def main():
                          f"(tools/mmq_test.cu:269-294), output rows split over {ncpu} threads",
                "seconds": round(eln, 2), "host_threads_available": os.cpu_count(),
                "single_thread": {"value": round(gbs(step_bytes * steps1, el1 * 1e3), 3), "unit": "GB/s",
-                                 "steps": steps1, "seconds": round(el1, 2)}}
+                                 "steps": steps1, "seconds": round(el1, 2)},
+               "other_configs": {"what": "the same loop on configs 1, 3, 4 (a token-row slice scaled to M) and "
+                                         "5 (one layer + an 8192-row lm_head block, scaled to 32 layers + "
+                                         "131072 rows); each timed ~1.2 s",
+                                 f"threads_{ncpu}": cpu_configs(synth, w_gate, w_down, ncpu),
+                                 "threads_1": cpu_configs(synth, w_gate, w_down, 1)}}
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,

@@ -41,7 +41,8 @@ EXPORTS = [
     "bq_gate_norm_q8", "bq_silu_mul_norm_q8", "bq_gguf_open", "bq_gguf_close", "bq_gguf_n_tensors",
     "bq_gguf_find", "bq_gguf_tensor_info", "bq_gguf_kv_num", "bq_gguf_kv_str", "bq_gguf_read", "bq_gguf_load",
     "bq_gemv_norm_fused", "bq_gate_up_silu", "bq_gemm_workspace_bytes", "bq_gemm_b_fused_noalloc",
-    "bq_noalloc_scratch_bytes",
+    "bq_noalloc_scratch_bytes", "bq_decode_enqueue", "bq_decode_graph_create", "bq_decode_graph_launch",
+    "bq_decode_graph_destroy",
 ]
 
 
@@ -62,6 +63,33 @@ class GgufTensor(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("suffix", ctypes.c_char_p), ("ne", ctypes.c_uint64 * 4),
                 ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64), ("ggml_type", ctypes.c_uint32),
                 ("ndim", ctypes.c_uint32), ("block", ctypes.c_int32)]
+
+
+BLOCK_ATTN, BLOCK_FFN = 0, 1
+ATTN_HOOK = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p)
+
+
+class DecodeBlock(ctypes.Structure):
+    """bq_decode_block (include/bq.h): one attention or FFN block of the decode step."""
+    _fields_ = [("kind", ctypes.c_int), ("norm_before", ctypes.c_int), ("norm_after", ctypes.c_int),
+                ("alpha", ctypes.c_void_p),
+                ("qkv", ctypes.POINTER(Weight)), ("n_qkv", ctypes.c_int), ("qkv_out", ctypes.POINTER(ctypes.c_void_p)),
+                ("attn_out", ctypes.c_void_p), ("attn_gate", ctypes.c_void_p), ("sgate", ctypes.c_void_p),
+                ("n_attn", ctypes.c_int), ("o", ctypes.POINTER(Weight)),
+                ("gate", ctypes.POINTER(Weight)), ("up", ctypes.POINTER(Weight)),
+                ("s_gate", ctypes.c_void_p), ("s_up", ctypes.c_void_p), ("down", ctypes.POINTER(Weight)),
+                ("n_ff", ctypes.c_int)]
+
+
+class DecodeStep(ctypes.Structure):
+    """bq_decode_step (include/bq.h): the per-token decode launch sequence."""
+    _fields_ = [("n_blocks", ctypes.c_int), ("blocks", ctypes.POINTER(DecodeBlock)), ("n_embd", ctypes.c_int),
+                ("fold", ctypes.c_int), ("x", ctypes.c_void_p), ("input_h", ctypes.c_void_p),
+                ("xq", ctypes.c_void_p), ("xd", ctypes.c_void_p), ("xsum", ctypes.c_void_p),
+                ("proj", ctypes.c_void_p), ("ffn_g", ctypes.c_void_p), ("ffn_u", ctypes.c_void_p),
+                ("attention", ATTN_HOOK), ("user", ctypes.c_void_p),
+                ("head_q8s", ctypes.c_void_p), ("head_rs", ctypes.c_void_p), ("head", ctypes.POINTER(Weight)),
+                ("vocab", ctypes.c_int), ("logits", ctypes.c_void_p)]
 
 
 _lib = None
@@ -96,6 +124,10 @@ def load(path=LIB_PATH):
         "bq_gemm_b": (I, [P, WP, I, P, P, P, P, P, S, P]),
         "bq_gemm_b_fused": (I, [P, P, I, I, P, P, P, P, P, S, P]),
         "bq_gemm_b_fused_noalloc": (I, [P, P, I, I, P, P, P, P]),
+        "bq_decode_enqueue": (I, [ctypes.POINTER(DecodeStep), P]),
+        "bq_decode_graph_create": (I, [ctypes.POINTER(DecodeStep), P, ctypes.POINTER(P)]),
+        "bq_decode_graph_launch": (I, [P, P]),
+        "bq_decode_graph_destroy": (None, [P]),
         "bq_noalloc_scratch_bytes": (S, []),
         "bq_repack_q5k": (I, [P, I, I, P, P, P]),
         "bq_repack_q5k_bytes": (S, [I, I]),
@@ -473,3 +505,33 @@ class Gguf:
             raise BqError(r, "bq_gguf_load")
         w._keep = (raw, rep, rep_min)
         return w
+
+
+# ---------------------------------------------------------------- decode step
+def decode_enqueue(step):
+    return _check(load().bq_decode_enqueue(ctypes.byref(step), _stream()), "bq_decode_enqueue")
+
+
+class DecodeGraph:
+    """bq_decode_graph: the captured decode step; launch() replays one token."""
+
+    def __init__(self, step):
+        self.step = step   # keeps the ctypes structures alive
+        h = ctypes.c_void_p()
+        _check(load().bq_decode_graph_create(ctypes.byref(step), _stream(), ctypes.byref(h)),
+               "bq_decode_graph_create")
+        self.h = h
+
+    def launch(self):
+        return _check(load().bq_decode_graph_launch(self.h, _stream()), "bq_decode_graph_launch")
+
+    def close(self):
+        if self.h:
+            load().bq_decode_graph_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

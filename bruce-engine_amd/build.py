@@ -14,7 +14,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libbq.so")
 BENCH_LIB = os.path.join(HERE, "libbq_bench.so")
-SOURCES = ["bq_quant.hip", "bq_gemv.hip", "bq_repack.hip", "bq_gemm.hip", "bq_q8s.hip", "bq_norm.hip", "bq_gguf.hip", "bq_api.hip"]
+SOURCES = ["bq_quant.hip", "bq_gemv.hip", "bq_repack.hip", "bq_gemm.hip", "bq_q8s.hip", "bq_norm.hip", "bq_gguf.hip", "bq_decode.hip", "bq_api.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -196,120 +196,6 @@ int bqb_gemv_rows(int steps, int warmup, int nsets, const bq_weight* w, int rows
     return 0;
 }
 
-// The reference's decode sequence for the matmul path, per layer (bruce.cu
-// forward_launch :7902-8037, attention itself excluded): QKV GEMV on q8 x;
-// gate norm of the attention output -> q8 a (aout is a fixed input here, its
-// gate the first KO QKV outputs); O GEMV on q8 a; resid -> q8 x; fused
-// gate+up GEMV; silu*mul norm -> q8 t; down GEMV on q8 t; resid -> q8 x.  Then
-// the final norm -> q8 and the lm_head GEMV.  Every launch reads what the one
-// before it wrote.  One HIP graph per token; out[0] = timed region (ms).
-// w = [nlayers][5] (qkv, o, gate, up, down); f = fp32 buffers {x, proj, yqkv,
-// aout, yg, yu, logits, alpha, alpha2, sgate, sg, su}; q = q8 buffers
-// {xq, xd, xs, aq, ad, as, tq, td, ts} (as void*).
-// folded != 0: the same sequence with the q8 producers of the small GEMVs
-// folded into them (bq_gemv_norm_fused): per layer QKV with the resid of the
-// previous layer's down output (layer 0 reads the q8 x), O with the gate norm;
-// the resid before gate+up and the silu*mul norm before down stay standalone
-// (folded into those large GEMVs they cost more than their own launch); then
-// the last resid, the final norm and the lm_head as in the plain chain (the
-// 131072-row lm_head with the norm folded in measured 76 us against 4 + 56 us
-// for the two launches) -- 6 launches per layer instead of 8.  x ping-pongs
-// between x and x2 where a fused producer writes the new x (it cannot update
-// x in place: every workgroup reads it).  folded == 2: also gate+up with the
-// silu*mul epilogue (bq_gate_up_silu) and the norm + q8 of h inside the down
-// GEMV (bq_gemv_norm_fused, BQ_OP_NORM) -- 5 launches per layer.
-int bqb_chain(int steps, int warmup, int nlayers, const bq_weight* w, const bq_weight* lm_head, float* const* f,
-              void* const* q, int K, int KO, int FF, int folded, float* x2, bq_stream_t st, double* out) {
-    float *x = f[0], *proj = f[1], *yqkv = f[2], *aout = f[3], *yg = f[4], *yu = f[5], *logits = f[6];
-    const float *alpha = f[7], *alpha2 = f[8], *sgate = f[9], *sg = f[10], *su = f[11];
-    int8_t *xq = (int8_t*)q[0], *aq = (int8_t*)q[3], *tq = (int8_t*)q[6];
-    float *xd = (float*)q[1], *ad = (float*)q[4], *td = (float*)q[7];
-    int32_t *xs = (int32_t*)q[2], *as_ = (int32_t*)q[5], *ts = (int32_t*)q[8];
-    hipStream_t cs;
-    if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) return -1;
-    auto token_folded = [&](bq_stream_t s) -> int {
-        float* xc = x;   // current residual stream
-        float* xn = x2;  // the next one
-        for (int l = 0; l < nlayers; ++l) {
-            const bq_weight* lw = w + 5 * l;
-            float* y1[1] = {yqkv};
-            const bq_weight* p1[1] = {&lw[0]};
-            if (l == 0) {
-                if (int r = bq_verify_fused(y1, p1, 1, 1, xq, xd, xs, 0, s)) return r;
-            } else {
-                if (int r = bq_gemv_norm_fused(y1, p1, 1, BQ_OP_RESID, xn, xc, proj, alpha2, nullptr, nullptr,
-                                               nullptr, nullptr, s))
-                    return r;
-                std::swap(xc, xn);
-            }
-            float* yo[1] = {proj};
-            const bq_weight* po[1] = {&lw[1]};
-            if (int r = bq_gemv_norm_fused(yo, po, 1, BQ_OP_GATE, nullptr, aout, yqkv, sgate, nullptr, nullptr,
-                                           nullptr, nullptr, s))
-                return r;
-            if (int r = bq_resid_q8(xc, proj, alpha, 1, K, xq, xd, xs, s)) return r;
-            if (folded == 2) {
-                // gate+up with the silu*mul epilogue, its norm + q8 inside the down GEMV
-                if (int r = bq_gate_up_silu(yg, &lw[2], &lw[3], sg, su, xq, xd, xs, s)) return r;
-                float* yd[1] = {proj};
-                const bq_weight* pd[1] = {&lw[4]};
-                if (int r = bq_gemv_norm_fused(yd, pd, 1, BQ_OP_NORM, nullptr, yg, nullptr, nullptr, nullptr,
-                                               nullptr, nullptr, nullptr, s))
-                    return r;
-                continue;
-            }
-            float* y2[2] = {yg, yu};
-            const bq_weight* p2[2] = {&lw[2], &lw[3]};
-            if (int r = bq_verify_fused(y2, p2, 2, 1, xq, xd, xs, 0, s)) return r;
-            if (int r = bq_silu_mul_norm_q8(nullptr, yg, yu, sg, su, 1, FF, tq, td, ts, s)) return r;
-            if (int r = bq_gemv(proj, &lw[4], tq, td, ts, s)) return r;
-        }
-        if (int r = bq_resid_q8(xc, proj, alpha2, 1, K, xq, xd, xs, s)) return r;
-        if (int r = bq_norm_q8(nullptr, xc, 1, K, xq, xd, xs, s)) return r;
-        return bq_gemv(logits, lm_head, xq, xd, xs, s);
-    };
-    auto token_plain = [&](bq_stream_t s) -> int {
-        for (int l = 0; l < nlayers; ++l) {
-            const bq_weight* lw = w + 5 * l;
-            float* y1[1] = {yqkv};
-            const bq_weight* p1[1] = {&lw[0]};
-            if (int r = bq_verify_fused(y1, p1, 1, 1, xq, xd, xs, 0, s)) return r;
-            if (int r = bq_gate_norm_q8(nullptr, aout, yqkv, sgate, 1, KO, aq, ad, as_, s)) return r;
-            if (int r = bq_gemv(proj, &lw[1], aq, ad, as_, s)) return r;
-            if (int r = bq_resid_q8(x, proj, alpha, 1, K, xq, xd, xs, s)) return r;
-            float* y2[2] = {yg, yu};
-            const bq_weight* p2[2] = {&lw[2], &lw[3]};
-            if (int r = bq_verify_fused(y2, p2, 2, 1, xq, xd, xs, 0, s)) return r;
-            if (int r = bq_silu_mul_norm_q8(nullptr, yg, yu, sg, su, 1, FF, tq, td, ts, s)) return r;
-            if (int r = bq_gemv(proj, &lw[4], tq, td, ts, s)) return r;
-            if (int r = bq_resid_q8(x, proj, alpha2, 1, K, xq, xd, xs, s)) return r;
-        }
-        if (int r = bq_norm_q8(nullptr, x, 1, K, xq, xd, xs, s)) return r;
-        return bq_gemv(logits, lm_head, xq, xd, xs, s);
-    };
-    auto token = [&](bq_stream_t s) -> int { return folded ? token_folded(s) : token_plain(s); };
-    for (int i = 0; i < warmup; ++i)
-        if (int r = token(st)) return r;
-    hipGraph_t g;
-    hipGraphExec_t ex;
-    hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
-    const int r = token((bq_stream_t)cs);
-    if (hipStreamEndCapture(cs, &g) != hipSuccess || r) return r ? r : -1;
-    if (hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) != hipSuccess) return -1;
-    hipGraphDestroy(g);
-    hipGraphLaunch(ex, (hipStream_t)st);
-    EventPool pool(2);
-    hipDeviceSynchronize();
-    hipEventRecord(pool.ev[0], (hipStream_t)st);
-    for (int i = 0; i < steps; ++i) hipGraphLaunch(ex, (hipStream_t)st);
-    hipEventRecord(pool.ev[1], (hipStream_t)st);
-    hipDeviceSynchronize();
-    out[0] = elapsed(pool.ev[0], pool.ev[1]);
-    hipGraphExecDestroy(ex);
-    hipStreamDestroy(cs);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
-}
-
 // Fused quantize + GEMV: `steps` launches of bq_gemv_q8_fused over nparts
 // matrices, weight set s = i % nsets (w = [nsets][nparts]); out[1] = sum of
 // the kernels' own durations (ms), out[0] = timed region.

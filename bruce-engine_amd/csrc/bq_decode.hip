@@ -1,0 +1,178 @@
+// bq_decode.hip -- the per-token decode step as one launch sequence and as a
+// captured HIP graph (host C++ over the C ABI).
+//
+// Mirrors the reference's forward_launch (engine/src/bruce.cu:7902-8037), the
+// per-block launch sequence of one decoded token, and capture_graph
+// (:8046-8055) / the graph replay of bruce_decode_step (:8246-8252).  The
+// reference's attention kernels (:7940-7970) are outside this library: a
+// caller hook enqueues them between the QKV projection and the gate norm, so
+// they land in the same graph.
+#include <string.h>
+
+#include "../../include/bq.h"
+#include "bq_internal.hpp"
+
+namespace {
+
+bool dims_ok(const bq_decode_step* s) {
+    return s && s->n_blocks >= 0 && (s->n_blocks == 0 || s->blocks) && s->x && s->xq && s->xd && s->xsum &&
+           s->proj && s->n_embd > 0 && (s->n_embd % 32) == 0;
+}
+
+// one attention block: bruce.cu:7915-7993 (QKV, attention, gate norm, O)
+int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, bq_stream_t st) {
+    if (b.n_qkv < 1 || b.n_qkv > BQ_MAX_PARTS || !b.qkv || !b.qkv_out || !b.o || !b.attn_out || !b.attn_gate ||
+        !b.sgate || b.n_attn <= 0 || (b.n_attn % 32) != 0)
+        return BQ_EINVAL;
+    // QKV: one fused launch over the parts (launch_verify_fused rows = 1,
+    // :7921-7924); parts the fused kernel does not take (a Q6_K V, :7925-7926)
+    // run as their own GEMVs
+    const bq_weight* wp[BQ_MAX_PARTS];
+    float* yp[BQ_MAX_PARTS];
+    int nf = 0;
+    for (int p = 0; p < b.n_qkv; ++p)
+        if (b.qkv[p].ggml_type == BQ_TYPE_Q5_K) {
+            wp[nf] = &b.qkv[p];
+            yp[nf++] = b.qkv_out[p];
+        }
+    if (nf > 0) {
+        const int r = bq_verify_fused(yp, wp, nf, 1, s->xq, s->xd, s->xsum, 0, st);
+        if (r != BQ_OK && r != BQ_UNSUPPORTED) return r;
+        if (r == BQ_UNSUPPORTED)
+            for (int p = 0; p < nf; ++p)
+                if (int e = bq_gemv(yp[p], wp[p], s->xq, s->xd, s->xsum, st)) return e;
+    }
+    for (int p = 0; p < b.n_qkv; ++p)
+        if (b.qkv[p].ggml_type != BQ_TYPE_Q5_K)
+            if (int e = bq_gemv(b.qkv_out[p], &b.qkv[p], s->xq, s->xd, s->xsum, st)) return e;
+    if (s->attention) s->attention(s->user, bi, st);
+    // gate norm -> q8, then O (k_gate_norm :7975-7978, launch_gemv :7982);
+    // folded: the gate norm runs inside the O GEMV (bq_gemv_norm_fused)
+    if (s->fold) {
+        float* yo[1] = {s->proj};
+        const bq_weight* po[1] = {b.o};
+        return bq_gemv_norm_fused(yo, po, 1, BQ_OP_GATE, nullptr, b.attn_out, b.attn_gate, b.sgate, nullptr,
+                                  nullptr, nullptr, nullptr, st);
+    }
+    if (int e = bq_gate_norm_q8(nullptr, b.attn_out, b.attn_gate, b.sgate, 1, b.n_attn, s->xq, s->xd, s->xsum, st))
+        return e;
+    return bq_gemv(s->proj, b.o, s->xq, s->xd, s->xsum, st);
+}
+
+// one FFN block: bruce.cu:7994-8012 (gate+up, silu*mul norm, down)
+int ffn_block(const bq_decode_step* s, const bq_decode_block& b, bq_stream_t st) {
+    if (!b.gate || !b.up || !b.down || !b.s_gate || !b.s_up || !s->ffn_g || b.n_ff <= 0 || (b.n_ff % 32) != 0)
+        return BQ_EINVAL;
+    if (s->fold) {
+        // silu*mul in the gate+up epilogue (h -> ffn_g), its norm + q8 inside the down GEMV
+        if (int e = bq_gate_up_silu(s->ffn_g, b.gate, b.up, b.s_gate, b.s_up, s->xq, s->xd, s->xsum, st)) return e;
+        float* yd[1] = {s->proj};
+        const bq_weight* pd[1] = {b.down};
+        return bq_gemv_norm_fused(yd, pd, 1, BQ_OP_NORM, nullptr, s->ffn_g, nullptr, nullptr, nullptr, nullptr,
+                                  nullptr, nullptr, st);
+    }
+    if (!s->ffn_u) return BQ_EINVAL;
+    float* y2[2] = {s->ffn_g, s->ffn_u};
+    const bq_weight* p2[2] = {b.gate, b.up};
+    int r = bq_verify_fused(y2, p2, 2, 1, s->xq, s->xd, s->xsum, 0, st);
+    if (r == BQ_UNSUPPORTED) {
+        if ((r = bq_gemv(s->ffn_g, b.gate, s->xq, s->xd, s->xsum, st))) return r;
+        r = bq_gemv(s->ffn_u, b.up, s->xq, s->xd, s->xsum, st);
+    }
+    if (r) return r;
+    if (int e = bq_silu_mul_norm_q8(nullptr, s->ffn_g, s->ffn_u, b.s_gate, b.s_up, 1, b.n_ff, s->xq, s->xd,
+                                    s->xsum, st))
+        return e;
+    return bq_gemv(s->proj, b.down, s->xq, s->xd, s->xsum, st);
+}
+
+}  // namespace
+
+struct bq_decode_graph {
+    hipGraphExec_t exec;
+};
+
+extern "C" {
+
+int bq_decode_enqueue(const bq_decode_step* s, bq_stream_t st) {
+    if (int r = bq_init()) return r;
+    if (!dims_ok(s)) return BQ_EINVAL;
+    const int n = s->n_embd;
+    for (int i = 0; i < s->n_blocks; ++i) {
+        const bq_decode_block& b = s->blocks[i];
+        // loop start: x = norm(x + input_h) (k_add_norm, :7914)
+        if (b.norm_before) {
+            if (!s->input_h) return BQ_EINVAL;
+            if (int e = bq_add_norm_q8(s->x, s->input_h, 1, n, s->xq, s->xd, s->xsum, st)) return e;
+        }
+        const int r = b.kind == BQ_BLOCK_FFN ? ffn_block(s, b, st) : b.kind == BQ_BLOCK_ATTN
+                                                                       ? attn_block(s, b, i, st)
+                                                                       : BQ_EINVAL;
+        if (r) return r;
+        // x = resid(x, proj, alpha) -> q8 x (k_resid_vec4, :8017)
+        if (!b.alpha) return BQ_EINVAL;
+        if (int e = bq_resid_q8(s->x, s->proj, b.alpha, 1, n, s->xq, s->xd, s->xsum, st)) return e;
+        // loop end: x = norm(x) (k_norm, :8022)
+        if (b.norm_after)
+            if (int e = bq_norm_q8(s->x, s->x, 1, n, s->xq, s->xd, s->xsum, st)) return e;
+    }
+    // logits from the last q8 row of x (:8026-8032)
+    if (s->head_q8s) {
+        if (!s->logits) return BQ_EINVAL;
+        return bq_gemv_q8s(s->logits, s->head_q8s, s->xq, s->xd, n, s->vocab, 1, s->head_rs, st);
+    }
+    if (s->head) {
+        if (!s->logits) return BQ_EINVAL;
+        return bq_gemv(s->logits, s->head, s->xq, s->xd, s->xsum, st);
+    }
+    return BQ_OK;
+}
+
+int bq_decode_graph_create(const bq_decode_step* s, bq_stream_t st, bq_decode_graph** out) {
+    if (!out) return BQ_EINVAL;
+    *out = nullptr;
+    if (int r = bq_init()) return r;
+    if (!dims_ok(s)) return BQ_EINVAL;
+    // capture on a private stream that follows the caller's, as capture_graph
+    // does on S (:8046-8055), in thread-local mode so other threads' work is
+    // not captured
+    hipStream_t cs;
+    hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
+    if (e != hipSuccess) return -(int)e;
+    int r = BQ_OK;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ex = nullptr;
+    if ((e = hipStreamSynchronize((hipStream_t)st)) != hipSuccess ||
+        (e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal)) != hipSuccess) {
+        r = -(int)e;
+    } else {
+        r = bq_decode_enqueue(s, (bq_stream_t)cs);
+        e = hipStreamEndCapture(cs, &g);
+        if (!r && e != hipSuccess) r = -(int)e;
+        if (!r && (e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0)) != hipSuccess) r = -(int)e;
+        if (g) (void)hipGraphDestroy(g);
+    }
+    (void)hipStreamDestroy(cs);
+    if (r) {
+        if (ex) (void)hipGraphExecDestroy(ex);
+        return r;
+    }
+    bq_decode_graph* dg = new bq_decode_graph;
+    dg->exec = ex;
+    *out = dg;
+    return BQ_OK;
+}
+
+int bq_decode_graph_launch(const bq_decode_graph* g, bq_stream_t st) {
+    if (!g) return BQ_EINVAL;
+    const hipError_t e = hipGraphLaunch(g->exec, (hipStream_t)st);
+    return e == hipSuccess ? BQ_OK : -(int)e;
+}
+
+void bq_decode_graph_destroy(bq_decode_graph* g) {
+    if (!g) return;
+    (void)hipGraphExecDestroy(g->exec);
+    delete g;
+}
+
+}  // extern "C"

@@ -331,6 +331,72 @@ int bq_gguf_read(const bq_gguf* g, int64_t i, void* dst, size_t n, uint64_t off)
  * K % 256 != 0. */
 int bq_gguf_load(bq_gguf* g, int64_t i, void* raw, void* rep, void* rep_min, bq_weight* w, bq_stream_t st);
 
+/* ---- decode step -------------------------------------------------------------
+ * The per-token decode launch sequence of the reference's forward_launch
+ * (bruce.cu:7902-8037) over a caller's block list, eagerly or as one captured
+ * HIP graph (capture_graph :8046-8055, replayed per token as bruce_decode_step
+ * does, :8246-8252).  Per block, in the reference's order:
+ *   norm_before: x = norm(x + input_h) -> q8                      (k_add_norm :7914)
+ *   attention block: QKV GEMV over the q8 row (bq_verify_fused over the Q5_K
+ *     parts, bq_gemv for others), the caller's attention hook, gate norm of
+ *     attn_out by attn_gate -> q8, O GEMV -> proj                   (:7915-7993)
+ *   FFN block: gate+up GEMV, silu*mul norm -> q8, down GEMV -> proj (:7994-8012)
+ *   x = resid(x, proj, alpha) -> q8                               (k_resid :8017)
+ *   norm_after: x = norm(x) -> q8                                 (k_norm :8022)
+ * then the logits from the last q8 row: the Q8_0 head (head_q8s, bq_gemv_q8s
+ * with head_rs) or a k-quant head (head, bq_gemv)                  (:8026-8032).
+ * fold = 1 runs the gate norm inside the O GEMV and the silu*mul inside the
+ * gate+up epilogue with its norm inside the down GEMV (bq_gemv_norm_fused,
+ * bq_gate_up_silu; 2 launches fewer per block pair, outputs equal to rounding).
+ * The attention kernels are the caller's: `attention(user, block, st)` must
+ * enqueue them on st (and only there) and write attn_out; NULL leaves attn_out
+ * as it is.  Scratch (caller-owned): xq/xd/xsum hold one q8 row of
+ * max(n_embd, n_attn, n_ff) values, proj [n_embd], ffn_g and ffn_u [n_ff]
+ * (ffn_u unused when fold = 1).  x is updated in place.  A graph captures the
+ * pointers it is created with: replays read and write the same buffers. */
+enum { BQ_BLOCK_ATTN = 0, BQ_BLOCK_FFN = 1 };
+typedef struct bq_decode_block {
+    int kind;                     /* BQ_BLOCK_ATTN or BQ_BLOCK_FFN */
+    int norm_before, norm_after;  /* loop start / end of the reference's recurrence */
+    const float* alpha;           /* resid blend [n_embd] */
+    /* attention block */
+    const bq_weight* qkv; int n_qkv;   /* q, k, gate, v parts (1..4) sharing K = n_embd */
+    float* const* qkv_out;
+    const float* attn_out;        /* written by the hook; [n_attn] */
+    const float* attn_gate;       /* gate pre-activation [n_attn] (usually one of qkv_out) */
+    const float* sgate;           /* [n_attn] */
+    int n_attn;
+    const bq_weight* o;           /* K = n_attn, N = n_embd */
+    /* FFN block */
+    const bq_weight* gate; const bq_weight* up;   /* K = n_embd, N = n_ff */
+    const float* s_gate; const float* s_up;       /* [n_ff] */
+    const bq_weight* down;                        /* K = n_ff, N = n_embd */
+    int n_ff;
+} bq_decode_block;
+typedef struct bq_decode_step {
+    int n_blocks;
+    const bq_decode_block* blocks;
+    int n_embd;
+    int fold;
+    float* x;                     /* residual stream [n_embd]; its q8 row must be current in xq/xd/xsum */
+    const float* input_h;         /* for norm_before */
+    int8_t* xq; float* xd; int32_t* xsum;
+    float* proj; float* ffn_g; float* ffn_u;
+    void (*attention)(void* user, int block, bq_stream_t st);
+    void* user;
+    const void* head_q8s; const float* head_rs; const bq_weight* head;  /* one of the two heads, or neither */
+    int vocab;
+    float* logits;
+} bq_decode_step;
+/* Enqueue one token's launch sequence on st (stream-ordered, allocates nothing). */
+int bq_decode_enqueue(const bq_decode_step* s, bq_stream_t st);
+/* Capture bq_decode_enqueue into a HIP graph and instantiate it: a set-up
+ * call (synchronises st, allocates the graph), outside any capture. */
+typedef struct bq_decode_graph bq_decode_graph;
+int bq_decode_graph_create(const bq_decode_step* s, bq_stream_t st, bq_decode_graph** g);
+int bq_decode_graph_launch(const bq_decode_graph* g, bq_stream_t st);  /* one token */
+void bq_decode_graph_destroy(bq_decode_graph* g);
+
 /* ---- tooling ---------------------------------------------------------------
  * No counterpart in the reference (its harnesses bracket launches with
  * cudaEventRecord, tools/gemvbench.cu:360-371).  Times the calling thread's

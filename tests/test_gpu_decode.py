@@ -1,0 +1,200 @@
+"""The decode step (bq_decode_enqueue / bq_decode_graph_*): the reference's
+per-token launch sequence (forward_launch, engine/src/bruce.cu:7902-8037)
+over a block list, replayed from one captured HIP graph (capture_graph
+:8046-8055).
+
+Two layers of BASELINE config 5's shapes (hidden 3072, attention width 4096,
+FF 9216; QKV as Q5_K q / k / gate parts plus a Q6_K v, O Q5_K, gate/up Q5_K,
+down Q6_K) and a Q8_0 logits head are run eagerly and from the graph:
+* every block matches the oracle's block -- the same sequence evaluated with
+  the oracle's GEMVs (double precision over the q8 codes), norms
+  (orc_norm_rows) and quantizer -- applied to the same input row, within 2e-4
+  normwise (a block requantizes twice; a value on a q8 rounding boundary can
+  round differently after an fp32 norm and move one code by one);
+* the logits match the oracle's Q8_0 head on the final q8 row within 1e-4;
+* with the reference's own sequence (fold = 0) the whole chain from x0 stays
+  within 2e-4 of the oracle's whole chain;
+* every graph replay is bit-identical to the eager run.
+The folded form (fold = 1: gate norm inside the O GEMV, silu*mul inside the
+gate+up epilogue, its norm inside the down GEMV) is checked the same way.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from helpers import dev, host, weights
+
+pytestmark = pytest.mark.gpu
+
+E, A, FF, V = 3072, 4096, 9216, 8192
+PARTS = [("q", A, "q5k"), ("k", 512, "q5k"), ("gate", A, "q5k"), ("v", 512, "q6k")]
+
+
+def _model(bq, oracle):
+    import torch
+    g = lambda s, n, m=0.0, sd=1.0: oracle.gaussian(s, n, m, sd).astype(np.float32)
+    layers = []
+    for l in range(2):
+        s0 = 3000 + 100 * l
+        qkv = [(name, n, qt, weights(s0 + i, n, E, qt)) for i, (name, n, qt) in enumerate(PARTS)]
+        layers.append({
+            "qkv": qkv,
+            "o": weights(s0 + 10, E, A, "q5k"),
+            "gate": weights(s0 + 11, FF, E, "q5k"), "up": weights(s0 + 12, FF, E, "q5k"),
+            "down": weights(s0 + 13, E, FF, "q6k"),
+            "attn_out": g(s0 + 20, A), "sgate": g(s0 + 21, A, 1.0, 0.3),
+            "sg": g(s0 + 22, FF, 1.0, 0.3), "su": g(s0 + 23, FF, 1.0, 0.3),
+            "alpha_a": g(s0 + 24, E, 0.5, 0.2), "alpha_f": g(s0 + 25, E, 0.5, 0.2),
+        })
+    head_bf16 = oracle.f32_to_bf16(g(3900, V * E, 0.0, 0.02).reshape(V, E))
+    return {"layers": layers, "x0": g(3901, E), "input_h": g(3902, E), "head": head_bf16,
+            "rs": g(3903, V, 1.0, 0.1)}
+
+
+def _oracle_block(oracle, m, bi, x):
+    """Block bi (even: attention of layer bi // 2, odd: its FFN) of the
+    reference's sequence applied to the fp32 row x, with the oracle's GEMVs
+    (double precision over the q8 codes), norms and quantizer; returns the
+    new x (fp32)."""
+    f32 = lambda a: np.asarray(a, np.float32)
+    L = m["layers"][bi // 2]
+    x = x[None]
+    if bi == 0:
+        x = f32(oracle.norm_rows("add", x, m["input_h"][None]))
+    q = oracle.q8_rows(x)
+    if bi % 2 == 0:
+        ys = {}
+        for name, n, qt, raw in L["qkv"]:
+            ys[name] = f32(oracle.gemm_q5k(raw, *q) if qt == "q5k" else oracle.gemm_q6k(raw, q[0], q[1]))
+        t = f32(oracle.norm_rows("gate", L["attn_out"][None], ys["gate"], L["sgate"][None]))
+        qa = oracle.q8_rows(t)
+        proj = f32(oracle.gemm_q5k(L["o"], *qa))
+        x = f32(oracle.norm_rows("resid", x, proj, L["alpha_a"][None]))
+    else:
+        yg, yu = f32(oracle.gemm_q5k(L["gate"], *q)), f32(oracle.gemm_q5k(L["up"], *q))
+        t = f32(oracle.norm_rows("silu", yg, yu, L["sg"][None], L["su"][None]))
+        qt = oracle.q8_rows(t)
+        proj = f32(oracle.gemm_q6k(L["down"], qt[0], qt[1]))
+        x = f32(oracle.norm_rows("resid", x, proj, L["alpha_f"][None]))
+        if bi == 2 * len(m["layers"]) - 1:
+            x = f32(oracle.norm_rows("norm", x))
+    return x[0]
+
+
+def _oracle_logits(oracle, m, x):
+    q = oracle.q8_rows(x[None])
+    return oracle.gemv_q8s(oracle.quantize_q8s(m["head"]), E, q[0], q[1], m["rs"])[0]
+
+
+def _gpu_step(bq, m, fold):
+    """Device buffers and the bq_decode_step for the model (kept alive in `keep`)."""
+    import torch
+    keep = []
+    D = lambda a: keep.append(dev(np.ascontiguousarray(a))) or keep[-1]
+    ptr = lambda t: t.data_ptr()
+    blocks = (bq.DecodeBlock * 4)()
+    for l, L in enumerate(m["layers"]):
+        qw = (bq.Weight * 4)()
+        outs = []
+        for i, (name, n, qt, raw) in enumerate(L["qkv"]):
+            qw[i] = bq.make_weight(D(raw), bq.TYPE_Q5_K if qt == "q5k" else bq.TYPE_Q6_K, E, n)
+            outs.append(torch.empty(n, device="cuda"))
+        keep += [qw] + outs
+        optr = (ctypes.c_void_p * 4)(*[o.data_ptr() for o in outs])
+        keep.append(optr)
+        wo = bq.make_weight(D(L["o"]), bq.TYPE_Q5_K, A, E)
+        wg, wu = bq.make_weight(D(L["gate"]), bq.TYPE_Q5_K, E, FF), bq.make_weight(D(L["up"]), bq.TYPE_Q5_K, E, FF)
+        wd = bq.make_weight(D(L["down"]), bq.TYPE_Q6_K, FF, E)
+        keep += [wo, wg, wu, wd]
+        a = blocks[2 * l]
+        a.kind, a.norm_before, a.norm_after = bq.BLOCK_ATTN, int(l == 0), 0
+        a.alpha = ptr(D(L["alpha_a"]))
+        a.qkv, a.n_qkv, a.qkv_out = qw, 4, optr
+        a.attn_out, a.attn_gate, a.sgate, a.n_attn = ptr(D(L["attn_out"])), outs[2].data_ptr(), ptr(D(L["sgate"])), A
+        a.o = ctypes.pointer(wo)
+        f = blocks[2 * l + 1]
+        f.kind, f.norm_before, f.norm_after = bq.BLOCK_FFN, 0, int(l == len(m["layers"]) - 1)
+        f.alpha = ptr(D(L["alpha_f"]))
+        f.gate, f.up, f.down = ctypes.pointer(wg), ctypes.pointer(wu), ctypes.pointer(wd)
+        f.s_gate, f.s_up, f.n_ff = ptr(D(L["sg"])), ptr(D(L["su"])), FF
+        keep.append(outs)
+    head = bq.quantize_q8s(D(m["head"].view(np.int16)), E, V)
+    keep.append(head)
+    x = torch.empty(E, device="cuda")
+    xq = torch.empty(FF, dtype=torch.int8, device="cuda")
+    xd = torch.empty(FF // 32, device="cuda")
+    xs = torch.empty(FF // 32, dtype=torch.int32, device="cuda")
+    proj, fg, fu = torch.empty(E, device="cuda"), torch.empty(FF, device="cuda"), torch.empty(FF, device="cuda")
+    logits = torch.empty(V, device="cuda")
+    keep += [x, xq, xd, xs, proj, fg, fu, logits, blocks]
+    st = bq.DecodeStep()
+    st.n_blocks, st.blocks, st.n_embd, st.fold = 4, blocks, E, fold
+    st.x, st.input_h = x.data_ptr(), ptr(D(m["input_h"]))
+    st.xq, st.xd, st.xsum = xq.data_ptr(), xd.data_ptr(), xs.data_ptr()
+    st.proj, st.ffn_g, st.ffn_u = proj.data_ptr(), fg.data_ptr(), fu.data_ptr()
+    st.head_q8s, st.head_rs, st.vocab, st.logits = head.data_ptr(), ptr(D(m["rs"])), V, logits.data_ptr()
+    x0 = D(m["x0"])
+
+    def reset():
+        x.copy_(x0)
+        q = bq.quantize_q8(x.view(1, E))
+        xq[:E].copy_(q[0][0])
+        xd[:E // 32].copy_(q[1][0])
+        xs[:E // 32].copy_(q[2][0])
+        logits.fill_(float("nan"))
+    return st, keep, reset, x, logits
+
+
+@pytest.mark.parametrize("fold", [0, 1])
+def test_decode_graph_vs_oracle(bq, oracle, fold):
+    import torch
+    print(f"decode step fold={fold}", flush=True)
+    m = _model(bq, oracle)
+    st, keep, reset, x, logits = _gpu_step(bq, m, fold)
+    # block by block: the first nb - 1 blocks on the GPU, then block nb on the
+    # GPU and in the oracle from the same fp32 row
+    prev = m["x0"].copy()
+    for nb in range(1, 5):
+        st.n_blocks = nb
+        reset()
+        bq.decode_enqueue(st)
+        torch.cuda.synchronize()
+        got = host(x).copy()
+        err = oracle.normwise_err(got, _oracle_block(oracle, m, nb - 1, prev).astype(np.float64))
+        print(f"  block {nb - 1}: x vs oracle {err:.2e}", flush=True)
+        assert err < 2e-4, (nb, err)
+        prev = got
+    el = host(logits).copy()
+    lerr = oracle.normwise_err(el, _oracle_logits(oracle, m, prev))
+    print(f"  logits vs oracle head on the final q8 row: {lerr:.2e}", flush=True)
+    assert lerr < 1e-4
+    # the whole chain in the oracle from x0: fold = 0 issues the reference's
+    # own sequence, whose fp32 rounding the oracle reproduces, so its eight
+    # requantizations round alike and the chain stays within 2e-4; fold = 1
+    # reorders fp32 sums, a code on a rounding boundary can move by one and
+    # the difference compounds over the blocks (printed, not asserted)
+    rx = m["x0"].copy()
+    for bi in range(4):
+        rx = _oracle_block(oracle, m, bi, rx)
+    cx, cl = oracle.normwise_err(prev, rx), oracle.normwise_err(el, _oracle_logits(oracle, m, rx))
+    print(f"  whole chain vs oracle chain: x {cx:.2e}, logits {cl:.2e}", flush=True)
+    if fold == 0:
+        assert cx < 2e-4 and cl < 2e-4
+    # graph replays: bit-identical to the eager run
+    ex = prev
+    g = bq.DecodeGraph(st)
+    for rep in range(3):
+        reset()
+        torch.randn(1 << 20, device="cuda").sum()   # unrelated eager work between replays
+        torch.cuda.synchronize()
+        g.launch()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(x).view(np.uint32), ex.view(np.uint32)), rep
+        assert np.array_equal(host(logits).view(np.uint32), el.view(np.uint32)), rep
+    g.close()
+
+
+def test_decode_rejects(bq):
+    st = bq.DecodeStep()
+    assert bq.load().bq_decode_enqueue(ctypes.byref(st), bq._stream()) == bq.BQ_EINVAL
