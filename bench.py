@@ -377,6 +377,30 @@ def gguf_load(bq, torch):
         os.unlink(path)
 
 
+def stream_ceiling(B, torch, sp, sizes=(6504192, 19464192, 23224320, 39018240, 330301440)):
+    """HBM streaming-read ceiling per launch size (k_stream in bq_bench.hip:
+    16-byte loads of every byte once, buffers rotated past the last-level
+    cache), the bound a GEMV of that many bytes can reach in one launch.
+    Sizes: config 1, config 3, the down projection, the fused gate+up and
+    the lm_head launches."""
+    res = {}
+    out = (ctypes.c_double * 4)()
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    for nbytes in sizes:
+        nb = max(2, math.ceil(3 * LLC_BYTES / nbytes))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(nb)]
+        arr = (ctypes.c_void_p * nb)(*[b.data_ptr() for b in bufs])
+        steps = 200 if nbytes < 100e6 else 40
+        r = B.bqb_stream(steps, 10, nb, arr, nbytes, ctypes.c_void_p(sink.data_ptr()), sp, out)
+        if r != 0:
+            raise RuntimeError("bqb_stream failed")
+        us = out[0] / steps * 1e3
+        res[f"{nbytes / 1e6:.1f}MB"] = {"bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
+                                        "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+        del bufs
+    return res
+
+
 def gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out):
     """Config 4 (Q5_K 9216 x 3072 GEMM at M = 2048 / 512 / 8192, both tiers),
     the prompt-batch tail through bq_gemm_b and the Q6_K GEMM (down projection
@@ -455,6 +479,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode FFN step (for kernel traces); implies --no-cpu")
+    ap.add_argument("--stream-only", action="store_true",
+                    help="only the HBM streaming-read ceilings per launch size; prints their JSON object")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the prefill GEMMs of config 4 and the Q6_K GEMM (for counter profiles); "
                          "prints their JSON object")
@@ -479,6 +505,7 @@ def main():
     B.bqb_decode_ffn.argtypes = [I, I, I, I, WP, WP, WP, P, P, P, P, P, P, P, P, P, P, P, P, P]
     B.bqb_gemm.argtypes = [I, I, WP, I, P, P, P, P, P, P, P]
     B.bqb_gemv_rows.argtypes = [I, I, I, WP, I, P, P, P, P, P, P]
+    B.bqb_stream.argtypes = [I, I, I, P, ctypes.c_size_t, P, P, P]
     B.bqb_stack.argtypes = [I, I, I, WP, WP, P, P, P, P, P, P, P, P, P, P]
     B.bqb_q8s.argtypes = [I, I, I, P, I, I, I, P, P, P, P, P, P]
     B.bqb_norm.argtypes = [I, I, I, P, P, P, P, P, I, I, P, P, P, P, P]
@@ -523,6 +550,9 @@ def main():
     torch.cuda.synchronize()
 
     out = D4()
+    if args.stream_only:
+        print(json.dumps({"hbm_read_ceiling": stream_ceiling(B, torch, sp)}), flush=True)
+        return
     if args.gemm_only:
         print(json.dumps({"gemm": gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out)}), flush=True)
         return
@@ -555,8 +585,10 @@ def main():
     achieved = gbs(gu_bytes, gu_ms)
 
     gemm_obj, rows_res, c1_obj, stack_obj, q8s_obj, norm_obj, load_obj = None, None, None, None, None, None, None
+    ceil_obj = None
     if not args.decode_only:
         gemm_obj = gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out)
+        ceil_obj = stream_ceiling(B, torch, sp)
 
         # ---------------------------------------------------------------- config 3 / config 1 GEMV
         rows_res = {}
@@ -626,6 +658,7 @@ def main():
         "down_gemv": {"kernel": "k_gemv<FmtQ6KRaw, 1, 2, 1, 1024, 9216> (quantize t + down)", "avg_launch_us": round(dn_ms * 1e3, 3),
                       "GBps": round(gbs(dn_bytes, dn_ms), 1)},
         "decode_ffn_unfused": unfused,
+        "hbm_read_ceiling": ceil_obj,
         "gemv_config1_3072x3072": c1_obj,
         "gemv_config3_9216x3072": rows_res,
         "config5_whole_stack": stack_obj,

@@ -8,6 +8,7 @@
 // The same launch sequence is what the reference's decode loop issues per
 // token for one FFN block (bruce.cu:7992-8011): quantize the block input,
 // fused gate+up GEMV, quantize the down-projection input, down GEMV.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <utility>
@@ -34,9 +35,48 @@ float elapsed(hipEvent_t a, hipEvent_t b) {
     return ms;
 }
 
+// Streaming-read probe: every byte of `bytes` read once with 16-byte loads
+// (4 per thread, 256 threads per workgroup, consecutive lanes on consecutive
+// 16-byte chunks), reduced to nothing (a never-taken store keeps the loads).
+__global__ void __launch_bounds__(256) k_stream(const uint4* __restrict__ src, size_t n16, uint32_t* sink) {
+    const size_t base = (size_t)blockIdx.x * 1024 + threadIdx.x;
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const size_t j = base + 256 * i;
+        if (j < n16) {
+            const uint4 v = src[j];
+            acc ^= v.x ^ v.y ^ v.z ^ v.w;
+        }
+    }
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
 }  // namespace
 
 extern "C" {
+
+// The HBM streaming-read ceiling for one launch of `bytes`: `steps` timed
+// launches of k_stream over nbufs rotating buffers (so the 256 MB last-level
+// cache cannot serve them), each bracketed by dispatch events.  out[0] =
+// summed kernel durations (ms).
+int bqb_stream(int steps, int warmup, int nbufs, const void* const* bufs, size_t bytes, uint32_t* sink,
+               bq_stream_t st, double* out) {
+    const size_t n16 = bytes / 16;
+    const dim3 grid((unsigned)((n16 + 1023) / 1024));
+    for (int i = 0; i < warmup; ++i)
+        hipLaunchKernelGGL(k_stream, grid, dim3(256), 0, (hipStream_t)st, (const uint4*)bufs[i % nbufs], n16, sink);
+    EventPool pool((size_t)steps * 2);
+    hipDeviceSynchronize();
+    for (int i = 0; i < steps; ++i)
+        hipExtLaunchKernelGGL(k_stream, grid, dim3(256), 0, (hipStream_t)st, pool.ev[2 * i], pool.ev[2 * i + 1], 0,
+                              (const uint4*)bufs[i % nbufs], n16, sink);
+    hipDeviceSynchronize();
+    double t = 0;
+    for (int i = 0; i < steps; ++i) t += elapsed(pool.ev[2 * i], pool.ev[2 * i + 1]);
+    out[0] = t;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 // One decode FFN step per iteration, weight set s = i % nsets (sets rotate so
 // that the working set exceeds the 256 MB last-level cache).
