@@ -369,13 +369,13 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
     return from_hip(launch_mmq_q5k_raw(pt, rows, K, xq, xd, xsum, s, wf, wn));
 }
 
-// bq_gemm_b / bq_gemm_b_fused: one 128-row MMQ tile costs about the same for
-// any row count up to 128 (9216 x 3072 with the K split of a single token
-// tile: 22-30 us prepacked, 30-34 us raw), while the 8-row GEMV chunks stream
-// the weights once per chunk (16 rows 18 us, 24 rows 27 us, 32 rows 36 us):
-// the tile wins from 17 rows prepacked and 28 rows raw.  (The reference
+// bq_gemm_b / bq_gemm_b_fused: the 8-row GEMV chunks stream the weights once
+// per chunk (9216 x 3072: 16 rows 18 us, 32 rows 36 us); the prepacked tier's
+// 32-token MMQ tile takes 13 us at 9 rows and 16 us at 32, so it runs every
+// call above 8 rows.  The raw tier's 128-row tile costs about the same for
+// any row count up to 128 (30-34 us) and wins from 28 rows.  (The reference
 // sends rows 9..95 to its 64x64 MMA tile.)
-constexpr int kGemmBMmqW144 = 17;
+constexpr int kGemmBMmqW144 = 9;
 constexpr int kGemmBMmqRaw = 28;
 }  // namespace
 

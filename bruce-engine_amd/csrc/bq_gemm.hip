@@ -9,6 +9,8 @@
 //   * Workgroup = 4 waves, tile = 128 weight rows x 128 tokens, each wave a
 //     64x64 sub-tile of 2x2 v_mfma_i32_32x32x32_i8 (K = 32 = one Q5_K scale
 //     group per instruction, so the per-group scale is applied once per MFMA).
+//     The W144 kernel also has a 32-token tile (4 waves of 32x32) for calls
+//     up to 1536 rows.
 //   * K advances in 128-value stages.  The raw tier stages a stage in LDS
 //     with a 144-byte row stride (128 codes + 16 B pad: 4-dword bank offset
 //     per row, conflict-free 128-bit reads) and prefetches the next stage into
@@ -295,10 +297,22 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
 // ---------------------------------------------------------------------------
 constexpr int kXS = 128;  // token row stride in LDS (bytes)
 
+// Token-tile height TM of the W144 kernel (128, or 32 up to 1536 rows): the
+// weight tile stays 128 rows, the four waves form a WN x WM grid of
+// (NT x 32) x (MT x 32) sub-tiles (TM 128: 2 x 2 waves of 64 x 64; TM 32:
+// 4 x 1 waves of 32 x 32).
+template <int TM>
+struct W144Geo {
+    static constexpr int WN = TM == 32 ? 4 : 2, WM = 4 / WN;
+    static constexpr int NT = kTN / (32 * WN), MT = TM / (32 * WM);
+    static_assert(NT * WN * 32 == kTN && MT * WM * 32 == TM && MT >= 1, "W144 tile geometry");
+};
+
+template <int TM>
 struct SmemStage {
     uint8_t w[kTN * kW144];  // 18432 B: W144 rows verbatim
-    uint8_t x[kTM * kXS];    // 16384 B: token codes, swizzled 16-byte slots
-    float xs[kTM * 4];       //  2048 B: xd[tok][q]
+    uint8_t x[TM * kXS];     // token codes, swizzled 16-byte slots
+    float xs[TM * 4];        // xd[tok][q]
 };
 
 // Direct-to-LDS 16-byte load: lane i's 16 bytes from gbase + voff land at
@@ -324,7 +338,8 @@ struct Mmq144Dma {
     int tok_hi;                     // lane >> 3
 };
 
-BQ_DEV void mmq144_dma(SmemStage& sb, const uint8_t* wsrc, const int8_t* xq, const float* xd,
+template <int TM>
+BQ_DEV void mmq144_dma(SmemStage<TM>& sb, const uint8_t* wsrc, const int8_t* xq, const float* xd,
                        const Mmq144Dma& o, int m0, int rows, int K, int nb, int s, int wave, int lane) {
 #pragma unroll
     for (int i = 0; i < 5; ++i) {
@@ -333,30 +348,34 @@ BQ_DEV void mmq144_dma(SmemStage& sb, const uint8_t* wsrc, const int8_t* xq, con
     }
     const int8_t* xs0 = xq + (size_t)m0 * K + 128 * s;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < TM / 32; ++i) {
         const int c = wave + 4 * i;
         if (m0 + 8 * c + o.tok_hi < rows) dma16(xs0 + (size_t)(8 * c) * K, o.x_off, sb.x + 1024 * c);
     }
-    if (wave < 2 && m0 + 64 * wave + lane < rows)
+    if (wave < (TM + 63) / 64 && 64 * wave + lane < TM && m0 + 64 * wave + lane < rows)
         dma16(xd + (size_t)(m0 + 64 * wave) * nb + 4 * s, o.xd_off, (uint8_t*)sb.xs + 1024 * wave);
 }
 
 // Operands of one group pair (2qp, 2qp+1): this lane's 16 code bytes of each
 // weight tile / token tile for both groups.
+template <int NT, int MT>
 struct Mmq144Ops {
-    i32x4 a[2][2], b[2][2];  // [nt|mt][group of the pair]
+    i32x4 a[NT][2], b[MT][2];  // [nt|mt][group of the pair]
 };
 
-BQ_DEV void mmq144_ops(Mmq144Ops& o, const SmemStage& sb, int qp, int wn, int wm, int l32, int lh) {
+template <int TM>
+BQ_DEV void mmq144_ops(Mmq144Ops<W144Geo<TM>::NT, W144Geo<TM>::MT>& o, const SmemStage<TM>& sb, int qp, int n0,
+                       int t0, int l32, int lh) {
+    using G = W144Geo<TM>;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const int g = 2 * qp + e;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-            o.a[nt][e] = *(const i32x4*)(sb.w + (wn * 64 + nt * 32 + l32) * kW144 + 32 * g + 16 * lh);
+        for (int nt = 0; nt < G::NT; ++nt)
+            o.a[nt][e] = *(const i32x4*)(sb.w + (n0 + nt * 32 + l32) * kW144 + 32 * g + 16 * lh);
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            const int tok = wm * 64 + mt * 32 + l32;
+        for (int mt = 0; mt < G::MT; ++mt) {
+            const int tok = t0 + mt * 32 + l32;
             o.b[mt][e] = *(const i32x4*)(sb.x + tok * kXS + 16 * ((2 * g + lh) ^ (tok & 7)));
         }
     }
@@ -366,29 +385,32 @@ BQ_DEV void mmq144_ops(Mmq144Ops& o, const SmemStage& sb, int qp, int wn, int wm
 // from one two-block fp32 outer-product MFMA (lanes 0-31 feed group 2qp,
 // lanes 32-63 group 2qp+1), the two dots from two int8 MFMAs, then one convert
 // and one FMA per output and group.  The next pair's operands are read from
-// LDS while this pair is computed.
-BQ_DEV void mmq144_stage(const SmemStage& sb, f32x16 (&acc)[2][2], int wn, int wm, int l32, int lh) {
-    f32x4 wsq[2], xsq[2];  // the stage's four scales per weight row / token: one 16-byte read each
+// LDS while this pair is computed.  n0 / t0: the wave's first weight row /
+// token in the tile.
+template <int TM>
+BQ_DEV void mmq144_stage(const SmemStage<TM>& sb, f32x16 (&acc)[W144Geo<TM>::NT][W144Geo<TM>::MT], int n0,
+                         int t0, int l32, int lh) {
+    using G = W144Geo<TM>;
+    f32x4 wsq[G::NT], xsq[G::MT];  // the stage's four scales per weight row / token: one 16-byte read each
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) wsq[nt] = *(const f32x4*)(sb.w + (wn * 64 + nt * 32 + l32) * kW144 + 128);
+    for (int nt = 0; nt < G::NT; ++nt) wsq[nt] = *(const f32x4*)(sb.w + (n0 + nt * 32 + l32) * kW144 + 128);
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) xsq[mt] = *(const f32x4*)(sb.xs + 4 * (wm * 64 + mt * 32 + l32));
-    Mmq144Ops cur;
-    mmq144_ops(cur, sb, 0, wn, wm, l32, lh);
+    for (int mt = 0; mt < G::MT; ++mt) xsq[mt] = *(const f32x4*)(sb.xs + 4 * (t0 + mt * 32 + l32));
+    Mmq144Ops<G::NT, G::MT> cur;
+    mmq144_ops<TM>(cur, sb, 0, n0, t0, l32, lh);
 #pragma unroll 1
     for (int qp = 0; qp < 2; ++qp) {
-        Mmq144Ops nxt;
-        mmq144_ops(nxt, sb, 1, wn, wm, l32, lh);  // qp = 1: harmless reread
-        float wsv[2], xsv[2];
+        Mmq144Ops<G::NT, G::MT> nxt;
+        mmq144_ops<TM>(nxt, sb, 1, n0, t0, l32, lh);  // qp = 1: harmless reread
+        float wsv[G::NT], xsv[G::MT];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            wsv[t] = qp ? (lh ? wsq[t][3] : wsq[t][2]) : (lh ? wsq[t][1] : wsq[t][0]);
-            xsv[t] = qp ? (lh ? xsq[t][3] : xsq[t][2]) : (lh ? xsq[t][1] : xsq[t][0]);
-        }
+        for (int t = 0; t < G::NT; ++t) wsv[t] = qp ? (lh ? wsq[t][3] : wsq[t][2]) : (lh ? wsq[t][1] : wsq[t][0]);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int t = 0; t < G::MT; ++t) xsv[t] = qp ? (lh ? xsq[t][3] : xsq[t][2]) : (lh ? xsq[t][1] : xsq[t][0]);
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
+        for (int nt = 0; nt < G::NT; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < G::MT; ++mt) {
                 const f32x32 zf = {0.f};
                 const i32x16 zi = {0};
                 const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(wsv[nt], xsv[mt], zf, 0, 0, 0);
@@ -404,22 +426,24 @@ BQ_DEV void mmq144_stage(const SmemStage& sb, f32x16 (&acc)[2][2], int wn, int w
     }
 }
 
-__global__ void __launch_bounds__(256, 2)
+template <int TM>
+__global__ void __launch_bounds__(256, TM == 32 ? 3 : 2)
 k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
            const float* __restrict__ xd, const uint16_t* __restrict__ xdh, int ksplit, float* __restrict__ part) {
-    __shared__ __attribute__((aligned(16))) SmemStage sm0;
-    __shared__ __attribute__((aligned(16))) SmemStage sm1;
+    using G = W144Geo<TM>;
+    __shared__ __attribute__((aligned(16))) SmemStage<TM> sm0;
+    __shared__ __attribute__((aligned(16))) SmemStage<TM> sm1;
     TileMap tm;
     if (!map_tile(blockIdx.x, ntm, ntn, tm)) return;
     int nbase = tm.nt * kTN;
     const int p = part_of_ntile(pt, nbase);
     const int Nloc = pt.N[p];
     const uint8_t* __restrict__ W = (const uint8_t*)pt.W[p];
-    const int m0 = tm.mt * kTM;
+    const int m0 = tm.mt * TM;
     const int nb = K >> 5, nst = K >> 7;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave >> 1, wm = wave & 1;
+    const int n0 = (wave / G::WM) * G::NT * 32, t0 = (wave % G::WM) * G::MT * 32;
     const int l32 = lane & 31, lh = lane >> 5;
     auto wsrc = [&](int s) { return W + ((size_t)s * Nloc + nbase) * kW144; };
     // K split (blockIdx.y of ksplit): stage pairs [s0, s1) of this slice
@@ -431,13 +455,13 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
     dof.x_off = (uint32_t)(lane >> 3) * (uint32_t)K + 16u * (uint32_t)((lane & 7) ^ (lane >> 3));
     dof.xd_off = (uint32_t)lane * (uint32_t)(nb * 4);
 
-    mmq144_dma(sm0, wsrc(s0), xq, xd, dof, m0, rows, K, nb, s0, wave, lane);
+    mmq144_dma<TM>(sm0, wsrc(s0), xq, xd, dof, m0, rows, K, nb, s0, wave, lane);
 
-    f32x16 acc[2][2];
+    f32x16 acc[G::NT][G::MT];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < G::NT; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < G::MT; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
     // min term: sum_g f16(Dm[n][g]) * f16(xdh[m][g]) on fp16 MFMA, K/32 % 16 == 0
@@ -445,21 +469,21 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
     if (kc == 0) {
         const uint16_t* __restrict__ Dm = (const uint16_t*)pt.aux[p];
         for (int g0 = 0; g0 < nb; g0 += 16) {
-            f16x8 a[2], b[2];
+            f16x8 a[G::NT], b[G::MT];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const int n = nbase + wn * 64 + nt * 32 + l32;
+            for (int nt = 0; nt < G::NT; ++nt) {
+                const int n = nbase + n0 + nt * 32 + l32;
                 a[nt] = *(const f16x8*)(Dm + (size_t)n * nb + g0 + 8 * lh);
             }
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                const int m = min(m0 + wm * 64 + mt * 32 + l32, rows - 1);
+            for (int mt = 0; mt < G::MT; ++mt) {
+                const int m = min(m0 + t0 + mt * 32 + l32, rows - 1);
                 b[mt] = *(const f16x8*)(xdh + (size_t)m * nb + g0 + 8 * lh);
             }
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+            for (int nt = 0; nt < G::NT; ++nt)
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
+                for (int mt = 0; mt < G::MT; ++mt)
                     acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[nt], b[mt], acc[nt][mt], 0, 0, 0);
         }
     }
@@ -468,27 +492,27 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
         BQ_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (s + 1 < s1) mmq144_dma(sm1, wsrc(s + 1), xq, xd, dof, m0, rows, K, nb, s + 1, wave, lane);
-        mmq144_stage(sm0, acc, wn, wm, l32, lh);
+        if (s + 1 < s1) mmq144_dma<TM>(sm1, wsrc(s + 1), xq, xd, dof, m0, rows, K, nb, s + 1, wave, lane);
+        mmq144_stage<TM>(sm0, acc, n0, t0, l32, lh);
         if (s + 1 >= s1) break;
         BQ_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (s + 2 < s1) mmq144_dma(sm0, wsrc(s + 2), xq, xd, dof, m0, rows, K, nb, s + 2, wave, lane);
-        mmq144_stage(sm1, acc, wn, wm, l32, lh);
+        if (s + 2 < s1) mmq144_dma<TM>(sm0, wsrc(s + 2), xq, xd, dof, m0, rows, K, nb, s + 2, wave, lane);
+        mmq144_stage<TM>(sm1, acc, n0, t0, l32, lh);
     }
 
     // K split: slice kc's partial sums go to part[kc][part p: rows x N[p]]
     float* __restrict__ Y = ksplit > 1 ? part + split_offset(pt, p, kc, rows) : pt.Y[p];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-        const int m = m0 + wm * 64 + mt * 32 + l32;
+    for (int mt = 0; mt < G::MT; ++mt) {
+        const int m = m0 + t0 + mt * 32 + l32;
         if (m >= rows) continue;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < G::NT; ++nt)
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
-                const int n = nbase + wn * 64 + nt * 32 + 8 * rg + 4 * lh;
+                const int n = nbase + n0 + nt * 32 + 8 * rg + 4 * lh;
                 const f32x4 v = {acc[nt][mt][4 * rg], acc[nt][mt][4 * rg + 1], acc[nt][mt][4 * rg + 2],
                                  acc[nt][mt][4 * rg + 3]};
                 *(f32x4*)(Y + (size_t)m * Nloc + n) = v;
@@ -697,8 +721,8 @@ static dim3 mmq_grid(int ntm, int ntn) {
 // captured in a graph) and give equal bits.
 constexpr int kMaxKSplit = 8;
 
-int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats) {
-    const int ntiles = ((rows + kTM - 1) / kTM) * (ntot / kTN);
+int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, int tm) {
+    const int ntiles = ((rows + tm - 1) / tm) * (ntot / kTN);
     if (ntiles <= 0) return 1;
     const int units = stage_units ? (K >> 7) : (K >> 8);
     int ks = std::min(kMaxKSplit, std::max(1, 512 / ntiles));
@@ -739,14 +763,33 @@ static hipError_t sum_splits(const PartTable& pt, int ks, int rows, const float*
     return hipGetLastError();
 }
 
+// Token-tile height of the W144 kernel for a row count.  The 128-token tile
+// costs the same for any row count up to 128, and at a few hundred rows its
+// tile count fills the 512 workgroup slots unevenly; the 32-token tile (three
+// workgroups per CU, each weight panel re-read per token tile from L2) was
+// measured faster on a 9216 x 3072 weight from 9 up to 1536 rows (9 rows
+// 21.2 -> 13.2 us, 512 rows 76.8 -> 58.5 us) and slower from 2048 (193 vs
+// 205 us), so it takes every call up to 1536 rows.
+int w144_tile_rows(int rows) { return rows <= 1536 ? 32 : 128; }
+
+template <int TM>
+static void launch_w144_tm(const PartTable& pt, int ntm, int ntn, int ks, int rows, int K, const int8_t* xq,
+                           const float* xd, const uint16_t* xdh, hipStream_t st, float* ws) {
+    const dim3 grid(mmq_grid(ntm, ntn).x, ks);
+    launch_kernel(k_mmq_w144<TM>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xdh, ks, ws);
+}
+
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                               const uint16_t* xdh, hipStream_t st, float* ws, size_t ws_floats) {
-    const int ntm = (rows + kTM - 1) / kTM;
+    const int tm = w144_tile_rows(rows);
+    const int ntm = (rows + tm - 1) / tm;
     const int ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0);
-    const dim3 grid(mmq_grid(ntm, ntn).x, ks);
-    launch_kernel(k_mmq_w144, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xdh, ks, ws);
+    const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, tm);
+    if (tm == 32)
+        launch_w144_tm<32>(pt, ntm, ntn, ks, rows, K, xq, xd, xdh, st, ws);
+    else
+        launch_w144_tm<128>(pt, ntm, ntn, ks, rows, K, xq, xd, xdh, st, ws);
     if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
     return hipGetLastError();
 }
@@ -755,7 +798,7 @@ hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, c
                               const int32_t* xsum, hipStream_t st, float* ws, size_t ws_floats) {
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    const int ks = mmq_ksplit(rows, K, ntotal(pt), true, ws ? ws_floats : 0);
+    const int ks = mmq_ksplit(rows, K, ntotal(pt), true, ws ? ws_floats : 0, kTM);
     const dim3 grid(mmq_grid(ntm, ntn).x, ks);
     launch_kernel(k_mmq_q5k_raw, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xsum, ks, ws);
     if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
@@ -766,7 +809,7 @@ hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const
                           hipStream_t st, float* ws, size_t ws_floats) {
     const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0);
+    const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, kTM);
     const dim3 grid(mmq_grid(ntm, ntn).x, ks);
     launch_kernel(k_mmq_q6k_dma, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, ks, ws);
     if (ks > 1) return sum_splits(pt, ks, rows, ws, st);

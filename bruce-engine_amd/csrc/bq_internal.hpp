@@ -75,10 +75,11 @@ hipError_t launch_gemv(GemvKind kind, PartTable pt, int rows, int K, const int8_
 hipError_t launch_repack_q5k(const void* raw, int K, int N, void* w144, uint16_t* dm, hipStream_t st);
 hipError_t launch_repack_q6k(const void* raw, int K, int N, void* w160, hipStream_t st);
 
-// prefill GEMMs (128x128 tiles, int8 MFMA).  ws / ws_floats: the K-split
+// prefill GEMMs (128-row weight tiles, int8 MFMA).  ws / ws_floats: the K-split
 // workspace (nullptr: no split); mmq_ksplit gives the split a launch takes
-// (stage_units: the raw tier, which splits at 128-value stages).
-int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats);
+// (stage_units: the raw tier, which splits at 128-value stages; tm: the
+// token-tile height, 128 or the W144 kernel's 32).
+int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, int tm = 128);
 hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                               const int32_t* xsum, hipStream_t st, float* ws = nullptr, size_t ws_floats = 0);
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,

@@ -487,11 +487,12 @@ def test_mmq_w144_ksplit(bq, oracle, rows):
 
 
 # ---------------------------------------------------------------- dispatcher
-@pytest.mark.parametrize("rows", [3, 16, 17, 20, 27, 28, 43, 60, 130])
+@pytest.mark.parametrize("rows", [3, 8, 9, 12, 16, 17, 20, 27, 28, 43, 60, 130, 1536, 1537])
 def test_gemm_b_dispatch(bq, oracle, rows):
-    """bq_gemm_b: 8-row GEMV chunks below 17 rows (W144) / 28 rows (raw), the
-    MMQ tile from there (K-split for one token tile); bq_try_mmq keeps the
-    reference's rows >= 96."""
+    """bq_gemm_b: 8-row GEMV chunks up to 8 rows (W144) / below 28 rows (raw),
+    the MMQ tile from there (the W144 tier's 32-token tile up to 1536 rows, its
+    128-token tile above; K-split while the tiles leave workgroup slots
+    empty); bq_try_mmq keeps the reference's rows >= 96."""
     import torch
     K, N = 1024, 256
     raw5 = weights(1400, N, K, "q5k")
@@ -504,12 +505,12 @@ def test_gemm_b_dispatch(bq, oracle, rows):
     bq.gemm_b(y, bq.make_weight(g5, bq.TYPE_Q5_K, K, N), rows, gq, gd, gs, xdh)
     torch.cuda.synchronize()
     assert oracle.normwise_err(host(y), oracle.gemm_q5k(raw5, xq, xd, xs)) < TOL
-    # prepacked: the W144 tile (fp16 min term) from 17 rows
+    # prepacked: the W144 tile (fp16 min term) above 8 rows
     w144, dm = bq.repack_q5k(g5, K, N)
     yp = torch.full((rows, N), float("nan"), device="cuda")
     bq.gemm_b(yp, bq.make_weight(g5, bq.TYPE_Q5_K, K, N, rep=w144, rep_min=dm), rows, gq, gd, gs, xdh)
     torch.cuda.synchronize()
-    if rows >= 17:
+    if rows > 8:
         r144, rdm = oracle.repack_q5k_144(raw5, K)
         ref = oracle.gemm_q5k_144(r144, rdm, xq, xd, oracle.fill_xdh(xd, xs), N)
     else:
