@@ -381,7 +381,9 @@ constexpr int kGemmBMmqRaw = 28;
 
 size_t bq_gemm_workspace_bytes(int rows, int K, int n_total) {
     if (rows <= 0 || K <= 0 || n_total <= 0) return 0;
-    const int ks = mmq_ksplit(rows, K, n_total, true, (size_t)-1);
+    // the largest split any tier / tile height takes for this shape
+    const int ks = std::max(mmq_ksplit(rows, K, n_total, true, (size_t)-1, 128),
+                            mmq_ksplit(rows, K, n_total, true, (size_t)-1, 32));
     return ks > 1 ? (size_t)ks * rows * n_total * sizeof(float) : 0;
 }
 

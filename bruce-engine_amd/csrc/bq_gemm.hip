@@ -9,8 +9,8 @@
 //   * Workgroup = 4 waves, tile = 128 weight rows x 128 tokens, each wave a
 //     64x64 sub-tile of 2x2 v_mfma_i32_32x32x32_i8 (K = 32 = one Q5_K scale
 //     group per instruction, so the per-group scale is applied once per MFMA).
-//     The W144 kernel also has a 32-token tile (4 waves of 32x32) for calls
-//     up to 1536 rows.
+//     The W144 and Q6_K kernels also have a 32-token tile (4 waves of 32x32,
+//     three workgroups per CU), chosen per launch by a work estimate.
 //   * K advances in 128-value stages.  The raw tier stages a stage in LDS
 //     with a 144-byte row stride (128 codes + 16 B pad: 4-dword bank offset
 //     per row, conflict-free 128-bit reads) and prefetches the next stage into
@@ -297,10 +297,10 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
 // ---------------------------------------------------------------------------
 constexpr int kXS = 128;  // token row stride in LDS (bytes)
 
-// Token-tile height TM of the W144 kernel (128, or 32 up to 1536 rows): the
-// weight tile stays 128 rows, the four waves form a WN x WM grid of
-// (NT x 32) x (MT x 32) sub-tiles (TM 128: 2 x 2 waves of 64 x 64; TM 32:
-// 4 x 1 waves of 32 x 32).
+// Token-tile height TM of the DMA-staged kernels (W144 and Q6_K; 128 or 32,
+// chosen per launch by mmq_tile_rows): the weight tile stays 128 rows, the
+// four waves form a WN x WM grid of (NT x 32) x (MT x 32) sub-tiles (TM 128:
+// 2 x 2 waves of 64 x 64; TM 32: 4 x 1 waves of 32 x 32).
 template <int TM>
 struct W144Geo {
     static constexpr int WN = TM == 32 ? 4 : 2, WM = 4 / WN;
@@ -532,11 +532,12 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
 //   * 16 + 4 + 16 + 2 direct-to-LDS instructions per stage, two stage buffers
 //     (2 x 38 KB: two workgroups per CU), one barrier per stage.
 // ---------------------------------------------------------------------------
+template <int TM>
 struct SmemQ6Stage {
     uint8_t w[kTN * 128];  // 16384 B: codes, swizzled 16-byte slots
-    uint8_t x[kTM * 128];  // 16384 B: token codes, same swizzle
+    uint8_t x[TM * 128];   // token codes, same swizzle
     float ws[kTN * 8];     //  4096 B: d*sc [row][g16]
-    float xs[kTM * 4];     //  2048 B: xd [tok][q]
+    float xs[TM * 4];      // xd [tok][q]
 };
 
 BQ_DEV int q6_swz(int r) { return (r >> 1) & 7; }
@@ -549,7 +550,8 @@ struct Q6Dma {
     int tok_hi;         // lane >> 3
 };
 
-BQ_DEV void q6_dma(SmemQ6Stage& sb, const uint8_t* wstage, uint32_t row_bytes, const int8_t* xq, const float* xd,
+template <int TM>
+BQ_DEV void q6_dma(SmemQ6Stage<TM>& sb, const uint8_t* wstage, uint32_t row_bytes, const int8_t* xq, const float* xd,
                    const Q6Dma& o, int m0, int rows, int K, int nb, int s, int wave, int lane) {
     // weight codes: instruction c = rows 8c..8c+7
 #pragma unroll
@@ -562,43 +564,47 @@ BQ_DEV void q6_dma(SmemQ6Stage& sb, const uint8_t* wstage, uint32_t row_bytes, c
     // tokens: instruction c = tokens 8c..8c+7 (rows past `rows` skipped)
     const int8_t* xs0 = xq + (size_t)m0 * K + 128 * s;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < TM / 32; ++i) {
         const int c = wave + 4 * i;
         if (m0 + 8 * c + o.tok_hi < rows) dma16(xs0 + (size_t)(8 * c) * K, o.x_off, sb.x + 1024 * c);
     }
-    if (wave < 2 && m0 + 64 * wave + lane < rows)
+    if (wave < (TM + 63) / 64 && 64 * wave + lane < TM && m0 + 64 * wave + lane < rows)
         dma16(xd + (size_t)(m0 + 64 * wave) * nb + 4 * s, o.xd_off, (uint8_t*)sb.xs + 1024 * wave);
 }
 
 // One stage: per 32-group q and tile, the two-block fp32 outer product of the
 // scales of the 16-groups 2q (lanes 0-31) and 2q+1 (lanes 32-63), the two
 // int8 K=16 dots, then one convert and one FMA per output and 16-group.
-BQ_DEV void q6_stage(const SmemQ6Stage& sb, f32x16 (&acc)[2][2], int wn, int wm, int l32, int lh) {
+// n0 / t0: the wave's first weight row / token in the tile.
+template <int TM>
+BQ_DEV void q6_stage(const SmemQ6Stage<TM>& sb, f32x16 (&acc)[W144Geo<TM>::NT][W144Geo<TM>::MT], int n0, int t0,
+                     int l32, int lh) {
+    using G = W144Geo<TM>;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        long a[2][2], b[2][2];  // [tile][16-group half]
+        long a[G::NT][2], b[G::MT][2];  // [tile][16-group half]
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const int r = wn * 64 + nt * 32 + l32;
+            for (int nt = 0; nt < G::NT; ++nt) {
+                const int r = n0 + nt * 32 + l32;
                 a[nt][h] = *(const long*)(sb.w + r * 128 + 16 * ((2 * q + h) ^ q6_swz(r)) + 8 * lh);
             }
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                const int t = wm * 64 + mt * 32 + l32;
+            for (int mt = 0; mt < G::MT; ++mt) {
+                const int t = t0 + mt * 32 + l32;
                 b[mt][h] = *(const long*)(sb.x + t * 128 + 16 * ((2 * q + h) ^ q6_swz(t)) + 8 * lh);
             }
         }
-        float wsv[2], xsv[2];
+        float wsv[G::NT], xsv[G::MT];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) wsv[nt] = sb.ws[8 * (wn * 64 + nt * 32 + l32) + 2 * q + lh];
+        for (int nt = 0; nt < G::NT; ++nt) wsv[nt] = sb.ws[8 * (n0 + nt * 32 + l32) + 2 * q + lh];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) xsv[mt] = sb.xs[4 * (wm * 64 + mt * 32 + l32) + q];
+        for (int mt = 0; mt < G::MT; ++mt) xsv[mt] = sb.xs[4 * (t0 + mt * 32 + l32) + q];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < G::NT; ++nt)
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
+            for (int mt = 0; mt < G::MT; ++mt) {
                 const f32x32 zero32 = {0.f};
                 const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(wsv[nt], xsv[mt], zero32, 0, 0, 0);
                 const i32x16 zero = {0};
@@ -613,22 +619,24 @@ BQ_DEV void q6_stage(const SmemQ6Stage& sb, f32x16 (&acc)[2][2], int wn, int wm,
     }
 }
 
-__global__ void __launch_bounds__(256, 2)
+template <int TM>
+__global__ void __launch_bounds__(256, TM == 32 ? 3 : 2)
 k_mmq_q6k_dma(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
               const float* __restrict__ xd, int ksplit, float* __restrict__ part) {
-    __shared__ __attribute__((aligned(16))) SmemQ6Stage sm0;
-    __shared__ __attribute__((aligned(16))) SmemQ6Stage sm1;
+    using G = W144Geo<TM>;
+    __shared__ __attribute__((aligned(16))) SmemQ6Stage<TM> sm0;
+    __shared__ __attribute__((aligned(16))) SmemQ6Stage<TM> sm1;
     TileMap tm;
     if (!map_tile(blockIdx.x, ntm, ntn, tm)) return;
     int nbase = tm.nt * kTN;
     const int p = part_of_ntile(pt, nbase);
     const int Nloc = pt.N[p];
     const uint8_t* __restrict__ W = (const uint8_t*)pt.W[p];
-    const int m0 = tm.mt * kTM;
+    const int m0 = tm.mt * TM;
     const int nb = K >> 5, nst = K >> 7;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave >> 1, wm = wave & 1;
+    const int n0 = (wave / G::WM) * G::NT * 32, t0 = (wave % G::WM) * G::MT * 32;
     const int l32 = lane & 31, lh = lane >> 5;
     const uint32_t row_bytes = (uint32_t)nst * kW160;
     auto wstage = [&](int s) { return W + (size_t)nbase * row_bytes + (size_t)s * kW160; };
@@ -648,13 +656,13 @@ k_mmq_q6k_dma(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
     // K split (blockIdx.y of ksplit): stage pairs [s0, s1) of this slice
     const int kc = blockIdx.y;
     const int s0 = 2 * (kc * (nst / 2) / ksplit), s1 = 2 * ((kc + 1) * (nst / 2) / ksplit);
-    q6_dma(sm0, wstage(s0), row_bytes, xq, xd, o, m0, rows, K, nb, s0, wave, lane);
+    q6_dma<TM>(sm0, wstage(s0), row_bytes, xq, xd, o, m0, rows, K, nb, s0, wave, lane);
 
-    f32x16 acc[2][2];
+    f32x16 acc[G::NT][G::MT];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < G::NT; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < G::MT; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
@@ -662,27 +670,27 @@ k_mmq_q6k_dma(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
         BQ_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (s + 1 < s1) q6_dma(sm1, wstage(s + 1), row_bytes, xq, xd, o, m0, rows, K, nb, s + 1, wave, lane);
-        q6_stage(sm0, acc, wn, wm, l32, lh);
+        if (s + 1 < s1) q6_dma<TM>(sm1, wstage(s + 1), row_bytes, xq, xd, o, m0, rows, K, nb, s + 1, wave, lane);
+        q6_stage<TM>(sm0, acc, n0, t0, l32, lh);
         if (s + 1 >= s1) break;
         BQ_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (s + 2 < s1) q6_dma(sm0, wstage(s + 2), row_bytes, xq, xd, o, m0, rows, K, nb, s + 2, wave, lane);
-        q6_stage(sm1, acc, wn, wm, l32, lh);
+        if (s + 2 < s1) q6_dma<TM>(sm0, wstage(s + 2), row_bytes, xq, xd, o, m0, rows, K, nb, s + 2, wave, lane);
+        q6_stage<TM>(sm1, acc, n0, t0, l32, lh);
     }
 
     // K split: slice kc's partial sums go to part[kc][part p: rows x N[p]]
     float* __restrict__ Y = ksplit > 1 ? part + split_offset(pt, p, kc, rows) : pt.Y[p];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-        const int m = m0 + wm * 64 + mt * 32 + l32;
+    for (int mt = 0; mt < G::MT; ++mt) {
+        const int m = m0 + t0 + mt * 32 + l32;
         if (m >= rows) continue;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < G::NT; ++nt)
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
-                const int n = nbase + wn * 64 + nt * 32 + 8 * rg + 4 * lh;
+                const int n = nbase + n0 + nt * 32 + 8 * rg + 4 * lh;
                 const f32x4 v = {acc[nt][mt][4 * rg], acc[nt][mt][4 * rg + 1], acc[nt][mt][4 * rg + 2],
                                  acc[nt][mt][4 * rg + 3]};
                 *(f32x4*)(Y + (size_t)m * Nloc + n) = v;
@@ -711,8 +719,9 @@ static dim3 mmq_grid(int ntm, int ntn) {
     return dim3(per * kXcds);
 }
 
-// K split.  A launch with fewer tiles than the 512 workgroup slots (two per
-// CU) leaves CUs idle (one token tile of a 9216-row matrix: 72 tiles), so it
+// K split.  A launch with fewer tiles than the workgroup slots (two per CU
+// for the 128-token tiles, three for the 32-token tiles) leaves CUs idle (one
+// token tile of a 9216-row matrix: 72 tiles), so it
 // is split over K into up to kMaxKSplit slices of whole K units (stage pairs
 // for the DMA-staged kernels, stages for the raw tier) when the caller's
 // workspace holds the slices' partial outputs [slice][part][rows][N[part]];
@@ -725,9 +734,36 @@ int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, in
     const int ntiles = ((rows + tm - 1) / tm) * (ntot / kTN);
     if (ntiles <= 0) return 1;
     const int units = stage_units ? (K >> 7) : (K >> 8);
-    int ks = std::min(kMaxKSplit, std::max(1, 512 / ntiles));
+    const int slots = tm == 32 ? 768 : 512;  // workgroups resident at once (3 or 2 per CU)
+    int ks = std::min(kMaxKSplit, std::max(1, slots / ntiles));
     while (ks > 1 && ((size_t)ks * rows * ntot > ws_floats || units < ks)) --ks;
-    return ks;
+    // the fewest slices with the same longest slice (fewer partial outputs)
+    const int per = (units + ks - 1) / ks;
+    return (units + per - 1) / per;
+}
+
+// Token-tile height (128 or 32) of the DMA-staged kernels for a launch: the
+// one with the smaller estimated work on the busiest CU, ceil(workgroups /
+// 256 CUs) x tile height x the longest K slice, the 32-token tile's work
+// weighted by e32 (its cost per output relative to the 128-token tile on a
+// full GPU, measured at 4096 rows: W144 1.115, Q6_K 1.06).  Short calls take
+// the 32-token tile (the 128-token tile costs the same at any row count up
+// to 128); at a few hundred to a few thousand rows it depends on how evenly
+// the tiles fill the workgroup slots.
+int mmq_tile_rows(int rows, int K, int ntot, size_t ws_floats, float e32) {
+    float best = 0.f;
+    int pick = 128;
+    for (const int tm : {128, 32}) {
+        const int ks = mmq_ksplit(rows, K, ntot, false, ws_floats, tm);
+        const long long ctas = (long long)((rows + tm - 1) / tm) * (ntot / kTN) * ks;
+        const int per = ((K >> 8) + ks - 1) / ks;
+        const float est = (float)((ctas + 255) / 256) * tm * per * (tm == 32 ? e32 : 1.f);
+        if (tm == 128 || est < best) {
+            best = est;
+            pick = tm;
+        }
+    }
+    return pick;
 }
 
 // y_p = sum over the K slices of the workspace (fixed order), 4 floats per
@@ -763,15 +799,6 @@ static hipError_t sum_splits(const PartTable& pt, int ks, int rows, const float*
     return hipGetLastError();
 }
 
-// Token-tile height of the W144 kernel for a row count.  The 128-token tile
-// costs the same for any row count up to 128, and at a few hundred rows its
-// tile count fills the 512 workgroup slots unevenly; the 32-token tile (three
-// workgroups per CU, each weight panel re-read per token tile from L2) was
-// measured faster on a 9216 x 3072 weight from 9 up to 1536 rows (9 rows
-// 21.2 -> 13.2 us, 512 rows 76.8 -> 58.5 us) and slower from 2048 (193 vs
-// 205 us), so it takes every call up to 1536 rows.
-int w144_tile_rows(int rows) { return rows <= 1536 ? 32 : 128; }
-
 template <int TM>
 static void launch_w144_tm(const PartTable& pt, int ntm, int ntn, int ks, int rows, int K, const int8_t* xq,
                            const float* xd, const uint16_t* xdh, hipStream_t st, float* ws) {
@@ -781,7 +808,7 @@ static void launch_w144_tm(const PartTable& pt, int ntm, int ntn, int ks, int ro
 
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                               const uint16_t* xdh, hipStream_t st, float* ws, size_t ws_floats) {
-    const int tm = w144_tile_rows(rows);
+    const int tm = mmq_tile_rows(rows, K, ntotal(pt), ws ? ws_floats : 0, 1.115f);
     const int ntm = (rows + tm - 1) / tm;
     const int ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
@@ -807,11 +834,15 @@ hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, c
 
 hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                           hipStream_t st, float* ws, size_t ws_floats) {
-    const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
+    const int tm = mmq_tile_rows(rows, K, ntotal(pt), ws ? ws_floats : 0, 1.06f);
+    const int ntm = (rows + tm - 1) / tm, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, kTM);
+    const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, tm);
     const dim3 grid(mmq_grid(ntm, ntn).x, ks);
-    launch_kernel(k_mmq_q6k_dma, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, ks, ws);
+    if (tm == 32)
+        launch_kernel(k_mmq_q6k_dma<32>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, ks, ws);
+    else
+        launch_kernel(k_mmq_q6k_dma<128>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, ks, ws);
     if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
     return hipGetLastError();
 }

@@ -92,8 +92,10 @@ def test_workspace_bytes():
     of the prefill GEMMs, at most 32 MiB for any shape."""
     import bq
     L = bq.load()
-    # one token tile of a 9216-row matrix: 72 tiles -> 7 slices of rows x 9216
-    assert L.bq_gemm_workspace_bytes(64, 3072, 9216) == 7 * 64 * 9216 * 4
+    # one token tile of a 9216-row matrix: 72 tiles -> 7 slices for the 512
+    # slots, evened to 6 over the raw tier's 24 stages (4 each); the 32-token
+    # tile (144 tiles, 768 slots) takes 5: the larger is reserved
+    assert L.bq_gemm_workspace_bytes(64, 3072, 9216) == 6 * 64 * 9216 * 4
     assert L.bq_gemm_workspace_bytes(2048, 3072, 9216) == 0      # 1152 tiles fill the GPU
     assert L.bq_gemm_workspace_bytes(0, 3072, 9216) == 0
     worst = max(L.bq_gemm_workspace_bytes(r, 3072, n) for r in range(1, 600, 7) for n in (128, 1024, 9216, 36864))

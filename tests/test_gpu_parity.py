@@ -490,8 +490,8 @@ def test_mmq_w144_ksplit(bq, oracle, rows):
 @pytest.mark.parametrize("rows", [3, 8, 9, 12, 16, 17, 20, 27, 28, 43, 60, 130, 1536, 1537])
 def test_gemm_b_dispatch(bq, oracle, rows):
     """bq_gemm_b: 8-row GEMV chunks up to 8 rows (W144) / below 28 rows (raw),
-    the MMQ tile from there (the W144 tier's 32-token tile up to 1536 rows, its
-    128-token tile above; K-split while the tiles leave workgroup slots
+    the MMQ tile from there (W144 / W160: the 32- or 128-token tile by the
+    launch's work estimate; K-split while the tiles leave workgroup slots
     empty); bq_try_mmq keeps the reference's rows >= 96."""
     import torch
     K, N = 1024, 256

@@ -113,6 +113,31 @@ def test_config4_m(bq, oracle, M):
         del y
 
 
+# ---------------------------------------------------------------- Q6_K GEMM, both token-tile heights
+@pytest.mark.parametrize("M", [96, 768, 1024])
+def test_q6_gemm_tiles(bq, oracle, M):
+    """The Q6_K GEMM over W160 at the down projection's shape (3072 x 9216)
+    for row counts whose work estimate picks the 32-token tile (96, 1024) and
+    the 128-token tile (768); 64 token rows x 256 weight rows checked."""
+    import torch
+    K, N = 9216, 3072
+    print(f"q6 gemm M={M}", flush=True)
+    raw = weights(2200, N, K, "q6k")
+    x, _ = acts(2201 + M, M, K)
+    (xq, xd, xs), g = _q8(oracle, x)
+    gr = dev(raw)
+    w = bq.make_weight(gr, bq.TYPE_Q6_K, K, N, rep=bq.repack_q6k(gr, K, N))
+    rng = np.random.default_rng(M + 1)
+    mi = np.unique(np.concatenate([rng.choice(M, 62, replace=False), [0, M - 1]]))
+    ni = np.unique(np.concatenate([rng.choice(N, 254, replace=False), [0, N - 1]]))
+    y = _nan(M, N)
+    bq.gemm_q6k_mma(y, w, M, g[0], g[1])
+    torch.cuda.synchronize()
+    yh = host(y)
+    assert np.isfinite(yh).all()
+    check(oracle, yh[np.ix_(mi, ni)], oracle.gemm_q6k(raw[ni], xq[mi], xd[mi]), what=f"M={M}")
+
+
 # ---------------------------------------------------------------- the reference model's shapes
 REF_SHAPES = [("q5k", 7168, 2560), ("q5k", 2560, 7168), ("q6k", 2560, 7168)]
 
