@@ -463,7 +463,7 @@ def gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out):
                      "frac": g["frac"], "traffic": traffic_for("mmq_w144_M2048"),
                      "kernel": "k_mmq_w144", "ops_per_launch": 2 * 2048 * FF * K},
         "shapes": gemm,
-        "tail_rows_bq_gemm_b": {"what": "Q5_K 9216x3072 W144, bq_gemm_b: the K-split 32-token MMQ tile "
+        "tail_rows_bq_gemm_b": {"what": "Q5_K 9216x3072 W144, bq_gemm_b: the MMQ tile (32-token at these rows, K-split) "
                                         "above 8 rows", **tail},
         "q6k_down_M2048": {"what": "Q6_K 3072x9216 over W160 (k_mmq_q6k_dma), M=2048", "ms": round(q6ms, 4),
                            "tops": round(q6tops, 1), "frac": round(q6tops / INT8_PEAK_TOPS, 4)},

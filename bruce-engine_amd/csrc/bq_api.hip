@@ -370,13 +370,11 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
 }
 
 // bq_gemm_b / bq_gemm_b_fused: the 8-row GEMV chunks stream the weights once
-// per chunk (9216 x 3072: 16 rows 18 us, 32 rows 36 us); the prepacked tier's
-// 32-token MMQ tile takes 13 us at 9 rows and 16 us at 32, so it runs every
-// call above 8 rows.  The raw tier's 128-row tile costs about the same for
-// any row count up to 128 (30-34 us) and wins from 28 rows.  (The reference
+// per chunk (9216 x 3072: 9 rows 14.5 us, 20 rows 25.6 us, 32 rows 33 us);
+// the MMQ kernels' 32-token tile takes 13-14 us at 9 rows and 16-17 us at 32
+// (prepacked and raw), so both tiers take it above 8 rows.  (The reference
 // sends rows 9..95 to its 64x64 MMA tile.)
-constexpr int kGemmBMmqW144 = 9;
-constexpr int kGemmBMmqRaw = 28;
+constexpr int kGemmBMmqMin = 9;
 }  // namespace
 
 size_t bq_gemm_workspace_bytes(int rows, int K, int n_total) {
@@ -416,8 +414,8 @@ int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const fl
         if (q5) {
             float* ys[1] = {y};
             const bq_weight* wsp[1] = {w};
-            const int r = try_mmq_impl(ys, wsp, 1, rows, xq, xd, xsum, xdh, work, work_bytes, st, kGemmBMmqW144,
-                                       kGemmBMmqRaw);
+            const int r = try_mmq_impl(ys, wsp, 1, rows, xq, xd, xsum, xdh, work, work_bytes, st, kGemmBMmqMin,
+                                       kGemmBMmqMin);
             if (r != BQ_UNSUPPORTED) return r;
         } else if (w->rep && (w->N % 128) == 0) {
             return bq_gemm_q6k_mma(y, w, rows, xq, xd, work, work_bytes, st);
@@ -481,7 +479,7 @@ int bq_gemm_b_fused(float* const* ys, const bq_weight* const* ws, int nparts, in
     if (!ys || !ws || nparts < 1 || nparts > BQ_MAX_PARTS) return BQ_EINVAL;
     if (rows > BQ_MAX_ROWS) {
         const int r = try_mmq_impl(ys, ws, nparts, rows, xq, xd, xsum, xdh, work, work_bytes, st,
-                                   kGemmBMmqW144, kGemmBMmqRaw);
+                                   kGemmBMmqMin, kGemmBMmqMin);
         if (r != BQ_UNSUPPORTED) return r;
     }
     for (int p = 0; p < nparts; ++p) {

@@ -9,8 +9,8 @@
 //   * Workgroup = 4 waves, tile = 128 weight rows x 128 tokens, each wave a
 //     64x64 sub-tile of 2x2 v_mfma_i32_32x32x32_i8 (K = 32 = one Q5_K scale
 //     group per instruction, so the per-group scale is applied once per MFMA).
-//     The W144 and Q6_K kernels also have a 32-token tile (4 waves of 32x32,
-//     three workgroups per CU), chosen per launch by a work estimate.
+//     Each kernel also has a 32-token tile (4 waves of 32x32, three
+//     workgroups per CU), chosen per launch by a work estimate.
 //   * K advances in 128-value stages.  The raw tier stages a stage in LDS
 //     with a 144-byte row stride (128 codes + 16 B pad: 4-dword bank offset
 //     per row, conflict-free 128-bit reads) and prefetches the next stage into
@@ -75,49 +75,63 @@ BQ_DEV int part_of_ntile(const PartTable& pt, int& nbase) {
     return p;
 }
 
-// LDS layout for one stage
-struct Smem {
-    uint8_t w[kTN * kRS];      // weight codes, row stride 144
-    uint8_t x[kTM * kRS];      // token codes, row stride 144
-    float ws[4 * kTN];         // ds   [q][row]
-    float xs[4 * kTM];         // xd   [q][tok]
-    float wm[4 * kTN];         // raw: dmin*m      [q][row]
-    float xm[4 * kTM];         // raw: -(xd*xsum)  [q][tok]
+// Token-tile height TM of the prefill kernels (128 or 32, chosen per launch
+// by mmq_tile_rows): the weight tile stays 128 rows, the
+// four waves form a WN x WM grid of (NT x 32) x (MT x 32) sub-tiles (TM 128:
+// 2 x 2 waves of 64 x 64; TM 32: 4 x 1 waves of 32 x 32).
+template <int TM>
+struct TileGeo {
+    static constexpr int WN = TM == 32 ? 4 : 2, WM = 4 / WN;
+    static constexpr int NT = kTN / (32 * WN), MT = TM / (32 * WM);
+    static_assert(NT * WN * 32 == kTN && MT * WM * 32 == TM && MT >= 1, "tile geometry");
 };
 
-__global__ void __launch_bounds__(256, 2)
+// LDS layout for one stage
+template <int TM>
+struct Smem {
+    uint8_t w[kTN * kRS];      // weight codes, row stride 144
+    uint8_t x[TM * kRS];       // token codes, row stride 144
+    float ws[4 * kTN];         // ds   [q][row]
+    float xs[4 * TM];          // xd   [q][tok]
+    float wm[4 * kTN];         // raw: dmin*m      [q][row]
+    float xm[4 * TM];          // raw: -(xd*xsum)  [q][tok]
+};
+
+template <int TM>
+__global__ void __launch_bounds__(256, TM == 32 ? 3 : 2)
 k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
               const float* __restrict__ xd, const int32_t* __restrict__ xsum, int ksplit,
               float* __restrict__ part) {
-    __shared__ __attribute__((aligned(16))) Smem sm;
+    using G = TileGeo<TM>;
+    __shared__ __attribute__((aligned(16))) Smem<TM> sm;
     TileMap tm;
     if (!map_tile(blockIdx.x, ntm, ntn, tm)) return;
     int nbase = tm.nt * kTN;
     const int p = part_of_ntile(pt, nbase);
     const int Nloc = pt.N[p];
     const uint8_t* __restrict__ W = (const uint8_t*)pt.W[p];
-    const int m0 = tm.mt * kTM;
+    const int m0 = tm.mt * TM;
     const int nb = K >> 5, nst = K >> 7, nsb = K >> 8;
     // K split (blockIdx.y of ksplit): stages [s0, s1) of this slice
     const int kc = blockIdx.y;
     const int s0 = kc * nst / ksplit, s1 = (kc + 1) * nst / ksplit;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wn = wave >> 1, wm = wave & 1;
+    const int n0 = (wave / G::WM) * G::NT * 32, t0 = (wave % G::WM) * G::MT * 32;
     const int l32 = lane & 31, lh = lane >> 5;
 
-    f32x16 acc[2][2];
+    f32x16 acc[G::NT][G::MT];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < G::NT; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < G::MT; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
     // ---- register prefetch of one stage -------------------------------------
-    // tokens: 1024 chunks of 16 B (tok = c >> 3, part = c & 7), 4 per thread;
-    // token scales: threads 0..127 load xd[tok][4s..4s+3] (+ xsum for raw).
-    u32x4 px[4];
+    // tokens: 8 TM chunks of 16 B (tok = c >> 3, part = c & 7), TM / 32 per
+    // thread; token scales: threads 0..TM-1 load xd[tok][4s..4s+3] and xsum.
+    u32x4 px[TM / 32];
     f32x4 pxd;
     i32x4 pxs;
     // weights, raw: thread -> (row = tid >> 1, 64-value half hv = tid & 1)
@@ -125,13 +139,13 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
 
     auto load_stage = [&](int s) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < TM / 32; ++i) {
             const int c = tid + 256 * i, tok = c >> 3, part = c & 7;
             const int m = m0 + tok;
             if (m < rows) px[i] = ld16(xq + (size_t)m * K + 128 * s + 16 * part);
             else px[i] = (u32x4){0, 0, 0, 0};
         }
-        if (tid < kTM) {
+        if (tid < TM) {
             const int m = m0 + tid;
             if (m < rows) {
                 pxd = *(const f32x4*)(xd + (size_t)m * nb + 4 * s);
@@ -155,15 +169,15 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
 
     auto store_stage = [&](int s) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < TM / 32; ++i) {
             const int c = tid + 256 * i, tok = c >> 3, part = c & 7;
             *(u32x4*)(sm.x + tok * kRS + 16 * part) = px[i];
         }
-        if (tid < kTM) {
+        if (tid < TM) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) sm.xs[q * kTM + tid] = pxd[q];
+            for (int q = 0; q < 4; ++q) sm.xs[q * TM + tid] = pxd[q];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) sm.xm[q * kTM + tid] = -(pxd[q] * (float)pxs[q]);
+            for (int q = 0; q < 4; ++q) sm.xm[q * TM + tid] = -(pxd[q] * (float)pxs[q]);
         }
         {
             const int row = tid >> 1, hv = tid & 1;
@@ -207,26 +221,26 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
         // VALU epilogue is one convert and one FMA per output and group.
 #pragma unroll
         for (int qp = 0; qp < 2; ++qp) {
-            i32x4 a[2][2], b[2][2];  // [tile][group of the pair]
-            float wsv[2], xsv[2];
+            i32x4 a[G::NT][2], b[G::MT][2];  // [tile][group of the pair]
+            float wsv[G::NT], xsv[G::MT];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const int q = 2 * qp + e;
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-                    a[nt][e] = *(const i32x4*)(sm.w + (wn * 64 + nt * 32 + l32) * kRS + 32 * q + 16 * lh);
+                for (int nt = 0; nt < G::NT; ++nt)
+                    a[nt][e] = *(const i32x4*)(sm.w + (n0 + nt * 32 + l32) * kRS + 32 * q + 16 * lh);
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
-                    b[mt][e] = *(const i32x4*)(sm.x + (wm * 64 + mt * 32 + l32) * kRS + 32 * q + 16 * lh);
+                for (int mt = 0; mt < G::MT; ++mt)
+                    b[mt][e] = *(const i32x4*)(sm.x + (t0 + mt * 32 + l32) * kRS + 32 * q + 16 * lh);
             }
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) wsv[nt] = sm.ws[(2 * qp + lh) * kTN + wn * 64 + nt * 32 + l32];
+            for (int nt = 0; nt < G::NT; ++nt) wsv[nt] = sm.ws[(2 * qp + lh) * kTN + n0 + nt * 32 + l32];
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) xsv[mt] = sm.xs[(2 * qp + lh) * kTM + wm * 64 + mt * 32 + l32];
+            for (int mt = 0; mt < G::MT; ++mt) xsv[mt] = sm.xs[(2 * qp + lh) * TM + t0 + mt * 32 + l32];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+            for (int nt = 0; nt < G::NT; ++nt)
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt) {
+                for (int mt = 0; mt < G::MT; ++mt) {
                     const f32x32 zero32 = {0.f};
                     const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(wsv[nt], xsv[mt], zero32, 0, 0, 0);
 #pragma unroll
@@ -244,15 +258,15 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
 #pragma unroll
             for (int qp = 0; qp < 2; ++qp) {
                 const int q = 2 * qp + lh;
-                float a[2], b[2];
+                float a[G::NT], b[G::MT];
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) a[nt] = sm.wm[q * kTN + wn * 64 + nt * 32 + l32];
+                for (int nt = 0; nt < G::NT; ++nt) a[nt] = sm.wm[q * kTN + n0 + nt * 32 + l32];
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt) b[mt] = sm.xm[q * kTM + wm * 64 + mt * 32 + l32];
+                for (int mt = 0; mt < G::MT; ++mt) b[mt] = sm.xm[q * TM + t0 + mt * 32 + l32];
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
+                for (int nt = 0; nt < G::NT; ++nt)
 #pragma unroll
-                    for (int mt = 0; mt < 2; ++mt)
+                    for (int mt = 0; mt < G::MT; ++mt)
                         acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[nt], b[mt], acc[nt][mt], 0, 0, 0);
             }
         }
@@ -262,14 +276,14 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
     // K split: slice kc's partial sums go to part[kc][part p: rows x N[p]]
     float* __restrict__ Y = ksplit > 1 ? part + split_offset(pt, p, kc, rows) : pt.Y[p];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-        const int m = m0 + wm * 64 + mt * 32 + l32;
+    for (int mt = 0; mt < G::MT; ++mt) {
+        const int m = m0 + t0 + mt * 32 + l32;
         if (m >= rows) continue;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < G::NT; ++nt)
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
-                const int n = nbase + wn * 64 + nt * 32 + 8 * rg + 4 * lh;
+                const int n = nbase + n0 + nt * 32 + 8 * rg + 4 * lh;
                 const f32x4 v = {acc[nt][mt][4 * rg], acc[nt][mt][4 * rg + 1], acc[nt][mt][4 * rg + 2],
                                  acc[nt][mt][4 * rg + 3]};
                 *(f32x4*)(Y + (size_t)m * Nloc + n) = v;
@@ -296,17 +310,6 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
 //     variant with the MFMAs of the next unit issued ahead was slower.)
 // ---------------------------------------------------------------------------
 constexpr int kXS = 128;  // token row stride in LDS (bytes)
-
-// Token-tile height TM of the DMA-staged kernels (W144 and Q6_K; 128 or 32,
-// chosen per launch by mmq_tile_rows): the weight tile stays 128 rows, the
-// four waves form a WN x WM grid of (NT x 32) x (MT x 32) sub-tiles (TM 128:
-// 2 x 2 waves of 64 x 64; TM 32: 4 x 1 waves of 32 x 32).
-template <int TM>
-struct W144Geo {
-    static constexpr int WN = TM == 32 ? 4 : 2, WM = 4 / WN;
-    static constexpr int NT = kTN / (32 * WN), MT = TM / (32 * WM);
-    static_assert(NT * WN * 32 == kTN && MT * WM * 32 == TM && MT >= 1, "W144 tile geometry");
-};
 
 template <int TM>
 struct SmemStage {
@@ -364,9 +367,9 @@ struct Mmq144Ops {
 };
 
 template <int TM>
-BQ_DEV void mmq144_ops(Mmq144Ops<W144Geo<TM>::NT, W144Geo<TM>::MT>& o, const SmemStage<TM>& sb, int qp, int n0,
+BQ_DEV void mmq144_ops(Mmq144Ops<TileGeo<TM>::NT, TileGeo<TM>::MT>& o, const SmemStage<TM>& sb, int qp, int n0,
                        int t0, int l32, int lh) {
-    using G = W144Geo<TM>;
+    using G = TileGeo<TM>;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const int g = 2 * qp + e;
@@ -388,9 +391,9 @@ BQ_DEV void mmq144_ops(Mmq144Ops<W144Geo<TM>::NT, W144Geo<TM>::MT>& o, const Sme
 // LDS while this pair is computed.  n0 / t0: the wave's first weight row /
 // token in the tile.
 template <int TM>
-BQ_DEV void mmq144_stage(const SmemStage<TM>& sb, f32x16 (&acc)[W144Geo<TM>::NT][W144Geo<TM>::MT], int n0,
+BQ_DEV void mmq144_stage(const SmemStage<TM>& sb, f32x16 (&acc)[TileGeo<TM>::NT][TileGeo<TM>::MT], int n0,
                          int t0, int l32, int lh) {
-    using G = W144Geo<TM>;
+    using G = TileGeo<TM>;
     f32x4 wsq[G::NT], xsq[G::MT];  // the stage's four scales per weight row / token: one 16-byte read each
 #pragma unroll
     for (int nt = 0; nt < G::NT; ++nt) wsq[nt] = *(const f32x4*)(sb.w + (n0 + nt * 32 + l32) * kW144 + 128);
@@ -430,7 +433,7 @@ template <int TM>
 __global__ void __launch_bounds__(256, TM == 32 ? 3 : 2)
 k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
            const float* __restrict__ xd, const uint16_t* __restrict__ xdh, int ksplit, float* __restrict__ part) {
-    using G = W144Geo<TM>;
+    using G = TileGeo<TM>;
     __shared__ __attribute__((aligned(16))) SmemStage<TM> sm0;
     __shared__ __attribute__((aligned(16))) SmemStage<TM> sm1;
     TileMap tm;
@@ -577,9 +580,9 @@ BQ_DEV void q6_dma(SmemQ6Stage<TM>& sb, const uint8_t* wstage, uint32_t row_byte
 // int8 K=16 dots, then one convert and one FMA per output and 16-group.
 // n0 / t0: the wave's first weight row / token in the tile.
 template <int TM>
-BQ_DEV void q6_stage(const SmemQ6Stage<TM>& sb, f32x16 (&acc)[W144Geo<TM>::NT][W144Geo<TM>::MT], int n0, int t0,
+BQ_DEV void q6_stage(const SmemQ6Stage<TM>& sb, f32x16 (&acc)[TileGeo<TM>::NT][TileGeo<TM>::MT], int n0, int t0,
                      int l32, int lh) {
-    using G = W144Geo<TM>;
+    using G = TileGeo<TM>;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         long a[G::NT][2], b[G::MT][2];  // [tile][16-group half]
@@ -623,7 +626,7 @@ template <int TM>
 __global__ void __launch_bounds__(256, TM == 32 ? 3 : 2)
 k_mmq_q6k_dma(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
               const float* __restrict__ xd, int ksplit, float* __restrict__ part) {
-    using G = W144Geo<TM>;
+    using G = TileGeo<TM>;
     __shared__ __attribute__((aligned(16))) SmemQ6Stage<TM> sm0;
     __shared__ __attribute__((aligned(16))) SmemQ6Stage<TM> sm1;
     TileMap tm;
@@ -746,17 +749,19 @@ int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, in
 // one with the smaller estimated work on the busiest CU, ceil(workgroups /
 // 256 CUs) x tile height x the longest K slice, the 32-token tile's work
 // weighted by e32 (its cost per output relative to the 128-token tile on a
-// full GPU, measured at 4096 rows: W144 1.115, Q6_K 1.06).  Short calls take
+// full GPU, measured at 4096 rows: W144 1.115, Q6_K 1.06, raw Q5_K 1.33 --
+// its in-kernel unpack of the weight tile is shared by a quarter of the
+// tokens).  Short calls take
 // the 32-token tile (the 128-token tile costs the same at any row count up
 // to 128); at a few hundred to a few thousand rows it depends on how evenly
 // the tiles fill the workgroup slots.
-int mmq_tile_rows(int rows, int K, int ntot, size_t ws_floats, float e32) {
+int mmq_tile_rows(int rows, int K, int ntot, bool stage_units, size_t ws_floats, float e32) {
     float best = 0.f;
     int pick = 128;
     for (const int tm : {128, 32}) {
-        const int ks = mmq_ksplit(rows, K, ntot, false, ws_floats, tm);
+        const int ks = mmq_ksplit(rows, K, ntot, stage_units, ws_floats, tm);
         const long long ctas = (long long)((rows + tm - 1) / tm) * (ntot / kTN) * ks;
-        const int per = ((K >> 8) + ks - 1) / ks;
+        const int per = ((stage_units ? K >> 7 : K >> 8) + ks - 1) / ks;
         const float est = (float)((ctas + 255) / 256) * tm * per * (tm == 32 ? e32 : 1.f);
         if (tm == 128 || est < best) {
             best = est;
@@ -808,7 +813,7 @@ static void launch_w144_tm(const PartTable& pt, int ntm, int ntn, int ks, int ro
 
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                               const uint16_t* xdh, hipStream_t st, float* ws, size_t ws_floats) {
-    const int tm = mmq_tile_rows(rows, K, ntotal(pt), ws ? ws_floats : 0, 1.115f);
+    const int tm = mmq_tile_rows(rows, K, ntotal(pt), false, ws ? ws_floats : 0, 1.115f);
     const int ntm = (rows + tm - 1) / tm;
     const int ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
@@ -823,18 +828,22 @@ hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, c
 
 hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                               const int32_t* xsum, hipStream_t st, float* ws, size_t ws_floats) {
-    const int ntm = (rows + kTM - 1) / kTM, ntn = ntile_count(pt);
+    const int tm = mmq_tile_rows(rows, K, ntotal(pt), true, ws ? ws_floats : 0, 1.33f);
+    const int ntm = (rows + tm - 1) / tm, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    const int ks = mmq_ksplit(rows, K, ntotal(pt), true, ws ? ws_floats : 0, kTM);
+    const int ks = mmq_ksplit(rows, K, ntotal(pt), true, ws ? ws_floats : 0, tm);
     const dim3 grid(mmq_grid(ntm, ntn).x, ks);
-    launch_kernel(k_mmq_q5k_raw, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xsum, ks, ws);
+    if (tm == 32)
+        launch_kernel(k_mmq_q5k_raw<32>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xsum, ks, ws);
+    else
+        launch_kernel(k_mmq_q5k_raw<128>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xsum, ks, ws);
     if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
     return hipGetLastError();
 }
 
 hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                           hipStream_t st, float* ws, size_t ws_floats) {
-    const int tm = mmq_tile_rows(rows, K, ntotal(pt), ws ? ws_floats : 0, 1.06f);
+    const int tm = mmq_tile_rows(rows, K, ntotal(pt), false, ws ? ws_floats : 0, 1.06f);
     const int ntm = (rows + tm - 1) / tm, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
     const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, tm);

@@ -222,10 +222,10 @@ int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, co
                     void* work, size_t work_bytes, bq_stream_t st);
 
 /* Prompt-batch dispatcher.  Replaces launch_gemm_b (bruce.cu:7428-7568): rows
- * <= 8 -> the verify / GEMV kernels above; Q5_K above 8 rows (W144 prepack)
- * or from 28 rows (raw) and Q6_K W160 above 8 rows -> the MFMA GEMMs (W144
- * and W160: a 32- or 128-token tile, whichever a work estimate for the
- * launch's shape favours; the 8-row chunks stream
+ * <= 8 -> the verify / GEMV kernels above; Q5_K (W144 prepack or raw) and
+ * Q6_K W160 above 8 rows -> the MFMA GEMMs (a 32- or 128-token tile,
+ * whichever a work estimate for the launch's shape favours; the 8-row chunks
+ * stream
  * the weights once per chunk); otherwise 8-row chunks of the multi-row
  * kernels.  (The reference sends rows 9..95 to a 64x64 MMA tile.)  Never returns
  * BQ_UNSUPPORTED for a Q5_K/Q6_K weight with K % 256 == 0. */

@@ -489,10 +489,10 @@ def test_mmq_w144_ksplit(bq, oracle, rows):
 # ---------------------------------------------------------------- dispatcher
 @pytest.mark.parametrize("rows", [3, 8, 9, 12, 16, 17, 20, 27, 28, 43, 60, 130, 1536, 1537])
 def test_gemm_b_dispatch(bq, oracle, rows):
-    """bq_gemm_b: 8-row GEMV chunks up to 8 rows (W144) / below 28 rows (raw),
-    the MMQ tile from there (W144 / W160: the 32- or 128-token tile by the
-    launch's work estimate; K-split while the tiles leave workgroup slots
-    empty); bq_try_mmq keeps the reference's rows >= 96."""
+    """bq_gemm_b: 8-row GEMV chunks up to 8 rows, the MMQ tile above (the 32-
+    or 128-token tile by the launch's work estimate; K-split while the tiles
+    leave workgroup slots empty); bq_try_mmq keeps the reference's
+    rows >= 96."""
     import torch
     K, N = 1024, 256
     raw5 = weights(1400, N, K, "q5k")
