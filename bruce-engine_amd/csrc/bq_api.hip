@@ -41,6 +41,7 @@ int ensure_init() {
         g_dev.lds_per_block = prop.sharedMemPerBlock;
         g_dev.cus = prop.multiProcessorCount;
         q8s_set_cus(g_dev.cus);
+        mmq_set_cus(g_dev.cus);
     });
     return g_init_status;
 }

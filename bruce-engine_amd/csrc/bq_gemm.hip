@@ -723,7 +723,8 @@ static dim3 mmq_grid(int ntm, int ntn) {
 }
 
 // K split.  A launch with fewer tiles than the workgroup slots (two per CU
-// for the 128-token tiles, three for the 32-token tiles) leaves CUs idle (one
+// for the 128-token tiles, three for the 32-token tiles; 512 / 768 on
+// MI355X's 256 CUs) leaves CUs idle (one
 // token tile of a 9216-row matrix: 72 tiles), so it
 // is split over K into up to kMaxKSplit slices of whole K units (stage pairs
 // for the DMA-staged kernels, stages for the raw tier) when the caller's
@@ -733,11 +734,15 @@ static dim3 mmq_grid(int ntm, int ntn) {
 // captured in a graph) and give equal bits.
 constexpr int kMaxKSplit = 8;
 
+// CUs of the device (set by the library's init; MI355X: 256)
+static int g_mmq_cus = 256;
+void mmq_set_cus(int cus) { g_mmq_cus = cus > 0 ? cus : 256; }
+
 int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, int tm) {
     const int ntiles = ((rows + tm - 1) / tm) * (ntot / kTN);
     if (ntiles <= 0) return 1;
     const int units = stage_units ? (K >> 7) : (K >> 8);
-    const int slots = tm == 32 ? 768 : 512;  // workgroups resident at once (3 or 2 per CU)
+    const int slots = (tm == 32 ? 3 : 2) * g_mmq_cus;  // workgroups resident at once (3 or 2 per CU)
     int ks = std::min(kMaxKSplit, std::max(1, slots / ntiles));
     while (ks > 1 && ((size_t)ks * rows * ntot > ws_floats || units < ks)) --ks;
     // the fewest slices with the same longest slice (fewer partial outputs)
@@ -747,7 +752,7 @@ int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, in
 
 // Token-tile height (128 or 32) of the DMA-staged kernels for a launch: the
 // one with the smaller estimated work on the busiest CU, ceil(workgroups /
-// 256 CUs) x tile height x the longest K slice, the 32-token tile's work
+// CUs) x tile height x the longest K slice, the 32-token tile's work
 // weighted by e32 (its cost per output relative to the 128-token tile on a
 // full GPU, measured at 4096 rows: W144 1.115, Q6_K 1.06, raw Q5_K 1.33 --
 // its in-kernel unpack of the weight tile is shared by a quarter of the
@@ -762,7 +767,7 @@ int mmq_tile_rows(int rows, int K, int ntot, bool stage_units, size_t ws_floats,
         const int ks = mmq_ksplit(rows, K, ntot, stage_units, ws_floats, tm);
         const long long ctas = (long long)((rows + tm - 1) / tm) * (ntot / kTN) * ks;
         const int per = ((stage_units ? K >> 7 : K >> 8) + ks - 1) / ks;
-        const float est = (float)((ctas + 255) / 256) * tm * per * (tm == 32 ? e32 : 1.f);
+        const float est = (float)((ctas + g_mmq_cus - 1) / g_mmq_cus) * tm * per * (tm == 32 ? e32 : 1.f);
         if (tm == 128 || est < best) {
             best = est;
             pick = tm;
