@@ -8,7 +8,7 @@ the oracle evaluated in double precision.
 import numpy as np
 import pytest
 
-from helpers import acts, dev, host, weights
+from helpers import acts, check, dev, host, weights
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-4
@@ -398,6 +398,55 @@ def test_mmq_q5k(bq, oracle, prepacked):
 def test_mmq_q5k_ragged_parts(bq, oracle, prepacked):
     # 200 rows (not a multiple of the 128 tile), three parts
     _mmq_case(bq, oracle, 1100, 200, [128, 256, 128], 1536, prepacked)
+
+
+# Row counts that are not multiples of either token tile, multi-part launches
+# with unequal N, and K-split classes: each case's tile height and split come
+# from the launch's work estimate (both heights occur below).
+@pytest.mark.parametrize("prepacked", [False, True])
+@pytest.mark.parametrize("M,Ns,K", [(97, [256, 128], 1024), (129, [128, 384], 1536), (300, [256, 128, 128], 1024),
+                                    (1000, [384], 512)])
+def test_mmq_tile_heights(bq, oracle, prepacked, M, Ns, K):
+    import torch
+    print(f"mmq tiles M={M} Ns={Ns} K={K} prepacked={prepacked}", flush=True)
+    raws = [weights(1200 + i + M, n, K, "q5k") for i, n in enumerate(Ns)]
+    _, (xq, xd, xs) = acts(1250 + M, M, K)
+    ws = []
+    for r, n in zip(raws, Ns):
+        g = dev(r)
+        if prepacked:
+            w144, dm = bq.repack_q5k(g, K, n)
+            ws.append(bq.make_weight(g, bq.TYPE_Q5_K, K, n, rep=w144, rep_min=dm))
+        else:
+            ws.append(bq.make_weight(g, bq.TYPE_Q5_K, K, n))
+    ys = [torch.full((M, n), float("nan"), device="cuda") for n in Ns]
+    xdh = torch.empty((M, K // 32), dtype=torch.int16, device="cuda")
+    gq, gd, gs = _xq_dev(xq, xd, xs)
+    assert bq.try_mmq(ys, ws, M, gq, gd, gs, xdh) == bq.BQ_OK
+    torch.cuda.synchronize()
+    for r, n, y in zip(raws, Ns, ys):
+        if prepacked:
+            w144, dm = oracle.repack_q5k_144(r, K)
+            ref = oracle.gemm_q5k_144(w144, dm, xq, xd, oracle.fill_xdh(xd, xs), n)
+        else:
+            ref = oracle.gemm_q5k(r, xq, xd, xs)
+        check(oracle, host(y), ref, what=f"N={n}")
+
+
+@pytest.mark.parametrize("M", [9, 33, 100, 257])
+def test_q6k_mma_rows(bq, oracle, M):
+    """The Q6_K GEMM over W160 at row counts off both token tiles (N 384,
+    K 2048: the K split is taken at every one of them)."""
+    import torch
+    K, N = 2048, 384
+    raw = weights(1300 + M, N, K, "q6k")
+    _, (xq, xd, xs) = acts(1350 + M, M, K)
+    gq, gd, gs = _xq_dev(xq, xd, xs)
+    g = dev(raw)
+    y = torch.full((M, N), float("nan"), device="cuda")
+    bq.gemm_q6k_mma(y, bq.make_weight(g, bq.TYPE_Q6_K, K, N, rep=bq.repack_q6k(g, K, N)), M, gq, gd)
+    torch.cuda.synchronize()
+    check(oracle, host(y), oracle.gemm_q6k(raw, xq, xd), what=f"M={M}")
 
 
 def test_mmq_unsupported(bq):
