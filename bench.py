@@ -377,6 +377,22 @@ def gguf_load(bq, torch):
         os.unlink(path)
 
 
+def mfma_ceiling(B, torch, sp):
+    """Dense int8 MFMA throughput measured on the box (k_mfma_peak in
+    bq_bench.hip: 8 waves per CU, four independent v_mfma_i32_32x32x32_i8
+    chains per wave, no memory traffic), beside the published 5.0 POPS."""
+    out = (ctypes.c_double * 4)()
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    props = torch.cuda.get_device_properties(0)
+    blocks = 2 * props.multi_processor_count
+    r = B.bqb_mfma_peak(blocks, 20000, ctypes.c_void_p(sink.data_ptr()), sp, out)
+    if r != 0:
+        raise RuntimeError("bqb_mfma_peak failed")
+    tops = out[1] / (out[0] * 1e-3) / 1e12
+    return {"kernel": "k_mfma_peak", "tops": round(tops, 1), "frac_of_published": round(tops / INT8_PEAK_TOPS, 4),
+            "cus": props.multi_processor_count}
+
+
 def stream_ceiling(B, torch, sp, sizes=(6504192, 19464192, 23224320, 39018240, 330301440)):
     """HBM streaming-read ceiling per launch size (k_stream in bq_bench.hip:
     16-byte loads of every byte once, buffers rotated past the last-level
@@ -391,7 +407,8 @@ def stream_ceiling(B, torch, sp, sizes=(6504192, 19464192, 23224320, 39018240, 3
         bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(nb)]
         arr = (ctypes.c_void_p * nb)(*[b.data_ptr() for b in bufs])
         steps = 200 if nbytes < 100e6 else 40
-        r = B.bqb_stream(steps, 10, nb, arr, nbytes, ctypes.c_void_p(sink.data_ptr()), sp, out)
+        # warm-up: one pass over every buffer (a fresh buffer's first touch is slower)
+        r = B.bqb_stream(steps, nb + 10, nb, arr, nbytes, ctypes.c_void_p(sink.data_ptr()), sp, out)
         if r != 0:
             raise RuntimeError("bqb_stream failed")
         us = out[0] / steps * 1e3
@@ -421,6 +438,12 @@ def gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out):
             kms = out[1] / gsteps
             tops = 2.0 * M * FF * K / (kms * 1e-3) / 1e12
             res[name] = {"ms": round(kms, 4), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)}
+        # bytes of one launch (weights as streamed: W144 + Dm or GGUF; q8 X
+        # with xd, xsum, xdh; fp32 Y) over the time, against 8 TB/s: the GEMM
+        # is near the int8 ridge at M = 512 (SURVEY config 4)
+        xbytes = M * K + M * (K // 32) * 10
+        for name, wb in (("w144", gw144.nbytes + gdm.nbytes), ("raw", g_gate.nbytes)):
+            res[name]["hbm_frac"] = round((wb + xbytes + 4 * M * FF) / (res[name]["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
         gemm[f"M{M}"] = res
         del xm, mq, md, ms_, mh, ym
     # prompt-batch tail (rows 9..95, bq_gemm_b: 8-row GEMV chunks or the
@@ -457,6 +480,7 @@ def gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out):
     del w160, x6, q6q, q6d, y6
     g = gemm["M2048"]["w144"]
     gemm_obj = {
+        "mfma_int8_ceiling": mfma_ceiling(B, torch, sp),
         "config": "prefill GEMM Q5_K 9216x3072 (W144 repack, fp16 min term), M=2048 q8 tokens, fp32 out",
         "value": g["tops"], "unit": "TOPS", "ms": g["ms"],
         "roofline": {"bound": "mfma", "achieved": g["tops"], "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
@@ -479,6 +503,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode FFN step (for kernel traces); implies --no-cpu")
+    ap.add_argument("--mfma-only", action="store_true",
+                    help="only the dense int8 MFMA throughput probe; prints its JSON object")
     ap.add_argument("--stream-only", action="store_true",
                     help="only the HBM streaming-read ceilings per launch size; prints their JSON object")
     ap.add_argument("--gemm-only", action="store_true",
@@ -506,6 +532,7 @@ def main():
     B.bqb_gemm.argtypes = [I, I, WP, I, P, P, P, P, P, P, P]
     B.bqb_gemv_rows.argtypes = [I, I, I, WP, I, P, P, P, P, P, P]
     B.bqb_stream.argtypes = [I, I, I, P, ctypes.c_size_t, P, P, P]
+    B.bqb_mfma_peak.argtypes = [I, I, P, P, P]
     B.bqb_stack.argtypes = [I, I, I, WP, WP, P, P, P, P, P, P, P, P, P, P]
     B.bqb_q8s.argtypes = [I, I, I, P, I, I, I, P, P, P, P, P, P]
     B.bqb_norm.argtypes = [I, I, I, P, P, P, P, P, I, I, P, P, P, P, P]
@@ -550,6 +577,9 @@ def main():
     torch.cuda.synchronize()
 
     out = D4()
+    if args.mfma_only:
+        print(json.dumps({"mfma_int8_ceiling": mfma_ceiling(B, torch, sp)}), flush=True)
+        return
     if args.stream_only:
         print(json.dumps({"hbm_read_ceiling": stream_ceiling(B, torch, sp)}), flush=True)
         return
@@ -595,17 +625,25 @@ def main():
         xr = torch.from_numpy(synth.gaussian(SEED + 7, (8, K))).cuda()
         rq, rd, rs = bq.quantize_q8(xr)
         yr = torch.empty((8, FF), device="cuda")
-        gsets = (bq.Weight * nsets)(*[gates[s] for s in range(nsets)])
+        # config 3 streams one 19.5 MB matrix: rotate >= 3 x the last-level
+        # cache of copies (the gate sets plus extra device copies)
+        n3 = max(nsets, math.ceil(3 * LLC_BYTES / w_gate.nbytes))
+        c3g = [g_gate.clone() for _ in range(n3 - nsets)]
+        gsets = (bq.Weight * n3)(*([gates[s] for s in range(nsets)] +
+                                   [bq.make_weight(a, bq.TYPE_Q5_K, K, FF) for a in c3g]))
         for rows in (1, 2, 4, 8):
-            r = B.bqb_gemv_rows(100, 10, nsets, gsets, rows, ptr(rq), ptr(rd), ptr(rs), ptr(yr), sp, out)
+            # warm-up: one pass over every copy (the first touch of a fresh
+            # copy is slower), then the timed launches
+            r = B.bqb_gemv_rows(100, n3 + 10, n3, gsets, rows, ptr(rq), ptr(rd), ptr(rs), ptr(yr), sp, out)
             kms = out[1] / 100
             rows_res[f"rows{rows}"] = {"us": round(kms * 1e3, 2),
                                        "GBps": round(gbs(w_gate.nbytes + q8_bytes(rows, K) + 4 * rows * FF, kms), 1)}
+        del c3g
         c1 = synth.quantize_q5k(synth.gaussian(SEED + 8, (K, K), 0.02))
         n1 = max(2, math.ceil(3 * LLC_BYTES / c1.nbytes))
         c1g = [torch.from_numpy(c1).cuda() for _ in range(n1)]
         c1w = (bq.Weight * n1)(*[bq.make_weight(a, bq.TYPE_Q5_K, K, K) for a in c1g])
-        r = B.bqb_gemv_rows(200, 10, n1, c1w, 1, ptr(rq), ptr(rd), ptr(rs), ptr(yr), sp, out)
+        r = B.bqb_gemv_rows(200, n1 + 10, n1, c1w, 1, ptr(rq), ptr(rd), ptr(rs), ptr(yr), sp, out)
         c1ms = out[1] / 200
         del c1g
         c1_obj = {"us": round(c1ms * 1e3, 2), "GBps": round(gbs(c1.nbytes + q8_bytes(1, K) + 4 * K, c1ms), 1)}

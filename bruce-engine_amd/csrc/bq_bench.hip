@@ -78,6 +78,40 @@ int bqb_stream(int steps, int warmup, int nbufs, const void* const* bufs, size_t
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// Dense int8 MFMA throughput: every wave runs `iters` rounds of four
+// independent v_mfma_i32_32x32x32_i8 chains (no memory traffic in the loop;
+// one operand changes per round so nothing is hoisted), 8 waves per CU.
+__global__ void __launch_bounds__(256) k_mfma_peak(int iters, uint32_t* sink) {
+    typedef int i32x4v __attribute__((ext_vector_type(4)));
+    typedef int i32x16v __attribute__((ext_vector_type(16)));
+    i32x4v a = {(int)threadIdx.x, 3, 5, 7}, b = {1, 2, 3, (int)threadIdx.x};
+    i32x16v c0 = {0}, c1 = {0}, c2 = {0}, c3 = {0};
+    for (int it = 0; it < iters; ++it) {
+        a.x += 1;
+        c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c3, 0, 0, 0);
+    }
+    int t = 0;
+    for (int i = 0; i < 16; ++i) t += c0[i] ^ c1[i] ^ c2[i] ^ c3[i];
+    if (t == 0x7fffffff) sink[threadIdx.x & 3] = (uint32_t)t;
+}
+
+// out[0] = the launch's duration (ms, dispatch events), out[1] = int8 ops
+// (2 x 32 x 32 x 32 per MFMA)
+int bqb_mfma_peak(int blocks, int iters, uint32_t* sink, bq_stream_t st, double* out) {
+    hipLaunchKernelGGL(k_mfma_peak, dim3(blocks), dim3(256), 0, (hipStream_t)st, iters / 10 + 1, sink);
+    EventPool pool(2);
+    hipDeviceSynchronize();
+    hipExtLaunchKernelGGL(k_mfma_peak, dim3(blocks), dim3(256), 0, (hipStream_t)st, pool.ev[0], pool.ev[1], 0, iters,
+                          sink);
+    hipDeviceSynchronize();
+    out[0] = elapsed(pool.ev[0], pool.ev[1]);
+    out[1] = (double)blocks * 4 * iters * 4 * 65536.0;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // One decode FFN step per iteration, weight set s = i % nsets (sets rotate so
 // that the working set exceeds the 256 MB last-level cache).
 // mode 0: nsets consecutive steps (sets 0..nsets-1) are captured into one
