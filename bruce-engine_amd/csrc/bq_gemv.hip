@@ -164,7 +164,7 @@ struct FmtQ5K {
 // lane 4b+r feeds weight row r's code dword as B and activation row 4ms+r's
 // dword as A, so after 8 instructions per 32-value sub-block the lane holds
 // the exact integer dots of its weight row with activation rows 4ms..4ms+3.
-// The float epilogue is the dot4 path's expression, term for term.
+// The float epilogue runs its scale products on the matrix cores as well (below).
 template <int MR>
 BQ_DEV void q5k_dot_mm(const FmtQ5K::Task& a, int t, const ActLds& act, int K, float (&acc)[MR], int lane) {
     const int jp = t & 3, j0 = 2 * jp, j1 = j0 + 1;
@@ -197,15 +197,26 @@ BQ_DEV void q5k_dot_mm(const FmtQ5K::Task& a, int t, const ActLds& act, int K, f
             c0 = __builtin_amdgcn_mfma_i32_4x4x4i8(xa, (int)u0[k], c0, 0, 0, 0);
             c1 = __builtin_amdgcn_mfma_i32_4x4x4i8(xb, (int)u1[k], c1, 0, 0, 0);
         }
+        // Scales on the matrix cores too (v_mfma_f32_4x4x1f32, same block
+        // layout): lane 4b+r feeds activation row 4ms+r's xd (and xd * xsum)
+        // as A and its weight row's ds (dm) as B, so lane 4b+r receives
+        // xd[4ms+q] * ds[r] for q = 0..3 -- the scale products -- and the
+        // min terms (xd * xsum)[4ms+q] * dm[r].  The epilogue is then one
+        // convert and one FMA per activation row and sub-block:
+        // sum_j (ds_j * xd) * dot_j - dm_j * (xd * xsum), the reference
+        // verify kernel's form (bruce.cu:6007-6010).
+        const float2 xdv = *(const float2*)(act.xd + (m < MR ? m : MR - 1) * nb + g0);
+        const int2 xsv = *(const int2*)(act.xs + (m < MR ? m : MR - 1) * nb + g0);
+        const f32x4 zf = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 s0 = __builtin_amdgcn_mfma_f32_4x4x1f32(xdv.x, ds0, zf, 0, 0, 0);
+        const f32x4 s1 = __builtin_amdgcn_mfma_f32_4x4x1f32(xdv.y, ds1, zf, 0, 0, 0);
+        f32x4 mn = __builtin_amdgcn_mfma_f32_4x4x1f32(xdv.x * (float)xsv.x, dm0, zf, 0, 0, 0);
+        mn = __builtin_amdgcn_mfma_f32_4x4x1f32(xdv.y * (float)xsv.y, dm1, mn, 0, 0, 0);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int mm = 4 * ms + q;
-            if (mm < MR) {
-                const float2 xdv = *(const float2*)(act.xd + mm * nb + g0);
-                const int2 xsv = *(const int2*)(act.xs + mm * nb + g0);
-                acc[mm] += xdv.x * (ds0 * (float)c0[q] - dm0 * (float)xsv.x) +
-                           xdv.y * (ds1 * (float)c1[q] - dm1 * (float)xsv.y);
-            }
+            if (mm < MR)
+                acc[mm] += __builtin_fmaf(s1[q], (float)c1[q], __builtin_fmaf(s0[q], (float)c0[q], -mn[q]));
         }
     }
 }
