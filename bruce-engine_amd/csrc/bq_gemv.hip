@@ -31,14 +31,16 @@
 namespace bq {
 
 constexpr int kRowsPerTile = 4;    // one row per 16-lane DPP row
-// Q5_K multi-row: dot products on the matrix cores from this many activation
-// rows up.  The matrix-core lane map (4 lanes = one task across the 4 rows)
-// loses the address merging of the per-block header / qh loads that the
-// dot4 map gets (4 lanes of one row read the same 16 bytes), measured at
-// +0.8 us for 2..4 rows with dot4 arithmetic on the new map; from 6 rows the
-// faster arithmetic wins (9216 x 3072: 6 / 7 / 8 rows 10.5 / 11.7 / 13.0 ->
-// 10.3 / 10.9 / 11.5 us).
-constexpr int kQ5kMfmaMinRows = 6;
+// Q5_K multi-row: dot products (and, since the scale products moved to
+// v_mfma_f32_4x4x1f32, the epilogue's scale products) on the matrix cores
+// from this many activation rows up.  The matrix-core lane map (4 lanes = one
+// task across the 4 rows) loses the address merging of the per-block header /
+// qh loads that the dot4 map gets (4 lanes of one row read the same 16
+// bytes).  Measured with 40 rotating copies (dot4 -> matrix cores, us):
+// 9216 x 3072 4 / 5 rows 7.95 / 8.84 -> 7.2 / 8.45, 18432 x 3072 12.1 / 14.7
+// -> 10.0 / 12.6, 3072 x 3072 5.1 / 5.6 -> 4.5 / 5.0; at 2 / 3 rows dot4
+// stays ahead or level (9216 x 3072 2 rows 6.4 vs 6.7-6.8).
+constexpr int kQ5kMfmaMinRows = 4;
 // Q6_K (W160 and raw) from 3 rows: no per-block header is shared between the
 // lanes of a row there (W160), or only 2 of 8 loads (raw), and the dot4 path
 // needs two dot4 per dword for the -32 offset (raw).  Measured 3072 x 9216,
@@ -885,12 +887,11 @@ static void build_tiles(PartTable& pt, int rows_per_tile = kRowsPerTile) {
 //     else 3 from 20M values (gate+up 2 x 9216 x 3072: 12.07 -> 9.02), else
 //     1 (QKV 5120 x 3072: 5.66 -> 5.40; O 3072 x 4096: 4.84 -> 4.70)
 //   Q5_K, q8 input (9216 x 3072 = 28M, 18432 x 3072 = 57M, 3072 x 4096 = 12.6M):
-//     6..8 rows (matrix-core dots): 3 from 20M (28M, 8 rows 11.0 -> 9.6; 57M
-//       18.9 -> 14.6), else 1 (12.6M, 8 rows 8.9 -> 8.3)
-//     5 rows: 2 from 20M (9.65 / 9.63 -> 9.16), else 1 (7.0 -> 6.2)
-//     1..4 rows: 3 from 40M (57M: 1 row 9.4 -> 8.5, 2 rows 10.0 -> 9.4), else
-//       1 (28M, 4 rows 8.5 -> 7.8; 12.6M, 2 rows 5.2 -> 4.5; 5120 x 3072, 1
-//       row 5.15 -> 4.97); below 12M values 1..2 rows keep 3 (3072 x 3072 tie)
+//     4..8 rows (matrix-core dots): 3 from 20M (28M, 8 rows 11.0 -> 9.6; 57M
+//       18.9 -> 14.6, 4 rows 13.2 -> 9.7), else 1 (12.6M, 8 rows 8.9 -> 8.3)
+//     1..3 rows: 3 from 40M (57M: 1 row 9.4 -> 8.5, 2 rows 10.0 -> 9.4), else
+//       1 (12.6M, 2 rows 5.2 -> 4.5; 5120 x 3072, 1 row 5.15 -> 4.97); below
+//       12M values 1..2 rows keep 3 (3072 x 3072 tie)
 //   Q6_K: 2 once rows * K staged activation bytes per workgroup are large
 //     (want several row tiles per workgroup), else 3:
 //     raw 3072 x 9216: 3 up to 5 rows (4 rows 10.6 -> 10.2), 2 from 6 rows
@@ -905,7 +906,6 @@ int sps_cap(GemvKind kind, int K, long long N, int MR, bool fused) {
     if (kind == GemvKind::Q6KRep) return MR * K >= 3 * 9216 ? 2 : 3;
     const long long nk = N * K;
     if (MR >= kQ5kMfmaMinRows) return nk >= (20ll << 20) ? 3 : 1;
-    if (MR == 5) return nk >= (20ll << 20) ? 2 : 1;
     if (nk >= (40ll << 20)) return 3;
     if (nk < (12ll << 20) && MR <= 2) return 3;
     return 1;
