@@ -287,14 +287,20 @@ BQ_DEV void q6rep_dot_mm(const FmtQ6KRep::Task& a, int t, const ActLds& act, int
 #pragma unroll
             for (int i = 0; i < 4; ++i) c[g] = __builtin_amdgcn_mfma_i32_4x4x4i8((int)x[i], (int)a.c[g][i], c[g], 0, 0, 0);
         }
+        // scale products xd[4ms+q] * (d*sc)[g] on v_mfma_f32_4x4x1f32 (see q5k_dot_mm)
+        const float2 xdv = *(const float2*)(act.xd + (m < MR ? m : MR - 1) * nb + (k0 >> 5));
+        const f32x4 zf = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 s0 = __builtin_amdgcn_mfma_f32_4x4x1f32(xdv.x, a.sc.x, zf, 0, 0, 0);
+        const f32x4 s1 = __builtin_amdgcn_mfma_f32_4x4x1f32(xdv.x, a.sc.y, zf, 0, 0, 0);
+        const f32x4 s2 = __builtin_amdgcn_mfma_f32_4x4x1f32(xdv.y, a.sc.z, zf, 0, 0, 0);
+        const f32x4 s3 = __builtin_amdgcn_mfma_f32_4x4x1f32(xdv.y, a.sc.w, zf, 0, 0, 0);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int mm = 4 * ms + q;
-            if (mm < MR) {
-                const float2 xdv = *(const float2*)(act.xd + mm * nb + (k0 >> 5));
-                acc[mm] += xdv.x * (a.sc.x * (float)c[0][q] + a.sc.y * (float)c[1][q]) +
-                           xdv.y * (a.sc.z * (float)c[2][q] + a.sc.w * (float)c[3][q]);
-            }
+            if (mm < MR)
+                acc[mm] += __builtin_fmaf(s3[q], (float)c[3][q],
+                                          __builtin_fmaf(s2[q], (float)c[2][q],
+                                                         __builtin_fmaf(s1[q], (float)c[1][q], s0[q] * (float)c[0][q])));
         }
     }
 }
@@ -421,13 +427,21 @@ struct FmtQ6KRaw {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) c[u] = __builtin_amdgcn_mfma_i32_4x4x4i8((int)x[i], (int)q[u][i], c[u], 0, 0, 0);
             }
+            // scale products xd[4ms+qq] * (d*sc)[u] on v_mfma_f32_4x4x1f32 (the
+            // block layout of the int8 dots; see q5k_dot_mm)
+            const int ma = m < MR ? m : MR - 1;
+            const f32x4 zf = {0.f, 0.f, 0.f, 0.f};
+            f32x4 sx[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                sx[u] = __builtin_amdgcn_mfma_f32_4x4x1f32(act.xd[ma * nb + ((kb + 32 * u) >> 5)], sc[u], zf, 0, 0, 0);
 #pragma unroll
             for (int qq = 0; qq < 4; ++qq) {
                 const int mm = 4 * ms + qq;
                 if (mm < MR) {
-                    float v = 0.f;
+                    float v = sx[0][qq] * (float)c[0][qq];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) v += act.xd[mm * nb + ((kb + 32 * u) >> 5)] * sc[u] * (float)c[u][qq];
+                    for (int u = 1; u < 4; ++u) v = __builtin_fmaf(sx[u][qq], (float)c[u][qq], v);
                     acc[mm] += v;
                 }
             }
