@@ -223,16 +223,52 @@ BQ_DEV void q5k_dot_mm(const FmtQ5K::Task& a, int t, const ActLds& act, int K, f
     }
 }
 
-// sum over the 16 lanes 4i + (lane & 3): the row16_sum scan (shift 1, 2, 4,
-// 8 tasks, zero below the first) on the multi-row lane map; lanes 60..63 end
-// with the totals, in the same association as row16_sum
-BQ_DEV float lane4_sum(float v, int li) {
+// The MR rows' sums over the 16 task lanes 4i + (lane & 3) of the multi-row
+// lane map at once, as a reduce-scatter butterfly: each exchange with the
+// lane 4d apart (d = 8, 4, 2 while the lane carries more than one row) keeps
+// the half of its rows selected by bit d of i and adds the partner's copy of
+// them, so a lane ends with one row m = rows_of(i), which the remaining
+// exchanges (plain sums) complete.  P = MR rounded up to a power of two
+// shuffles instead of 4 per row: 8 for 5..8 rows against 32.  Lanes with
+// (i & (16 / P - 1)) == 0 hold distinct rows; m >= MR are padding.
+// b where bit `lane` of the wave mask is set, else a: one v_cndmask_b32.
+// (A C select here lets the compiler turn the butterfly's selects between
+// array elements into a dynamically indexed array: a compare-and-select chain
+// over every element per select.)
+BQ_DEV float lane_sel(float a, float b, uint64_t mask) {
+    float r;
+    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
+    return r;
+}
+
+template <int MR>
+BQ_DEV float lane4_scatter_sum(const float (&acc)[MR], int li, int& m) {
+    constexpr int P = MR > 4 ? 8 : MR > 2 ? 4 : MR > 1 ? 2 : 1;
+    float v[P];
 #pragma unroll
-    for (int sh = 1; sh < 16; sh <<= 1) {
-        const float u = __shfl_up(v, 4 * sh, 64);
-        v += li >= sh ? u : 0.f;
+    for (int k = 0; k < P; ++k) v[k] = k < MR ? acc[k] : 0.f;
+    m = 0;
+    int d = 8;
+#pragma unroll
+    for (int h = P / 2; h >= 1; h >>= 1, d >>= 1) {
+        const bool up = (li & d) != 0;
+        const uint64_t um = __builtin_amdgcn_ballot_w64(up);
+#pragma unroll
+        for (int k = 0; k < h; ++k) {
+            const float keep = lane_sel(v[k], v[k + h], um);
+            const float send = lane_sel(v[k + h], v[k], um);
+            v[k] = keep + __shfl_xor(send, 4 * d, 64);
+        }
+        m += up ? h : 0;
     }
-    return v;
+#pragma unroll
+    for (; d >= 1; d >>= 1) v[0] += __shfl_xor(v[0], 4 * d, 64);
+    return v[0];
+}
+
+template <int MR>
+BQ_DEV constexpr int lane4_scatter_mask() {
+    return 16 / (MR > 4 ? 8 : MR > 2 ? 4 : MR > 1 ? 2 : 1) - 1;
 }
 
 struct FmtQ6KRep {
@@ -846,17 +882,29 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
             if (g < 2 && li == 15 && rowok) fq.out[row] = silu_mul(v, u, fq.c[row], fq.d[row]);
             return;
         }
+        if constexpr (kMmLanes) {
+            int m;
+            const float v = lane4_scatter_sum<MR>(acc, li, m);
+            if ((li & lane4_scatter_mask<MR>()) == 0 && m < MR && rowok) Y[(size_t)m * Nloc + row] = v;
+        } else {
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            const float v = kMmLanes ? lane4_sum(acc[m], li) : row16_sum(acc[m]);
-            if (li == 15 && rowok) Y[(size_t)m * Nloc + row] = v;
+            for (int m = 0; m < MR; ++m) {
+                const float v = row16_sum(acc[m]);
+                if (li == 15 && rowok) Y[(size_t)m * Nloc + row] = v;
+            }
         }
         return;
     }
+    if constexpr (kMmLanes) {
+        int m;
+        const float v = lane4_scatter_sum<MR>(acc, li, m);
+        if ((li & lane4_scatter_mask<MR>()) == 0 && m < MR) part_sums[(wave * MR + m) * 4 + g] = v;
+    } else {
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-        const float v = kMmLanes ? lane4_sum(acc[m], li) : row16_sum(acc[m]);
-        if (li == 15) part_sums[(wave * MR + m) * 4 + g] = v;
+        for (int m = 0; m < MR; ++m) {
+            const float v = row16_sum(acc[m]);
+            if (li == 15) part_sums[(wave * MR + m) * 4 + g] = v;
+        }
     }
     __syncthreads();
     if constexpr (PAIR) {
