@@ -78,10 +78,81 @@ BQ_DEV float wave_sum(float v) {
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
+// Wave64 sum left in lane 63 with DPP only (no LDS shuffles): row_shr 1, 2,
+// 4, 8 scans each 16-lane row (its lane 15 ends with the row's total), then
+// row_bcast:15 adds row 0's total into row 1 and row 2's into row 3, and
+// row_bcast:31 adds lane 31 (rows 0 + 1) into rows 2 and 3.  Other lanes hold
+// partial sums.
+template <int CTRL, int ROW_MASK, bool BOUND>
+BQ_DEV float dpp_f(float x) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF, BOUND));
+}
+BQ_DEV float wave_sum_dpp63(float v) {
+    v += dpp_f<0x111, 0xF, true>(v);   // row_shr:1
+    v += dpp_f<0x112, 0xF, true>(v);   // row_shr:2
+    v += dpp_f<0x114, 0xF, true>(v);   // row_shr:4
+    v += dpp_f<0x118, 0xF, true>(v);   // row_shr:8
+    v += dpp_f<0x142, 0xA, false>(v);  // row_bcast:15 into rows 1, 3
+    v += dpp_f<0x143, 0xC, false>(v);  // row_bcast:31 into rows 2, 3
+    return v;
+}
 BQ_DEV int wave_sum_i(int v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
+}
+
+// b where bit `lane` of the wave mask is set, else a: one v_cndmask_b32.
+// (C selects between array elements with a lane-dependent condition let the
+// compiler turn the array into a dynamically indexed one: a compare-and-
+// select chain over every element per select.)
+BQ_DEV float lane_sel(float a, float b, uint64_t mask) {
+    float r;
+    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
+    return r;
+}
+
+constexpr int pow2_ceil(int v) { return v <= 1 ? 1 : 2 * pow2_ceil((v + 1) / 2); }
+
+// Sums of V values per lane over the NL lanes lane0 + S*j (j = 0..NL-1) that
+// share the other lane bits, all V at once, as a reduce-scatter butterfly:
+// each exchange with the lane S*d apart (d = NL/2, NL/4, ... while the lane
+// carries more than one value) keeps the half of its values selected by lane
+// bit S*d and adds the partner's copy of them; the remaining exchanges are
+// plain sums.  Shuffles: log2 NL in all, against V * log2 NL for V separate
+// reductions.  Returns the total of value `idx` (idx >= V: padding); the
+// lanes with ((lane / S) & scatter_writers<V, NL>()) == 0 hold distinct idx.
+template <int V, int NL, int S>
+BQ_DEV float scatter_sum(const float (&acc)[V], int lane, int& idx) {
+    constexpr int P = pow2_ceil(V);
+    static_assert(P <= NL && NL * S <= 64, "butterfly shape");
+    float v[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) v[k] = k < V ? acc[k] : 0.f;
+    idx = 0;
+    int d = NL / 2;
+#pragma unroll
+    for (int h = P / 2; h >= 1; h >>= 1, d >>= 1) {
+        const bool up = (lane & (S * d)) != 0;
+        const uint64_t um = __builtin_amdgcn_ballot_w64(up);
+#pragma unroll
+        for (int k = 0; k < h; ++k) {
+            const float keep = lane_sel(v[k], v[k + h], um);
+            const float send = lane_sel(v[k + h], v[k], um);
+            v[k] = keep + __shfl_xor(send, S * d, 64);
+        }
+        idx += up ? h : 0;
+    }
+#pragma unroll
+    for (; d >= 1; d >>= 1) v[0] += __shfl_xor(v[0], S * d, 64);
+    return v[0];
+}
+
+template <int V, int NL>
+BQ_DEV constexpr int scatter_writers() {
+    constexpr int P = pow2_ceil(V);  // evaluated at compile time
+    return NL / P - 1;
 }
 
 // q8 quantization of one 32-value group held by a lane pair (lanes 2i, 2i+1,

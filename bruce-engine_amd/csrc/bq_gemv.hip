@@ -231,46 +231,6 @@ BQ_DEV void q5k_dot_mm(const FmtQ5K::Task& a, int t, const ActLds& act, int K, f
 // exchanges (plain sums) complete.  P = MR rounded up to a power of two
 // shuffles instead of 4 per row: 8 for 5..8 rows against 32.  Lanes with
 // (i & (16 / P - 1)) == 0 hold distinct rows; m >= MR are padding.
-// b where bit `lane` of the wave mask is set, else a: one v_cndmask_b32.
-// (A C select here lets the compiler turn the butterfly's selects between
-// array elements into a dynamically indexed array: a compare-and-select chain
-// over every element per select.)
-BQ_DEV float lane_sel(float a, float b, uint64_t mask) {
-    float r;
-    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(mask));
-    return r;
-}
-
-template <int MR>
-BQ_DEV float lane4_scatter_sum(const float (&acc)[MR], int li, int& m) {
-    constexpr int P = MR > 4 ? 8 : MR > 2 ? 4 : MR > 1 ? 2 : 1;
-    float v[P];
-#pragma unroll
-    for (int k = 0; k < P; ++k) v[k] = k < MR ? acc[k] : 0.f;
-    m = 0;
-    int d = 8;
-#pragma unroll
-    for (int h = P / 2; h >= 1; h >>= 1, d >>= 1) {
-        const bool up = (li & d) != 0;
-        const uint64_t um = __builtin_amdgcn_ballot_w64(up);
-#pragma unroll
-        for (int k = 0; k < h; ++k) {
-            const float keep = lane_sel(v[k], v[k + h], um);
-            const float send = lane_sel(v[k + h], v[k], um);
-            v[k] = keep + __shfl_xor(send, 4 * d, 64);
-        }
-        m += up ? h : 0;
-    }
-#pragma unroll
-    for (; d >= 1; d >>= 1) v[0] += __shfl_xor(v[0], 4 * d, 64);
-    return v[0];
-}
-
-template <int MR>
-BQ_DEV constexpr int lane4_scatter_mask() {
-    return 16 / (MR > 4 ? 8 : MR > 2 ? 4 : MR > 1 ? 2 : 1) - 1;
-}
-
 struct FmtQ6KRep {
     static constexpr int kLoads = 5;
     struct Task { u32x4 c[4]; f32x4 sc; };
@@ -883,9 +843,10 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
             return;
         }
         if constexpr (kMmLanes) {
+            // the 16 task lanes 4i + g of a weight row, all MR rows at once
             int m;
-            const float v = lane4_scatter_sum<MR>(acc, li, m);
-            if ((li & lane4_scatter_mask<MR>()) == 0 && m < MR && rowok) Y[(size_t)m * Nloc + row] = v;
+            const float v = scatter_sum<MR, 16, 4>(acc, lane, m);
+            if ((li & scatter_writers<MR, 16>()) == 0 && m < MR && rowok) Y[(size_t)m * Nloc + row] = v;
         } else {
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
@@ -897,8 +858,8 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     }
     if constexpr (kMmLanes) {
         int m;
-        const float v = lane4_scatter_sum<MR>(acc, li, m);
-        if ((li & lane4_scatter_mask<MR>()) == 0 && m < MR) part_sums[(wave * MR + m) * 4 + g] = v;
+        const float v = scatter_sum<MR, 16, 4>(acc, lane, m);
+        if ((li & scatter_writers<MR, 16>()) == 0 && m < MR) part_sums[(wave * MR + m) * 4 + g] = v;
     } else {
 #pragma unroll
         for (int m = 0; m < MR; ++m) {

@@ -132,8 +132,8 @@ k_gemv_q8s(const uint8_t* __restrict__ W, int K, int N, const int8_t* __restrict
             const int row = r0 + r;
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const float s = wave_sum(acc[m]);
-                if (lane == 0 && row < N) y[(size_t)m * N + row] = rs ? s * rs[row] : s;
+                const float s = wave_sum_dpp63(acc[m]);
+                if (lane == 63 && row < N) y[(size_t)m * N + row] = rs ? s * rs[row] : s;
             }
         }
     }
