@@ -73,11 +73,6 @@ BQ_DEV u32x4 ld16_a2(const uint8_t* p) {
 #define BQ_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
 
 // Wave64 sum.  Butterfly over the 64 lanes; every lane ends with the total.
-BQ_DEV float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
 // Wave64 sum left in lane 63 with DPP only (no LDS shuffles): row_shr 1, 2,
 // 4, 8 scans each 16-lane row (its lane 15 ends with the row's total), then
 // row_bcast:15 adds row 0's total into row 1 and row 2's into row 3, and
@@ -222,9 +217,9 @@ template <int X>
 BQ_DEV void block_sum(float (&v)[X], float* red) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
 #pragma unroll
-    for (int i = 0; i < X; ++i) v[i] = wave_sum(v[i]);
+    for (int i = 0; i < X; ++i) v[i] = wave_sum_dpp63(v[i]);
     __syncthreads();  // red may still be read by a previous reduction
-    if (lane == 0)
+    if (lane == 63)
 #pragma unroll
         for (int i = 0; i < X; ++i) red[i * 16 + w] = v[i];
     __syncthreads();

@@ -576,8 +576,8 @@ BQ_DEV void fp_load(f32x4 (&in)[4][4], const FusedQ8& fq, int K, int wave, int l
 template <int X>
 BQ_DEV void chunk_sum(float (&v)[X], float* red, int wave, int lane, int nch) {
 #pragma unroll
-    for (int i = 0; i < X; ++i) v[i] = wave_sum(v[i]);
-    if (lane == 0 && wave < nch)
+    for (int i = 0; i < X; ++i) v[i] = wave_sum_dpp63(v[i]);
+    if (lane == 63 && wave < nch)
 #pragma unroll
         for (int i = 0; i < X; ++i) red[i * 16 + wave] = v[i];
     asm volatile("" ::: "memory");

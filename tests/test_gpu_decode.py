@@ -9,11 +9,18 @@ down Q6_K) and a Q8_0 logits head are run eagerly and from the graph:
 * every block matches the oracle's block -- the same sequence evaluated with
   the oracle's GEMVs (double precision over the q8 codes), norms
   (orc_norm_rows) and quantizer -- applied to the same input row, within 2e-4
-  normwise (a block requantizes twice; a value on a q8 rounding boundary can
-  round differently after an fp32 norm and move one code by one);
+  normwise.  Inside a block one fp32 row is requantized (the gate norm of
+  attention, the silu*mul norm of the FFN).  The GPU computes its norm in
+  fp32 (a tree-ordered sum of squares), the oracle in double, so a value
+  whose exact code-space value t/d lies within AMBIG of a rounding boundary
+  may round either way; one such code moving by one shifts the block output
+  by about 2e-4.  The oracle therefore also evaluates the block with those
+  codes rounded the other way (every combination, at most 2^6), and the
+  block must match one of these candidates;
 * the logits match the oracle's Q8_0 head on the final q8 row within 1e-4;
-* with the reference's own sequence (fold = 0) the whole chain from x0 stays
-  within 2e-4 of the oracle's whole chain;
+* the whole chain from x0 stays within 2e-4 of the oracle's whole chain, the
+  oracle taking at each block the candidate rounding that the GPU's block
+  output matches;
 * every graph replay is bit-identical to the eager run.
 The folded form (fold = 1: gate norm inside the O GEMV, silu*mul inside the
 gate+up epilogue, its norm inside the down GEMV) is checked the same way.
@@ -52,34 +59,70 @@ def _model(bq, oracle):
             "rs": g(3903, V, 1.0, 0.1)}
 
 
+AMBIG = 2e-4  # code units: |t/d - (k + 1/2)| below this can round either way
+
+
+def _q8_candidates(oracle, t, limit=6):
+    """The oracle's q8 row of the fp32 row t (1 x n) and the variants in
+    which codes whose exact value t/d lies within AMBIG of a rounding
+    boundary round the other way (xsum adjusted); returns (candidates,
+    number of such codes)."""
+    xq, xd, xs = oracle.q8_rows(t)
+    d = np.repeat(xd[0].astype(np.float64), 32)
+    v = np.divide(t[0].astype(np.float64), d, out=np.zeros_like(d), where=d > 0)
+    amb = np.nonzero((np.abs(v - np.floor(v) - 0.5) < AMBIG) & (np.abs(v) < 127))[0][:limit]
+    cands = []
+    for mask in range(1 << len(amb)):
+        q, s = xq.copy(), xs.copy()
+        for j, i in enumerate(amb):
+            if mask >> j & 1:
+                lo = int(np.floor(v[i]))
+                alt = lo if int(q[0, i]) == lo + 1 else lo + 1
+                s[0, i // 32] += alt - int(q[0, i])
+                q[0, i] = alt
+        cands.append((q, xd, s))
+    return cands, len(amb)
+
+
 def _oracle_block(oracle, m, bi, x):
     """Block bi (even: attention of layer bi // 2, odd: its FFN) of the
     reference's sequence applied to the fp32 row x, with the oracle's GEMVs
-    (double precision over the q8 codes), norms and quantizer; returns the
-    new x (fp32)."""
+    (double precision over the q8 codes), norms and quantizer.  Returns the
+    candidate new x rows (fp32), one per rounding of the block's requantized
+    row (_q8_candidates), and the number of ambiguous codes."""
     f32 = lambda a: np.asarray(a, np.float32)
     L = m["layers"][bi // 2]
     x = x[None]
     if bi == 0:
         x = f32(oracle.norm_rows("add", x, m["input_h"][None]))
     q = oracle.q8_rows(x)
+    outs = []
     if bi % 2 == 0:
         ys = {}
         for name, n, qt, raw in L["qkv"]:
             ys[name] = f32(oracle.gemm_q5k(raw, *q) if qt == "q5k" else oracle.gemm_q6k(raw, q[0], q[1]))
         t = f32(oracle.norm_rows("gate", L["attn_out"][None], ys["gate"], L["sgate"][None]))
-        qa = oracle.q8_rows(t)
-        proj = f32(oracle.gemm_q5k(L["o"], *qa))
-        x = f32(oracle.norm_rows("resid", x, proj, L["alpha_a"][None]))
+        cands, namb = _q8_candidates(oracle, t)
+        for qa in cands:
+            proj = f32(oracle.gemm_q5k(L["o"], *qa))
+            outs.append(f32(oracle.norm_rows("resid", x, proj, L["alpha_a"][None]))[0])
     else:
         yg, yu = f32(oracle.gemm_q5k(L["gate"], *q)), f32(oracle.gemm_q5k(L["up"], *q))
         t = f32(oracle.norm_rows("silu", yg, yu, L["sg"][None], L["su"][None]))
-        qt = oracle.q8_rows(t)
-        proj = f32(oracle.gemm_q6k(L["down"], qt[0], qt[1]))
-        x = f32(oracle.norm_rows("resid", x, proj, L["alpha_f"][None]))
-        if bi == 2 * len(m["layers"]) - 1:
-            x = f32(oracle.norm_rows("norm", x))
-    return x[0]
+        cands, namb = _q8_candidates(oracle, t)
+        for qt in cands:
+            proj = f32(oracle.gemm_q6k(L["down"], qt[0], qt[1]))
+            xo = f32(oracle.norm_rows("resid", x, proj, L["alpha_f"][None]))
+            if bi == 2 * len(m["layers"]) - 1:
+                xo = f32(oracle.norm_rows("norm", xo))
+            outs.append(xo[0])
+    return outs, namb
+
+
+def _closest(oracle, got, cands):
+    errs = [oracle.normwise_err(got, c.astype(np.float64)) for c in cands]
+    k = int(np.argmin(errs))
+    return errs[k], cands[k]
 
 
 def _oracle_logits(oracle, m, x):
@@ -155,32 +198,33 @@ def test_decode_graph_vs_oracle(bq, oracle, fold):
     # block by block: the first nb - 1 blocks on the GPU, then block nb on the
     # GPU and in the oracle from the same fp32 row
     prev = m["x0"].copy()
+    gpu_x = []
     for nb in range(1, 5):
         st.n_blocks = nb
         reset()
         bq.decode_enqueue(st)
         torch.cuda.synchronize()
         got = host(x).copy()
-        err = oracle.normwise_err(got, _oracle_block(oracle, m, nb - 1, prev).astype(np.float64))
-        print(f"  block {nb - 1}: x vs oracle {err:.2e}", flush=True)
+        cands, namb = _oracle_block(oracle, m, nb - 1, prev)
+        err, _ = _closest(oracle, got, cands)
+        print(f"  block {nb - 1}: x vs oracle {err:.2e} ({namb} codes within {AMBIG:g} of a rounding boundary, "
+              f"unrounded-as-GPU error {oracle.normwise_err(got, cands[0].astype(np.float64)):.2e})", flush=True)
         assert err < 2e-4, (nb, err)
+        gpu_x.append(got)
         prev = got
     el = host(logits).copy()
     lerr = oracle.normwise_err(el, _oracle_logits(oracle, m, prev))
     print(f"  logits vs oracle head on the final q8 row: {lerr:.2e}", flush=True)
     assert lerr < 1e-4
-    # the whole chain in the oracle from x0: fold = 0 issues the reference's
-    # own sequence, whose fp32 rounding the oracle reproduces, so its eight
-    # requantizations round alike and the chain stays within 2e-4; fold = 1
-    # reorders fp32 sums, a code on a rounding boundary can move by one and
-    # the difference compounds over the blocks (printed, not asserted)
+    # the whole chain in the oracle from x0, each block's ambiguous roundings
+    # taken as the GPU's block output shows them (without that choice a code
+    # that rounds the other way compounds over the blocks)
     rx = m["x0"].copy()
     for bi in range(4):
-        rx = _oracle_block(oracle, m, bi, rx)
+        _, rx = _closest(oracle, gpu_x[bi], _oracle_block(oracle, m, bi, rx)[0])
     cx, cl = oracle.normwise_err(prev, rx), oracle.normwise_err(el, _oracle_logits(oracle, m, rx))
     print(f"  whole chain vs oracle chain: x {cx:.2e}, logits {cl:.2e}", flush=True)
-    if fold == 0:
-        assert cx < 2e-4 and cl < 2e-4
+    assert cx < 2e-4 and cl < 2e-4
     # graph replays: bit-identical to the eager run
     ex = prev
     g = bq.DecodeGraph(st)
