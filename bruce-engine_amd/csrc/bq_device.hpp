@@ -72,7 +72,6 @@ BQ_DEV u32x4 ld16_a2(const uint8_t* p) {
 // s_waitcnt lgkmcnt(0) only (LDS writes done; vector loads may stay in flight)
 #define BQ_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
 
-// Wave64 sum.  Butterfly over the 64 lanes; every lane ends with the total.
 // Wave64 sum left in lane 63 with DPP only (no LDS shuffles): row_shr 1, 2,
 // 4, 8 scans each 16-lane row (its lane 15 ends with the row's total), then
 // row_bcast:15 adds row 0's total into row 1 and row 2's into row 3, and
@@ -90,11 +89,6 @@ BQ_DEV float wave_sum_dpp63(float v) {
     v += dpp_f<0x118, 0xF, true>(v);   // row_shr:8
     v += dpp_f<0x142, 0xA, false>(v);  // row_bcast:15 into rows 1, 3
     v += dpp_f<0x143, 0xC, false>(v);  // row_bcast:31 into rows 2, 3
-    return v;
-}
-BQ_DEV int wave_sum_i(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
 
