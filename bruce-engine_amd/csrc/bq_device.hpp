@@ -76,7 +76,8 @@ BQ_DEV u32x4 ld16_a2(const uint8_t* p) {
 // 4, 8 scans each 16-lane row (its lane 15 ends with the row's total), then
 // row_bcast:15 adds row 0's total into row 1 and row 2's into row 3, and
 // row_bcast:31 adds lane 31 (rows 0 + 1) into rows 2 and 3.  Other lanes hold
-// partial sums.
+// partial sums.  Every lane of the wave must be active (DPP reads the other
+// lanes' registers).
 template <int CTRL, int ROW_MASK, bool BOUND>
 BQ_DEV float dpp_f(float x) {
     return __builtin_bit_cast(float,
@@ -109,9 +110,11 @@ constexpr int pow2_ceil(int v) { return v <= 1 ? 1 : 2 * pow2_ceil((v + 1) / 2);
 // each exchange with the lane S*d apart (d = NL/2, NL/4, ... while the lane
 // carries more than one value) keeps the half of its values selected by lane
 // bit S*d and adds the partner's copy of them; the remaining exchanges are
-// plain sums.  Shuffles: log2 NL in all, against V * log2 NL for V separate
-// reductions.  Returns the total of value `idx` (idx >= V: padding); the
-// lanes with ((lane / S) & scatter_writers<V, NL>()) == 0 hold distinct idx.
+// plain sums.  Shuffles: P - 1 for the halving exchanges plus one per plain
+// one (P = V rounded up to a power of two), against V * log2 NL for V
+// separate reductions.  Returns the total of value `idx` (idx >= V:
+// padding); the lanes with ((lane / S) & scatter_writers<V, NL>()) == 0 hold
+// distinct idx.  Every lane of the wave must be active (ballot, shuffles).
 template <int V, int NL, int S>
 BQ_DEV float scatter_sum(const float (&acc)[V], int lane, int& idx) {
     constexpr int P = pow2_ceil(V);
