@@ -44,27 +44,6 @@ BQ_DEV int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, fa
 // 16-byte load of read-once weight data
 BQ_DEV u32x4 ld16(const void* p) { return *(const u32x4*)p; }
 
-// 16 bytes starting at a 2-byte aligned address, built from dword-aligned loads
-// (v_alignbyte_b32 funnel shift).  Reads only [p & ~3, p + 18) when p % 4 == 2,
-// [p, p + 16) when p % 4 == 0.
-BQ_DEV u32x4 ld16_a2(const uint8_t* p) {
-    const uintptr_t a = (uintptr_t)p;
-    const uint32_t* w = (const uint32_t*)(a & ~(uintptr_t)3);
-    if ((a & 2) == 0) {
-        u32x4 r;
-        __builtin_memcpy(&r, w, 16);
-        return r;
-    }
-    uint32_t v[5];
-    __builtin_memcpy(v, w, 20);
-    u32x4 r;
-    r.x = __builtin_amdgcn_alignbyte(v[1], v[0], 2);
-    r.y = __builtin_amdgcn_alignbyte(v[2], v[1], 2);
-    r.z = __builtin_amdgcn_alignbyte(v[3], v[2], 2);
-    r.w = __builtin_amdgcn_alignbyte(v[4], v[3], 2);
-    return r;
-}
-
 // s_waitcnt vmcnt(N) leaving lgkmcnt / expcnt unconstrained (gfx9 encoding:
 // vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
 #define BQ_WAIT_VM(n) \
