@@ -21,17 +21,17 @@ namespace {
 struct EventPool {
     std::vector<hipEvent_t> ev;
     explicit EventPool(size_t n) : ev(n, nullptr) {
-        for (auto& e : ev) hipEventCreate(&e);
+        for (auto& e : ev) (void)hipEventCreate(&e);
     }
     ~EventPool() {
         for (auto& e : ev)
-            if (e) hipEventDestroy(e);
+            if (e) (void)hipEventDestroy(e);
     }
 };
 
 float elapsed(hipEvent_t a, hipEvent_t b) {
     float ms = 0.f;
-    hipEventElapsedTime(&ms, a, b);
+    (void)hipEventElapsedTime(&ms, a, b);
     return ms;
 }
 
@@ -67,11 +67,11 @@ int bqb_stream(int steps, int warmup, int nbufs, const void* const* bufs, size_t
     for (int i = 0; i < warmup; ++i)
         hipLaunchKernelGGL(k_stream, grid, dim3(256), 0, (hipStream_t)st, (const uint4*)bufs[i % nbufs], n16, sink);
     EventPool pool((size_t)steps * 2);
-    hipDeviceSynchronize();
+    (void)hipDeviceSynchronize();
     for (int i = 0; i < steps; ++i)
         hipExtLaunchKernelGGL(k_stream, grid, dim3(256), 0, (hipStream_t)st, pool.ev[2 * i], pool.ev[2 * i + 1], 0,
                               (const uint4*)bufs[i % nbufs], n16, sink);
-    hipDeviceSynchronize();
+    (void)hipDeviceSynchronize();
     double t = 0;
     for (int i = 0; i < steps; ++i) t += elapsed(pool.ev[2 * i], pool.ev[2 * i + 1]);
     out[0] = t;
@@ -103,10 +103,10 @@ __global__ void __launch_bounds__(256) k_mfma_peak(int iters, uint32_t* sink) {
 int bqb_mfma_peak(int blocks, int iters, uint32_t* sink, bq_stream_t st, double* out) {
     hipLaunchKernelGGL(k_mfma_peak, dim3(blocks), dim3(256), 0, (hipStream_t)st, iters / 10 + 1, sink);
     EventPool pool(2);
-    hipDeviceSynchronize();
+    (void)hipDeviceSynchronize();
     hipExtLaunchKernelGGL(k_mfma_peak, dim3(blocks), dim3(256), 0, (hipStream_t)st, pool.ev[0], pool.ev[1], 0, iters,
                           sink);
-    hipDeviceSynchronize();
+    (void)hipDeviceSynchronize();
     out[0] = elapsed(pool.ev[0], pool.ev[1]);
     out[1] = (double)blocks * 4 * iters * 4 * 65536.0;
     return hipGetLastError() == hipSuccess ? 0 : -1;
@@ -168,40 +168,40 @@ int bqb_decode_ffn(int mode, int steps, int warmup, int nsets, const bq_weight* 
             *ex = nullptr;
             if (n == 0) return 0;
             hipGraph_t g;
-            hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+            (void)hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
             int r = 0;
             for (int i = 0; i < n && !r; ++i) r = step(i, nullptr, nullptr, nullptr, nullptr, (bq_stream_t)cs);
             if (hipStreamEndCapture(cs, &g) != hipSuccess || r) return r ? r : -1;
             const hipError_t e = hipGraphInstantiate(ex, g, nullptr, nullptr, 0);
-            hipGraphDestroy(g);
+            (void)hipGraphDestroy(g);
             return e == hipSuccess ? 0 : -1;
         };
         hipGraphExec_t full, tail;
         if (int r = capture(nsets, &full)) return r;
         if (int r = capture(steps % nsets, &tail)) return r;
-        hipGraphLaunch(full, (hipStream_t)st);  // warm the graph
+        (void)hipGraphLaunch(full, (hipStream_t)st);  // warm the graph
         EventPool pool(2);
-        hipDeviceSynchronize();
-        hipEventRecord(pool.ev[0], (hipStream_t)st);
-        for (int i = 0; i < steps / nsets; ++i) hipGraphLaunch(full, (hipStream_t)st);
-        if (tail) hipGraphLaunch(tail, (hipStream_t)st);
-        hipEventRecord(pool.ev[1], (hipStream_t)st);
-        hipDeviceSynchronize();
+        (void)hipDeviceSynchronize();
+        (void)hipEventRecord(pool.ev[0], (hipStream_t)st);
+        for (int i = 0; i < steps / nsets; ++i) (void)hipGraphLaunch(full, (hipStream_t)st);
+        if (tail) (void)hipGraphLaunch(tail, (hipStream_t)st);
+        (void)hipEventRecord(pool.ev[1], (hipStream_t)st);
+        (void)hipDeviceSynchronize();
         out[0] = elapsed(pool.ev[0], pool.ev[1]);
-        hipGraphExecDestroy(full);
-        if (tail) hipGraphExecDestroy(tail);
-        hipStreamDestroy(cs);
+        (void)hipGraphExecDestroy(full);
+        if (tail) (void)hipGraphExecDestroy(tail);
+        (void)hipStreamDestroy(cs);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     EventPool pool((size_t)steps * 4 + 2);
-    hipDeviceSynchronize();
-    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[0], (hipStream_t)st);
     for (int i = 0; i < steps; ++i) {
         hipEvent_t* e = &pool.ev[2 + 4 * (size_t)i];
         if (int r = step(i, e[0], e[1], e[2], e[3], st)) return r;
     }
-    hipEventRecord(pool.ev[1], (hipStream_t)st);
-    hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[1], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
     out[0] = elapsed(pool.ev[0], pool.ev[1]);
     double g = 0, d = 0;
     for (int i = 0; i < steps; ++i) {
@@ -224,16 +224,16 @@ int bqb_gemm(int steps, int warmup, const bq_weight* w, int M, const int8_t* xq,
     for (int i = 0; i < warmup; ++i)
         if (int r = bq_try_mmq(ys, ws, 1, M, xq, xd, xs, xdh, nullptr, 0, st)) return r;
     EventPool pool((size_t)steps * 2 + 2);
-    hipDeviceSynchronize();
-    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[0], (hipStream_t)st);
     for (int i = 0; i < steps; ++i) {
         // the fill_xdh pre-pass of the W144 path is not timed: the event pair
         // brackets the GEMM kernel itself
         bq_time_next_launch(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
         if (int r = bq_try_mmq(ys, ws, 1, M, xq, xd, xs, xdh, nullptr, 0, st)) return r;
     }
-    hipEventRecord(pool.ev[1], (hipStream_t)st);
-    hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[1], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
     out[0] = elapsed(pool.ev[0], pool.ev[1]);
     double k = 0;
     for (int i = 0; i < steps; ++i) k += elapsed(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
@@ -255,14 +255,14 @@ int bqb_gemv_rows(int steps, int warmup, int nsets, const bq_weight* w, int rows
     for (int i = 0; i < warmup; ++i)
         if (int r = launch(i)) return r;
     EventPool pool((size_t)steps * 2 + 2);
-    hipDeviceSynchronize();
-    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[0], (hipStream_t)st);
     for (int i = 0; i < steps; ++i) {
         bq_time_next_launch(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
         if (int r = launch(i)) return r;
     }
-    hipEventRecord(pool.ev[1], (hipStream_t)st);
-    hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[1], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
     out[0] = elapsed(pool.ev[0], pool.ev[1]);
     double k = 0;
     for (int i = 0; i < steps; ++i) k += elapsed(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
@@ -283,14 +283,14 @@ int bqb_gemv_fused(int steps, int warmup, int nsets, int nparts, const bq_weight
     for (int i = 0; i < warmup; ++i)
         if (int r = launch(i)) return r;
     EventPool pool((size_t)steps * 2 + 2);
-    hipDeviceSynchronize();
-    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[0], (hipStream_t)st);
     for (int i = 0; i < steps; ++i) {
         bq_time_next_launch(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
         if (int r = launch(i)) return r;
     }
-    hipEventRecord(pool.ev[1], (hipStream_t)st);
-    hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[1], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
     out[0] = elapsed(pool.ev[0], pool.ev[1]);
     double k = 0;
     for (int i = 0; i < steps; ++i) k += elapsed(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
@@ -305,14 +305,14 @@ int bqb_q8s(int steps, int warmup, int nsets, const void* const* ws, int K, int 
     for (int i = 0; i < warmup; ++i)
         if (int r = bq_gemv_q8s(y, ws[i % nsets], xq, xd, K, N, rows, rs, st)) return r;
     EventPool pool((size_t)steps * 2 + 2);
-    hipDeviceSynchronize();
-    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[0], (hipStream_t)st);
     for (int i = 0; i < steps; ++i) {
         bq_time_next_launch(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
         if (int r = bq_gemv_q8s(y, ws[i % nsets], xq, xd, K, N, rows, rs, st)) return r;
     }
-    hipEventRecord(pool.ev[1], (hipStream_t)st);
-    hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[1], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
     out[0] = elapsed(pool.ev[0], pool.ev[1]);
     double k = 0;
     for (int i = 0; i < steps; ++i) k += elapsed(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
@@ -339,14 +339,14 @@ int bqb_norm(int op, int steps, int warmup, float* out, float* a, const float* b
     for (int i = 0; i < warmup; ++i)
         if (int r = launch()) return r;
     EventPool pool((size_t)steps * 2 + 2);
-    hipDeviceSynchronize();
-    hipEventRecord(pool.ev[0], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[0], (hipStream_t)st);
     for (int i = 0; i < steps; ++i) {
         bq_time_next_launch(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
         if (int r = launch()) return r;
     }
-    hipEventRecord(pool.ev[1], (hipStream_t)st);
-    hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[1], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
     out_t[0] = elapsed(pool.ev[0], pool.ev[1]);
     double k = 0;
     for (int i = 0; i < steps; ++i) k += elapsed(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
@@ -389,21 +389,21 @@ int bqb_stack(int steps, int warmup, int nlayers, const bq_weight* w, const bq_w
         if (int r = token(st)) return r;
     hipGraph_t g;
     hipGraphExec_t ex;
-    hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+    (void)hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
     const int r = token((bq_stream_t)cs);
     if (hipStreamEndCapture(cs, &g) != hipSuccess || r) return r ? r : -1;
     if (hipGraphInstantiate(&ex, g, nullptr, nullptr, 0) != hipSuccess) return -1;
-    hipGraphDestroy(g);
-    hipGraphLaunch(ex, (hipStream_t)st);
+    (void)hipGraphDestroy(g);
+    (void)hipGraphLaunch(ex, (hipStream_t)st);
     EventPool pool(2);
-    hipDeviceSynchronize();
-    hipEventRecord(pool.ev[0], (hipStream_t)st);
-    for (int i = 0; i < steps; ++i) hipGraphLaunch(ex, (hipStream_t)st);
-    hipEventRecord(pool.ev[1], (hipStream_t)st);
-    hipDeviceSynchronize();
+    (void)hipDeviceSynchronize();
+    (void)hipEventRecord(pool.ev[0], (hipStream_t)st);
+    for (int i = 0; i < steps; ++i) (void)hipGraphLaunch(ex, (hipStream_t)st);
+    (void)hipEventRecord(pool.ev[1], (hipStream_t)st);
+    (void)hipDeviceSynchronize();
     out[0] = elapsed(pool.ev[0], pool.ev[1]);
-    hipGraphExecDestroy(ex);
-    hipStreamDestroy(cs);
+    (void)hipGraphExecDestroy(ex);
+    (void)hipStreamDestroy(cs);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

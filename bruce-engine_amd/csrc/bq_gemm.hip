@@ -35,7 +35,6 @@
 
 namespace bq {
 
-constexpr int kTM = 128;   // tokens per tile
 constexpr int kTN = 128;   // weight rows per tile
 constexpr int kRS = 144;   // LDS row stride (bytes)
 constexpr int kXcds = 8;
@@ -372,7 +371,11 @@ struct SmemStage {
 // treat LDS reads of the other stage buffer as dependent on it (it would wait
 // for vmcnt(0) before them); the kernel orders the copies itself (vmcnt(0) +
 // barrier before a buffer is read).  An untracked VMEM op can only make the
-// compiler's own vmcnt waits stricter, never looser.
+// compiler's own vmcnt waits stricter, never looser.  m0 is written here; the compiler
+// warns that it reserves m0 and will not preserve it around the asm, which
+// is safe because on gfx9 no other instruction of these kernels uses m0 (LDS
+// instructions do not; the kernels have no other direct-to-LDS loads or
+// indirect register indexing).
 BQ_DEV void dma16(const void* gbase, uint32_t voff, const void* lds) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
