@@ -1,4 +1,5 @@
-"""Every output of the prefill GEMMs at BASELINE config 4's full size, checked.
+"""Every output of the prefill GEMMs at BASELINE config 4's full size (M = 2048
+and 8192), checked.
 
 The oracle's scalar GEMM cannot finish M = 2048 x 9216 x 3072 in test time,
 so the sampled oracle checks (test_gpu_pinned.py) are joined here by a
@@ -29,7 +30,8 @@ from helpers import acts, check, dev, host, weights
 
 pytestmark = pytest.mark.gpu
 
-M, K, N = 2048, 3072, 9216
+K, N = 3072, 9216   # BASELINE config 4 (M = 2048 and the bench's largest, 8192)
+M = 2048
 
 
 def _np_dmin_m(raw, K):
@@ -48,9 +50,9 @@ def _np_dmin_m(raw, K):
 
 
 def _gemv_chunks(fn, y, w, xq, xd, xs=None):
-    """y[r0:r0+8] = GEMV of activation rows r0..r0+7, over all M rows."""
+    """y[r0:r0+8] = GEMV of activation rows r0..r0+7, over all rows of y."""
     import torch
-    for r0 in range(0, M, 8):
+    for r0 in range(0, y.shape[0], 8):
         args = (xq[r0:r0 + 8], xd[r0:r0 + 8]) + ((xs[r0:r0 + 8],) if xs is not None else ())
         assert fn([y[r0:r0 + 8]], [w], 8, *args) == 0
     torch.cuda.synchronize()
@@ -71,12 +73,13 @@ def test_dmin_m_decoder_matches_oracle(oracle):
                 assert dm[r, 8 * sb + j] == dmin * mj
 
 
+@pytest.mark.parametrize("M", [2048, 8192])
 @pytest.mark.parametrize("prepacked", [False, True])
-def test_config4_full_output_vs_gemv(bq, oracle, prepacked):
+def test_config4_full_output_vs_gemv(bq, oracle, prepacked, M):
     import torch
     print(f"config4 full output M={M} prepacked={prepacked}", flush=True)
     raw = weights(2401, N, K, "q5k")
-    x, (xq, xd, xs) = acts(2402, M, K)
+    x, (xq, xd, xs) = acts(2402 + M, M, K)
     gr = dev(raw)
     gq, gd, gs = dev(xq), dev(xd), dev(xs)
     w_raw = bq.make_weight(gr, bq.TYPE_Q5_K, K, N)
