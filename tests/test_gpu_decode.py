@@ -15,8 +15,10 @@ down Q6_K) and a Q8_0 logits head are run eagerly and from the graph:
   whose exact code-space value t/d lies within AMBIG of a rounding boundary
   may round either way; one such code moving by one shifts the block output
   by about 2e-4.  The oracle therefore also evaluates the block with those
-  codes rounded the other way (every combination, at most 2^6), and the
-  block must match one of these candidates;
+  codes rounded the other way (every combination of up to MAX_AMBIG codes;
+  the GEMV after the requantization is linear in the codes, so each flip is
+  one extra oracle GEMV of a one-hot row), and the block must match one of
+  these candidates;
 * the logits match the oracle's Q8_0 head on the final q8 row within 1e-4;
 * the whole chain from x0 stays within 2e-4 of the oracle's whole chain, the
   oracle taking at each block the candidate rounding that the GPU's block
@@ -59,29 +61,40 @@ def _model(bq, oracle):
             "rs": g(3903, V, 1.0, 0.1)}
 
 
-AMBIG = 2e-4  # code units: |t/d - (k + 1/2)| below this can round either way
+AMBIG = 2e-4    # code units: |t/d - (k + 1/2)| below this can round either way
+MAX_AMBIG = 10  # such codes per requantized row the check enumerates (2^10 roundings)
 
 
-def _q8_candidates(oracle, t, limit=6):
-    """The oracle's q8 row of the fp32 row t (1 x n) and the variants in
-    which codes whose exact value t/d lies within AMBIG of a rounding
-    boundary round the other way (xsum adjusted); returns (candidates,
-    number of such codes)."""
+def _q8_flips(oracle, t):
+    """The oracle's q8 row of the fp32 row t (1 x n), and the codes whose
+    exact value t/d lies within AMBIG of a rounding boundary, each as (index,
+    change to the code that rounds the other way)."""
     xq, xd, xs = oracle.q8_rows(t)
     d = np.repeat(xd[0].astype(np.float64), 32)
     v = np.divide(t[0].astype(np.float64), d, out=np.zeros_like(d), where=d > 0)
-    amb = np.nonzero((np.abs(v - np.floor(v) - 0.5) < AMBIG) & (np.abs(v) < 127))[0][:limit]
-    cands = []
-    for mask in range(1 << len(amb)):
-        q, s = xq.copy(), xs.copy()
-        for j, i in enumerate(amb):
-            if mask >> j & 1:
-                lo = int(np.floor(v[i]))
-                alt = lo if int(q[0, i]) == lo + 1 else lo + 1
-                s[0, i // 32] += alt - int(q[0, i])
-                q[0, i] = alt
-        cands.append((q, xd, s))
-    return cands, len(amb)
+    amb = np.nonzero((np.abs(v - np.floor(v) - 0.5) < AMBIG) & (np.abs(v) < 127))[0]
+    assert len(amb) <= MAX_AMBIG, f"{len(amb)} codes on a rounding boundary"
+    flips = []
+    for i in amb:
+        lo = int(np.floor(v[i]))
+        alt = lo if int(xq[0, i]) == lo + 1 else lo + 1
+        flips.append((int(i), alt - int(xq[0, i])))
+    return (xq, xd, xs), flips
+
+
+def _gemv_candidates(gemv, q, flips):
+    """The GEMV (double) of the q8 row q and of every rounding of its
+    ambiguous codes.  The GEMV is linear in the codes and xsum, so a flipped
+    code adds the GEMV of a one-hot code row (xsum changed alike)."""
+    xq, xd, xs = q
+    base = np.asarray(gemv(xq, xd, xs), np.float64)
+    deltas = []
+    for i, dv in flips:
+        dq, ds = np.zeros_like(xq), np.zeros_like(xs)
+        dq[0, i], ds[0, i // 32] = dv, dv
+        deltas.append(np.asarray(gemv(dq, xd, ds), np.float64))
+    for mask in range(1 << len(flips)):
+        yield base + sum((deltas[j] for j in range(len(flips)) if mask >> j & 1), np.zeros_like(base))
 
 
 def _oracle_block(oracle, m, bi, x):
@@ -89,7 +102,7 @@ def _oracle_block(oracle, m, bi, x):
     reference's sequence applied to the fp32 row x, with the oracle's GEMVs
     (double precision over the q8 codes), norms and quantizer.  Returns the
     candidate new x rows (fp32), one per rounding of the block's requantized
-    row (_q8_candidates), and the number of ambiguous codes."""
+    row's ambiguous codes (_q8_flips), and the number of those codes."""
     f32 = lambda a: np.asarray(a, np.float32)
     L = m["layers"][bi // 2]
     x = x[None]
@@ -102,21 +115,19 @@ def _oracle_block(oracle, m, bi, x):
         for name, n, qt, raw in L["qkv"]:
             ys[name] = f32(oracle.gemm_q5k(raw, *q) if qt == "q5k" else oracle.gemm_q6k(raw, q[0], q[1]))
         t = f32(oracle.norm_rows("gate", L["attn_out"][None], ys["gate"], L["sgate"][None]))
-        cands, namb = _q8_candidates(oracle, t)
-        for qa in cands:
-            proj = f32(oracle.gemm_q5k(L["o"], *qa))
-            outs.append(f32(oracle.norm_rows("resid", x, proj, L["alpha_a"][None]))[0])
+        qa, flips = _q8_flips(oracle, t)
+        for proj in _gemv_candidates(lambda a, b, c: oracle.gemm_q5k(L["o"], a, b, c), qa, flips):
+            outs.append(f32(oracle.norm_rows("resid", x, f32(proj), L["alpha_a"][None]))[0])
     else:
         yg, yu = f32(oracle.gemm_q5k(L["gate"], *q)), f32(oracle.gemm_q5k(L["up"], *q))
         t = f32(oracle.norm_rows("silu", yg, yu, L["sg"][None], L["su"][None]))
-        cands, namb = _q8_candidates(oracle, t)
-        for qt in cands:
-            proj = f32(oracle.gemm_q6k(L["down"], qt[0], qt[1]))
-            xo = f32(oracle.norm_rows("resid", x, proj, L["alpha_f"][None]))
+        qt, flips = _q8_flips(oracle, t)
+        for proj in _gemv_candidates(lambda a, b, c: oracle.gemm_q6k(L["down"], a, b), qt, flips):
+            xo = f32(oracle.norm_rows("resid", x, f32(proj), L["alpha_f"][None]))
             if bi == 2 * len(m["layers"]) - 1:
                 xo = f32(oracle.norm_rows("norm", xo))
             outs.append(xo[0])
-    return outs, namb
+    return outs, len(flips)
 
 
 def _closest(oracle, got, cands):
