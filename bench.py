@@ -394,11 +394,13 @@ def mfma_ceiling(B, torch, sp):
 
 
 def stream_ceiling(B, torch, sp, sizes=(6504192, 19464192, 23224320, 39018240, 330301440)):
-    """HBM streaming-read ceiling per launch size (k_stream in bq_bench.hip:
-    16-byte loads of every byte once, buffers rotated past the last-level
-    cache), the bound a GEMV of that many bytes can reach in one launch.
-    Sizes: config 1, config 3, the down projection, the fused gate+up and
-    the lm_head launches."""
+    """HBM streaming-read ceiling per launch size, the bound a GEMV of that
+    many bytes can reach in one launch: the faster of two read-only kernels in
+    bq_bench.hip (k_stream: one 16 KB chunk per workgroup; k_stream_gs: a
+    grid of 4 workgroups per CU looping over 16 KB chunks), 16-byte loads of
+    every byte once, buffers rotated past the last-level cache.  Sizes:
+    config 1, config 3, the down projection, the fused gate+up and the
+    lm_head launches."""
     res = {}
     out = (ctypes.c_double * 4)()
     sink = torch.zeros(4, dtype=torch.int32, device="cuda")
@@ -407,14 +409,45 @@ def stream_ceiling(B, torch, sp, sizes=(6504192, 19464192, 23224320, 39018240, 3
         bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(nb)]
         arr = (ctypes.c_void_p * nb)(*[b.data_ptr() for b in bufs])
         steps = 200 if nbytes < 100e6 else 40
-        # warm-up: one pass over every buffer (a fresh buffer's first touch is slower)
-        r = B.bqb_stream(steps, nb + 10, nb, arr, nbytes, ctypes.c_void_p(sink.data_ptr()), sp, out)
-        if r != 0:
-            raise RuntimeError("bqb_stream failed")
-        us = out[0] / steps * 1e3
+        per = {}
+        for pattern, name in ((0, "k_stream"), (1, "k_stream_gs")):
+            # warm-up: one pass over every buffer (a fresh buffer's first touch is slower)
+            r = B.bqb_stream(pattern, steps, nb + 10, nb, arr, nbytes, ctypes.c_void_p(sink.data_ptr()), sp, out)
+            if r != 0:
+                raise RuntimeError("bqb_stream failed")
+            per[name] = out[0] / steps * 1e3
+        best = min(per, key=per.get)
+        us = per[best]
         res[f"{nbytes / 1e6:.1f}MB"] = {"bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
-                                        "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+                                        "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "kernel": best,
+                                        "us_per_kernel": {k: round(v, 3) for k, v in per.items()}}
         del bufs
+    return res
+
+
+def issue_probes(B, torch, sp):
+    """Issue rates of the instructions the GEMV / GEMM kernels are built from
+    (k_inst_rate in bq_bench.hip: 8 waves per CU, 4 independent chains per
+    wave, no memory traffic), as wave instructions per second per SIMD and
+    relative to v_mfma_i32_32x32x32_i8, and the dispatch-event duration of an
+    empty kernel (k_empty, 1024 x 256 threads), the fixed cost of a launch."""
+    out = (ctypes.c_double * 4)()
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    blocks = 2 * torch.cuda.get_device_properties(0).multi_processor_count
+    names = ["v_mfma_i32_32x32x32_i8", "v_mfma_i32_32x32x16_i8", "v_mfma_f32_32x32x16_f16",
+             "v_mfma_f32_32x32x1_2b_f32", "v_mfma_i32_4x4x4_16b_i8", "v_fma_f32", "v_cvt_f32_i32 + v_add_f32"]
+    rates = {}
+    for w, name in enumerate(names):
+        if B.bqb_inst_rate(w, blocks, 20000, ctypes.c_void_p(sink.data_ptr()), sp, out) != 0:
+            raise RuntimeError("bqb_inst_rate failed")
+        rates[name] = out[1] / (out[0] * 1e-3)
+    base = rates[names[0]]
+    res = {"instructions_per_us_per_simd": {k: round(v / 1e6, 2) for k, v in rates.items()},
+           "time_relative_to_i8_32x32x32": {k: round(base / v, 3) for k, v in rates.items()}}
+    if B.bqb_empty(200, 1024, ctypes.c_void_p(sink.data_ptr()), sp, out) != 0:
+        raise RuntimeError("bqb_empty failed")
+    res["empty_kernel_us"] = {"back_to_back": round(out[0] / 200 * 1e3, 3),
+                              "after_sync": round(out[1] / 200 * 1e3, 3)}
     return res
 
 
@@ -507,6 +540,9 @@ def main():
                     help="only the dense int8 MFMA throughput probe; prints its JSON object")
     ap.add_argument("--stream-only", action="store_true",
                     help="only the HBM streaming-read ceilings per launch size; prints their JSON object")
+    ap.add_argument("--probe-only", action="store_true",
+                    help="only the instruction issue-rate probes and the empty-kernel launch cost; "
+                         "prints their JSON object")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the prefill GEMMs of config 4 and the Q6_K GEMM (for counter profiles); "
                          "prints their JSON object")
@@ -531,7 +567,9 @@ def main():
     B.bqb_decode_ffn.argtypes = [I, I, I, I, WP, WP, WP, P, P, P, P, P, P, P, P, P, P, P, P, P]
     B.bqb_gemm.argtypes = [I, I, WP, I, P, P, P, P, P, P, P]
     B.bqb_gemv_rows.argtypes = [I, I, I, WP, I, P, P, P, P, P, P]
-    B.bqb_stream.argtypes = [I, I, I, P, ctypes.c_size_t, P, P, P]
+    B.bqb_stream.argtypes = [I, I, I, I, P, ctypes.c_size_t, P, P, P]
+    B.bqb_inst_rate.argtypes = [I, I, I, P, P, P]
+    B.bqb_empty.argtypes = [I, I, P, P, P]
     B.bqb_mfma_peak.argtypes = [I, I, P, P, P]
     B.bqb_stack.argtypes = [I, I, I, WP, WP, P, P, P, P, P, P, P, P, P, P]
     B.bqb_q8s.argtypes = [I, I, I, P, I, I, I, P, P, P, P, P, P]
@@ -583,6 +621,9 @@ def main():
     if args.stream_only:
         print(json.dumps({"hbm_read_ceiling": stream_ceiling(B, torch, sp)}), flush=True)
         return
+    if args.probe_only:
+        print(json.dumps({"issue_probes": issue_probes(B, torch, sp)}), flush=True)
+        return
     if args.gemm_only:
         print(json.dumps({"gemm": gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out)}), flush=True)
         return
@@ -615,10 +656,11 @@ def main():
     achieved = gbs(gu_bytes, gu_ms)
 
     gemm_obj, rows_res, c1_obj, stack_obj, q8s_obj, norm_obj, load_obj = None, None, None, None, None, None, None
-    ceil_obj = None
+    ceil_obj, probe_obj = None, None
     if not args.decode_only:
         gemm_obj = gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out)
         ceil_obj = stream_ceiling(B, torch, sp)
+        probe_obj = issue_probes(B, torch, sp)
 
         # ---------------------------------------------------------------- config 3 / config 1 GEMV
         rows_res = {}
@@ -697,6 +739,7 @@ def main():
                       "GBps": round(gbs(dn_bytes, dn_ms), 1)},
         "decode_ffn_unfused": unfused,
         "hbm_read_ceiling": ceil_obj,
+        "issue_probes": probe_obj,
         "gemv_config1_3072x3072": c1_obj,
         "gemv_config3_9216x3072": rows_res,
         "config5_whole_stack": stack_obj,

@@ -11,6 +11,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <utility>
 #include <vector>
 
@@ -52,24 +53,186 @@ __global__ void __launch_bounds__(256) k_stream(const uint4* __restrict__ src, s
     if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
+// The same bytes read by a persistent grid (gridDim = 4 workgroups per CU):
+// workgroup b reads 16 KB chunks b, b + gridDim, ... with 4 loads per thread
+// in flight per iteration.  Faster than k_stream at the GEMV launch sizes
+// (fewer workgroups to dispatch, every chunk of one round adjacent).
+__global__ void __launch_bounds__(256) k_stream_gs(const uint4* __restrict__ src, size_t n16, uint32_t* sink) {
+    uint32_t acc = 0;
+    const size_t stride = (size_t)gridDim.x * 1024;
+    for (size_t base = (size_t)blockIdx.x * 1024 + threadIdx.x; base < n16; base += stride) {
+        uint4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const size_t j = base + 256 * i;
+            v[i] = j < n16 ? src[j] : uint4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    }
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+// A kernel that does nothing: its dispatch-event duration is the fixed cost
+// every launch pays (dispatch, wave launch, end-of-kernel completion).
+__global__ void __launch_bounds__(256) k_empty(uint32_t* sink) {
+    if (threadIdx.x == 1023) sink[0] = 1;  // never true: keeps the kernel
+}
+
+// Issue-rate probes: every wave runs `iters` rounds of 4 independent chains of
+// one instruction (no memory traffic; one operand changes per round), 8 waves
+// per CU.  W selects the instruction.
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+typedef int i32x16v __attribute__((ext_vector_type(16)));
+typedef float f32x16v __attribute__((ext_vector_type(16)));
+typedef float f32x32v __attribute__((ext_vector_type(32)));
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+template <int W>
+__global__ void __launch_bounds__(256) k_inst_rate(int iters, uint32_t* sink) {
+    uint32_t t = 0;
+    if constexpr (W == 0 || W == 1) {  // int8 32x32x32 / 32x32x16
+        i32x4v a = {(int)threadIdx.x, 3, 5, 7}, b = {1, 2, 3, (int)threadIdx.x};
+        long a2 = threadIdx.x, b2 = 3;
+        i32x16v c[4] = {};
+        for (int it = 0; it < iters; ++it) {
+            a.x += 1;
+            a2 += 1;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if constexpr (W == 0) c[k] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c[k], 0, 0, 0);
+                else c[k] = __builtin_amdgcn_mfma_i32_32x32x16_i8(a2, b2, c[k], 0, 0, 0);
+            }
+        }
+        for (int k = 0; k < 4; ++k)
+            for (int i = 0; i < 16; ++i) t ^= (uint32_t)c[k][i];
+    } else if constexpr (W == 2) {  // fp16 32x32x16
+        f16x8v a = {(_Float16)threadIdx.x, 1, 2, 3, 4, 5, 6, 7}, b = {1, 2, 3, 4, 5, 6, 7, 8};
+        f32x16v c0 = {0.f}, c1 = {0.f}, c2 = {0.f}, c3 = {0.f};
+        for (int it = 0; it < iters; ++it) {
+            a[0] += (_Float16)1;
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c3, 0, 0, 0);
+        }
+        float f = 0.f;
+        for (int i = 0; i < 16; ++i) f += c0[i] + c1[i] + c2[i] + c3[i];
+        t = f == 1.2345f ? 0x7fffffffu : 0u;
+    } else if constexpr (W == 3) {  // fp32 32x32x1, two blocks (the GEMMs' scale outer product)
+        float a = threadIdx.x, b = 3.f;
+        f32x32v c0 = {0.f}, c1 = {0.f}, c2 = {0.f}, c3 = {0.f};
+        for (int it = 0; it < iters; ++it) {
+            a += 1.f;
+            c0 = __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c3, 0, 0, 0);
+        }
+        float f = 0.f;
+        for (int i = 0; i < 32; ++i) f += c0[i] + c1[i] + c2[i] + c3[i];
+        t = f == 1.2345f ? 0x7fffffffu : 0u;
+    } else if constexpr (W == 4) {  // int8 4x4x4, 16 blocks (the multi-row GEMV dots)
+        int a = threadIdx.x, b = 3;
+        i32x4v c[4] = {};
+        for (int it = 0; it < iters; ++it) {
+            a += 1;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) c[k] = __builtin_amdgcn_mfma_i32_4x4x4i8(a, b, c[k], 0, 0, 0);
+        }
+        for (int k = 0; k < 4; ++k)
+            for (int i = 0; i < 4; ++i) t ^= (uint32_t)c[k][i];
+    } else if constexpr (W == 5) {  // fp32 FMA (VALU)
+        float a = threadIdx.x, c[4] = {0.f, 1.f, 2.f, 3.f};
+        for (int it = 0; it < iters; ++it) {
+            a += 1.f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) c[k] = __builtin_fmaf(a, 1.0001f, c[k]);
+        }
+        for (int k = 0; k < 4; ++k) t ^= __builtin_bit_cast(uint32_t, c[k]);
+    } else {  // int32 -> fp32 convert (VALU; paired with an add per chain)
+        int a = threadIdx.x;
+        float c[4] = {0.f, 1.f, 2.f, 3.f};
+        for (int it = 0; it < iters; ++it) {
+            a += 1;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) c[k] += (float)(a ^ k);
+        }
+        for (int k = 0; k < 4; ++k) t ^= __builtin_bit_cast(uint32_t, c[k]);
+    }
+    if (t == 0x7fffffffu) sink[threadIdx.x & 3] = t;
+}
+
 }  // namespace
 
 extern "C" {
 
+// Issue rate of one instruction (k_inst_rate<which>): out[0] = the launch's
+// duration (ms), out[1] = instructions issued per SIMD.
+int bqb_inst_rate(int which, int blocks, int iters, uint32_t* sink, bq_stream_t st, double* out) {
+    void (*k)(int, uint32_t*) = nullptr;
+    switch (which) {
+        case 0: k = k_inst_rate<0>; break;
+        case 1: k = k_inst_rate<1>; break;
+        case 2: k = k_inst_rate<2>; break;
+        case 3: k = k_inst_rate<3>; break;
+        case 4: k = k_inst_rate<4>; break;
+        case 5: k = k_inst_rate<5>; break;
+        case 6: k = k_inst_rate<6>; break;
+        default: return -1;
+    }
+    int cus = 0;
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+    hipLaunchKernelGGL(k, dim3(blocks), dim3(256), 0, (hipStream_t)st, iters / 10 + 1, sink);
+    EventPool pool(2);
+    (void)hipDeviceSynchronize();
+    hipExtLaunchKernelGGL(k, dim3(blocks), dim3(256), 0, (hipStream_t)st, pool.ev[0], pool.ev[1], 0, iters, sink);
+    (void)hipDeviceSynchronize();
+    out[0] = elapsed(pool.ev[0], pool.ev[1]);
+    // waves per SIMD x rounds x chains (the convert probe counts convert + add)
+    out[1] = (double)blocks * 4 / (4.0 * (cus > 0 ? cus : 256)) * iters * 4 * (which == 6 ? 2 : 1);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// Dispatch-event duration of an empty kernel of `blocks` x 256 threads:
+// out[0] = summed over `steps` back-to-back launches, out[1] = summed over
+// `steps` launches each after a device synchronisation (ms).
+int bqb_empty(int steps, int blocks, uint32_t* sink, bq_stream_t st, double* out) {
+    EventPool pool((size_t)steps * 2);
+    hipLaunchKernelGGL(k_empty, dim3(blocks), dim3(256), 0, (hipStream_t)st, sink);
+    (void)hipDeviceSynchronize();
+    for (int i = 0; i < steps; ++i)
+        hipExtLaunchKernelGGL(k_empty, dim3(blocks), dim3(256), 0, (hipStream_t)st, pool.ev[2 * i],
+                              pool.ev[2 * i + 1], 0, sink);
+    (void)hipDeviceSynchronize();
+    out[0] = 0;
+    for (int i = 0; i < steps; ++i) out[0] += elapsed(pool.ev[2 * i], pool.ev[2 * i + 1]);
+    out[1] = 0;
+    for (int i = 0; i < steps; ++i) {
+        hipExtLaunchKernelGGL(k_empty, dim3(blocks), dim3(256), 0, (hipStream_t)st, pool.ev[0], pool.ev[1], 0, sink);
+        (void)hipDeviceSynchronize();
+        out[1] += elapsed(pool.ev[0], pool.ev[1]);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // The HBM streaming-read ceiling for one launch of `bytes`: `steps` timed
-// launches of k_stream over nbufs rotating buffers (so the 256 MB last-level
-// cache cannot serve them), each bracketed by dispatch events.  out[0] =
-// summed kernel durations (ms).
-int bqb_stream(int steps, int warmup, int nbufs, const void* const* bufs, size_t bytes, uint32_t* sink,
+// launches of k_stream (pattern 0) or k_stream_gs (pattern 1) over nbufs
+// rotating buffers (so the 256 MB last-level cache cannot serve them), each
+// bracketed by dispatch events.  out[0] = summed kernel durations (ms).
+int bqb_stream(int pattern, int steps, int warmup, int nbufs, const void* const* bufs, size_t bytes, uint32_t* sink,
                bq_stream_t st, double* out) {
     const size_t n16 = bytes / 16;
-    const dim3 grid((unsigned)((n16 + 1023) / 1024));
+    int cus = 0;
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+    auto k = pattern == 0 ? k_stream : k_stream_gs;
+    const dim3 grid(pattern == 0 ? (unsigned)((n16 + 1023) / 1024)
+                                 : (unsigned)std::min<size_t>((n16 + 1023) / 1024, 4 * (size_t)(cus > 0 ? cus : 256)));
     for (int i = 0; i < warmup; ++i)
-        hipLaunchKernelGGL(k_stream, grid, dim3(256), 0, (hipStream_t)st, (const uint4*)bufs[i % nbufs], n16, sink);
+        hipLaunchKernelGGL(k, grid, dim3(256), 0, (hipStream_t)st, (const uint4*)bufs[i % nbufs], n16, sink);
     EventPool pool((size_t)steps * 2);
     (void)hipDeviceSynchronize();
     for (int i = 0; i < steps; ++i)
-        hipExtLaunchKernelGGL(k_stream, grid, dim3(256), 0, (hipStream_t)st, pool.ev[2 * i], pool.ev[2 * i + 1], 0,
+        hipExtLaunchKernelGGL(k, grid, dim3(256), 0, (hipStream_t)st, pool.ev[2 * i], pool.ev[2 * i + 1], 0,
                               (const uint4*)bufs[i % nbufs], n16, sink);
     (void)hipDeviceSynchronize();
     double t = 0;
