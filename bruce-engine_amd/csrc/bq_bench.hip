@@ -79,8 +79,8 @@ __global__ void __launch_bounds__(256) k_empty(uint32_t* sink) {
     if (threadIdx.x == 1023) sink[0] = 1;  // never true: keeps the kernel
 }
 
-// Issue-rate probes: every wave runs `iters` rounds of 4 independent chains of
-// one instruction (no memory traffic; one operand changes per round), 8 waves
+// Issue-rate probes: every wave runs `iters` rounds of 4 (matrix) or 8 (VALU)
+// independent chains of one instruction (no memory traffic; one operand changes per round), 8 waves
 // per CU.  W selects the instruction.
 typedef int i32x4v __attribute__((ext_vector_type(4)));
 typedef int i32x16v __attribute__((ext_vector_type(16)));
@@ -141,23 +141,23 @@ __global__ void __launch_bounds__(256) k_inst_rate(int iters, uint32_t* sink) {
         }
         for (int k = 0; k < 4; ++k)
             for (int i = 0; i < 4; ++i) t ^= (uint32_t)c[k][i];
-    } else if constexpr (W == 5) {  // fp32 FMA (VALU)
-        float a = threadIdx.x, c[4] = {0.f, 1.f, 2.f, 3.f};
+    } else if constexpr (W == 5) {  // fp32 FMA (VALU; 8 chains, so latency does not limit)
+        float a = threadIdx.x, c[8] = {0.f, 1.f, 2.f, 3.f, 4.f, 5.f, 6.f, 7.f};
         for (int it = 0; it < iters; ++it) {
             a += 1.f;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) c[k] = __builtin_fmaf(a, 1.0001f, c[k]);
+            for (int k = 0; k < 8; ++k) c[k] = __builtin_fmaf(a, 1.0001f, c[k]);
         }
-        for (int k = 0; k < 4; ++k) t ^= __builtin_bit_cast(uint32_t, c[k]);
-    } else {  // int32 -> fp32 convert (VALU; paired with an add per chain)
-        int a = threadIdx.x;
-        float c[4] = {0.f, 1.f, 2.f, 3.f};
+        for (int k = 0; k < 8; ++k) t ^= __builtin_bit_cast(uint32_t, c[k]);
+    } else {  // int32 -> fp32 convert (VALU; paired with an add per chain, 8 chains)
+        int a = threadIdx.x - 7;
+        float c[8] = {0.f, 1.f, 2.f, 3.f, 4.f, 5.f, 6.f, 7.f};
         for (int it = 0; it < iters; ++it) {
             a += 1;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) c[k] += (float)(a ^ k);
+            for (int k = 0; k < 8; ++k) c[k] += (float)(a ^ k);
         }
-        for (int k = 0; k < 4; ++k) t ^= __builtin_bit_cast(uint32_t, c[k]);
+        for (int k = 0; k < 8; ++k) t ^= __builtin_bit_cast(uint32_t, c[k]);
     }
     if (t == 0x7fffffffu) sink[threadIdx.x & 3] = t;
 }
@@ -188,8 +188,9 @@ int bqb_inst_rate(int which, int blocks, int iters, uint32_t* sink, bq_stream_t 
     hipExtLaunchKernelGGL(k, dim3(blocks), dim3(256), 0, (hipStream_t)st, pool.ev[0], pool.ev[1], 0, iters, sink);
     (void)hipDeviceSynchronize();
     out[0] = elapsed(pool.ev[0], pool.ev[1]);
-    // waves per SIMD x rounds x chains (the convert probe counts convert + add)
-    out[1] = (double)blocks * 4 / (4.0 * (cus > 0 ? cus : 256)) * iters * 4 * (which == 6 ? 2 : 1);
+    // waves per SIMD x rounds x chains (4 for the matrix instructions, 8 for
+    // the VALU ones; the convert probe counts convert + add)
+    out[1] = (double)blocks * 4 / (4.0 * (cus > 0 ? cus : 256)) * iters * (which == 5 ? 8 : which == 6 ? 16 : 4);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
