@@ -104,3 +104,38 @@ def test_gguf_rejects(tmp_path, case):
         bq.Gguf(str(path))
     with pytest.raises(bq.BqError):
         bq.Gguf(str(tmp_path / "missing.gguf"))
+
+
+def test_gguf_hand_laid_file(tmp_path):
+    """A file laid out by hand, field by field from the GGUF v3 layout, not by
+    gguf_writer: the tensor table lists A then B, but B's data comes first in
+    the data section and A's starts after a 96-byte gap (offsets are free in
+    GGUF as long as each is a multiple of general.alignment, here 32).  The
+    reader must take every offset from the table, not from the order."""
+    import bq
+    rng = np.random.default_rng(11)
+    a = W.random_kquant(12, 2, 256, 176).tobytes()      # Q5_K 256 x 2: 352 B
+    b = rng.integers(0, 256, size=96, dtype=np.uint8).tobytes()   # F16, 48 values
+    off_b, off_a = 0, 96 + 96                             # B first, then a gap of 96 B
+    hdr = b"GGUF" + struct.pack("<I", 3) + struct.pack("<Q", 2) + struct.pack("<Q", 1)
+    key = b"general.alignment"
+    hdr += struct.pack("<Q", len(key)) + key + struct.pack("<I", 4) + struct.pack("<I", 32)   # u32 KV
+    for name, ne, gtype, off in ((b"blk.3.attn_q.weight", (256, 2), 13, off_a), (b"tok", (48,), 1, off_b)):
+        hdr += struct.pack("<Q", len(name)) + name + struct.pack("<I", len(ne))
+        hdr += b"".join(struct.pack("<Q", n) for n in ne) + struct.pack("<I", gtype) + struct.pack("<Q", off)
+    data_start = (len(hdr) + 31) // 32 * 32
+    blob = bytearray(hdr + b"\x00" * (data_start - len(hdr)))
+    data = bytearray(off_a + len(a))
+    data[off_b:off_b + len(b)] = b
+    data[off_b + len(b):off_a] = b"\xee" * (off_a - off_b - len(b))   # gap: must never be returned
+    data[off_a:off_a + len(a)] = a
+    blob += data
+    path = tmp_path / "hand.gguf"
+    path.write_bytes(bytes(blob))
+    with bq.Gguf(str(path)) as g:
+        assert len(g) == 2 and g.kv_num("general.alignment") == 32
+        ta, tb = g.tensor(0), g.tensor(1)
+        assert ta["offset"] == data_start + off_a and tb["offset"] == data_start + off_b
+        assert ta["nbytes"] == 352 and tb["nbytes"] == 96
+        assert ta["block"] == 3 and ta["suffix"] == "attn_q.weight"
+        assert g.read(0).tobytes() == a and g.read(1).tobytes() == b
