@@ -476,7 +476,7 @@ class Gguf:
     def tensor(self, i):
         t = GgufTensor()
         _check(load().bq_gguf_tensor_info(self._h, i, ctypes.byref(t)), "bq_gguf_tensor_info")
-        return {"name": t.name.decode(), "suffix": t.suffix.decode(), "ne": list(t.ne)[:t.ndim],
+        return {"name": t.name.decode(errors="replace"), "suffix": t.suffix.decode(errors="replace"), "ne": list(t.ne)[:t.ndim],
                 "offset": t.offset, "nbytes": t.nbytes, "type": t.ggml_type, "ndim": t.ndim, "block": t.block}
 
     def kv_num(self, key):
@@ -487,7 +487,7 @@ class Gguf:
     def kv_str(self, key):
         v = ctypes.c_char_p()
         r = load().bq_gguf_kv_str(self._h, key.encode(), ctypes.byref(v))
-        return v.value.decode() if r == BQ_OK else None
+        return v.value.decode(errors="replace") if r == BQ_OK else None
 
     def read(self, i, n=None, off=0):
         import numpy as np
