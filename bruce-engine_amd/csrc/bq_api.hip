@@ -51,10 +51,19 @@ constexpr int kMmqMinRows = 96;
 
 bool weight_ok(const bq_weight* w) { return w && w->K > 0 && w->N > 0 && (w->K % 256) == 0; }
 
+// Every kernel reads weights, activations and fp32 rows with 16-byte loads
+// (direct-to-LDS copies included), so each buffer must start 16-byte aligned;
+// a misaligned pointer is rejected here instead of reaching the device.
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+bool weight_al16(const bq_weight* w) { return al16(w->raw) && al16(w->rep) && al16(w->rep_min); }
+
 // Run a multi-row GEMV in row chunks that fit the per-block LDS limit.
 int gemv_rows(GemvKind kind, PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
               const int32_t* xsum, hipStream_t st) {
     if (K > kGemvMaxK) return BQ_UNSUPPORTED;
+    if (!al16(xq) || !al16(xd) || !al16(xsum)) return BQ_EINVAL;
+    for (int p = 0; p < pt.nparts; ++p)
+        if (!al16(pt.W[p])) return BQ_EINVAL;
     int r0 = 0;
     while (r0 < rows) {
         int c = std::min(rows - r0, (int)BQ_MAX_ROWS);
@@ -122,6 +131,7 @@ int bq_quantize_q8(const float* x, int rows, int K, int8_t* xq, float* xd, int32
     if (rows < 0 || K <= 0 || (K % 32) != 0) return BQ_EINVAL;
     if (rows == 0) return BQ_OK;
     if (!x || !xq || !xd || !xsum) return BQ_EINVAL;
+    if (!al16(x) || !al16(xq)) return BQ_EINVAL;
     return from_hip(launch_quant_q8(x, rows, K, xq, xd, xsum, xdh, (hipStream_t)st));
 }
 
@@ -241,6 +251,9 @@ int bq_gemv_q8_fused(float* const* ys, const bq_weight* const* ws, int nparts, c
         pt.N[p] = w->N;
     }
     pt.nparts = nparts;
+    for (int p = 0; p < nparts; ++p)
+        if (!al16(pt.W[p])) return BQ_EINVAL;
+    if (!al16(x) || !al16(xq) || !al16(xd) || !al16(xsum)) return BQ_EINVAL;
     const GemvKind kind = type == BQ_TYPE_Q5_K ? GemvKind::Q5K : (q6rep ? GemvKind::Q6KRep : GemvKind::Q6KRaw);
     hipStream_t s = (hipStream_t)st;
     if (!gemv_fused_supported(K)) return BQ_UNSUPPORTED;
@@ -285,7 +298,9 @@ int bq_gemv_norm_fused(float* const* ys, const bq_weight* const* ws, int nparts,
     const float* in[4] = {a, b, c, d};
     for (const float* q : in)
         if ((uintptr_t)q % 16) return BQ_EINVAL;
-    if ((uintptr_t)out % 16 || (uintptr_t)xq % 16) return BQ_EINVAL;
+    if ((uintptr_t)out % 16 || (uintptr_t)xq % 16 || !al16(xd) || !al16(xsum)) return BQ_EINVAL;
+    for (int p = 0; p < nparts; ++p)
+        if (!al16(pt.W[p])) return BQ_EINVAL;
     const GemvKind kind = type == BQ_TYPE_Q5_K ? GemvKind::Q5K : (q6rep ? GemvKind::Q6KRep : GemvKind::Q6KRaw);
     return from_hip(launch_gemv_producer(kind, pt, K, op, out, a, op != BQ_OP_NORM ? b : nullptr,
                                          op >= BQ_OP_RESID ? c : nullptr, op == BQ_OP_SILU ? d : nullptr, xq, xd,
@@ -318,6 +333,7 @@ int bq_gate_up_silu(float* h, const bq_weight* wg, const bq_weight* wu, const fl
     } else {
         return BQ_UNSUPPORTED;
     }
+    if (!al16(pt.W[0]) || !al16(pt.W[1]) || !al16(xq) || !al16(xd) || !al16(xsum)) return BQ_EINVAL;
     pt.N[0] = pt.N[1] = N;
     pt.Y[0] = pt.Y[1] = h;  // not written: the epilogue writes h
     pt.nparts = 2;
@@ -325,7 +341,6 @@ int bq_gate_up_silu(float* h, const bq_weight* wg, const bq_weight* wu, const fl
 }
 
 namespace {
-bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // The MMQ launch behind bq_try_mmq and the bq_gemm_b dispatchers.  min_w144 /
 // min_raw: the smallest row count taken by the prepacked / raw tier (below
@@ -336,7 +351,7 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
                  bq_stream_t st, int min_w144, int min_raw) {
     if (nparts < 1 || nparts > BQ_MAX_PARTS || rows < std::min(min_w144, min_raw)) return BQ_UNSUPPORTED;
     if (!ys || !ws || !ws[0] || !xq || !xd || !xsum) return BQ_EINVAL;
-    if (!al16(work) || !al16(xq)) return BQ_EINVAL;
+    if (!al16(work) || !al16(xq) || !al16(xd) || !al16(xsum) || !al16(xdh)) return BQ_EINVAL;
     const int K = ws[0]->K;
     PartTable pt;
     memset(&pt, 0, sizeof(pt));
@@ -345,7 +360,7 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
         const bq_weight* w = ws[p];
         if (!w || !w->raw || !ys[p] || w->ggml_type != BQ_TYPE_Q5_K) return BQ_UNSUPPORTED;
         if (w->K != K || w->N <= 0 || (w->N % 128) != 0) return BQ_UNSUPPORTED;
-        if (!al16(ys[p])) return BQ_EINVAL;  // the tiles store 16-byte vectors
+        if (!al16(ys[p]) || !weight_al16(w)) return BQ_EINVAL;  // the tiles store 16-byte vectors
         if (!w->rep || !w->rep_min || (K % 512) != 0) prepacked = false;
         pt.Y[p] = ys[p];
         pt.N[p] = w->N;
@@ -397,7 +412,7 @@ int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, co
                     void* work, size_t work_bytes, bq_stream_t st) {
     if (int s = ensure_init()) return s;
     if (!weight_ok(w) || !y || !xq || !xd || rows < 1) return BQ_EINVAL;
-    if (!al16(y) || !al16(xq) || !al16(work)) return BQ_EINVAL;
+    if (!al16(y) || !al16(xq) || !al16(xd) || !al16(work) || !weight_al16(w)) return BQ_EINVAL;
     if (w->ggml_type != BQ_TYPE_Q6_K || !w->rep || (w->N % 128) != 0) return BQ_UNSUPPORTED;
     return from_hip(launch_mmq_q6k(one_part(y, w->rep, w->N), rows, w->K, xq, xd, (hipStream_t)st, (float*)work,
                                    work ? work_bytes / sizeof(float) : 0));
@@ -683,7 +698,7 @@ int bq_gemv_q8s(float* y, const void* w, const int8_t* xq, const float* xd, int 
                 const float* rs, bq_stream_t st) {
     if (int s = ensure_init()) return s;
     if (!y || !w || !xq || !xd || K <= 0 || N <= 0 || (K % 256) != 0) return BQ_EINVAL;
-    if (((uintptr_t)w & 15) || ((uintptr_t)xq & 15)) return BQ_EINVAL;
+    if (!al16(w) || !al16(xq) || !al16(xd)) return BQ_EINVAL;
     if (rows < 1 || rows > BQ_MAX_ROWS || K > kQ8SMaxK) return BQ_UNSUPPORTED;
     return from_hip(launch_gemv_q8s(w, K, N, rows, xq, xd, rs, y, (hipStream_t)st));
 }
