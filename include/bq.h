@@ -12,7 +12,8 @@
  * Return codes: BQ_OK (0); BQ_UNSUPPORTED (1) = shape/type not handled, nothing
  * was enqueued and the caller should fall back (the reference's `return false`,
  * bruce.cu:7147-7161, :7366-7390); BQ_EINVAL (2) = bad argument (null pointer,
- * K not a multiple of 256, ...); BQ_ETOOBIG (3) = larger than the static
+ * K not a multiple of 256, a weight / activation / fp32 row buffer that does
+ * not start 16-byte aligned, ...); BQ_ETOOBIG (3) = larger than the static
  * scratch of the allocation-free entry point; a negative value = -(hipError_t) of a failed
  * launch.  bq_strerror() names each code.
  *
