@@ -462,15 +462,23 @@ def gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out):
         mq, md, ms_, mh = bq.quantize_q8(xm, with_xdh=True)
         ym = torch.empty((M, FF), device="cuda")
         res = {}
+        # the caller's K-split workspace, sized as INTEGRATION.md asks
+        # (bq_gemm_workspace_bytes); the call time runs from the GEMM kernel's
+        # start to the end of the call, so a leftover-tile sum is included
+        work = bq.workspace(M, K, FF)
+        wptr, wbytes = (ptr(work), work.numel() * 4) if work is not None else (None, 0)
         for name, w in (("w144", bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF, rep=gw144, rep_min=gdm)),
                         ("raw", bq.make_weight(g_gate, bq.TYPE_Q5_K, K, FF))):
             gsteps = 20 if M == 8192 else 50
-            r = B.bqb_gemm(gsteps, 5, ctypes.byref(w), M, ptr(mq), ptr(md), ptr(ms_), ptr(mh), ptr(ym), sp, out)
+            r = B.bqb_gemm(gsteps, 5, ctypes.byref(w), M, ptr(mq), ptr(md), ptr(ms_), ptr(mh), ptr(ym), wptr,
+                           wbytes, sp, out)
             if r != 0:
                 raise RuntimeError(f"bqb_gemm failed: {r}")
-            kms = out[1] / gsteps
-            tops = 2.0 * M * FF * K / (kms * 1e-3) / 1e12
-            res[name] = {"ms": round(kms, 4), "tops": round(tops, 1), "frac": round(tops / INT8_PEAK_TOPS, 4)}
+            cms, kms = out[2] / gsteps, out[1] / gsteps
+            tops = 2.0 * M * FF * K / (cms * 1e-3) / 1e12
+            res[name] = {"ms": round(cms, 4), "kernel_ms": round(kms, 4), "tops": round(tops, 1),
+                         "frac": round(tops / INT8_PEAK_TOPS, 4)}
+        del work
         # bytes of one launch (weights as streamed: W144 + Dm or GGUF; q8 X
         # with xd, xsum, xdh; fp32 Y) over the time, against 8 TB/s: the GEMM
         # is near the int8 ridge at M = 512 (SURVEY config 4)
@@ -565,7 +573,7 @@ def main():
     WP = ctypes.POINTER(bq.Weight)
     D4 = ctypes.c_double * 4
     B.bqb_decode_ffn.argtypes = [I, I, I, I, WP, WP, WP, P, P, P, P, P, P, P, P, P, P, P, P, P]
-    B.bqb_gemm.argtypes = [I, I, WP, I, P, P, P, P, P, P, P]
+    B.bqb_gemm.argtypes = [I, I, WP, I, P, P, P, P, P, P, ctypes.c_size_t, P, P]
     B.bqb_gemv_rows.argtypes = [I, I, I, WP, I, P, P, P, P, P, P]
     B.bqb_stream.argtypes = [I, I, I, I, P, ctypes.c_size_t, P, P, P]
     B.bqb_inst_rate.argtypes = [I, I, I, P, P, P]

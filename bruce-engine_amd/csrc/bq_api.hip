@@ -398,7 +398,8 @@ size_t bq_gemm_workspace_bytes(int rows, int K, int n_total) {
     // the largest split any tier / tile height takes for this shape
     const int ks = std::max(mmq_ksplit(rows, K, n_total, true, (size_t)-1, 128),
                             mmq_ksplit(rows, K, n_total, true, (size_t)-1, 32));
-    return ks > 1 ? (size_t)ks * rows * n_total * sizeof(float) : 0;
+    const size_t split = ks > 1 ? (size_t)ks * rows * n_total * sizeof(float) : 0;
+    return std::max(split, mmq_tail_ws_floats(rows, K, n_total) * sizeof(float));
 }
 
 int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int rows,

@@ -381,27 +381,40 @@ int bqb_decode_ffn(int mode, int steps, int warmup, int nsets, const bq_weight* 
 // Prefill GEMM: `steps` launches of try_launch_mmq over the same inputs (no
 // K-split workspace: the config 4 launches fill the GPU unsplit).
 //   out[0] = timed region (ms), out[1] = sum of per-launch event times (ms).
+// Prefill GEMM timing through bq_try_mmq with the caller's K-split workspace
+// (work, work_bytes; NULL / 0: none).  Per call, the GEMM kernel is bracketed
+// by its dispatch events and one more event is recorded after the call, so
+// out[1] = summed GEMM kernel durations and out[2] = summed call durations
+// from the GEMM kernel's start to the end of the call (the leftover-tile sum,
+// when the launch splits, included); the fill_xdh pre-pass of the W144 path
+// runs before the GEMM kernel and is in neither.  out[0] = the whole region.
 int bqb_gemm(int steps, int warmup, const bq_weight* w, int M, const int8_t* xq, const float* xd,
-             const int32_t* xs, uint16_t* xdh, float* y, bq_stream_t st, double* out) {
+             const int32_t* xs, uint16_t* xdh, float* y, void* work, size_t work_bytes, bq_stream_t st,
+             double* out) {
     float* ys[1] = {y};
     const bq_weight* ws[1] = {w};
     for (int i = 0; i < warmup; ++i)
-        if (int r = bq_try_mmq(ys, ws, 1, M, xq, xd, xs, xdh, nullptr, 0, st)) return r;
-    EventPool pool((size_t)steps * 2 + 2);
+        if (int r = bq_try_mmq(ys, ws, 1, M, xq, xd, xs, xdh, work, work_bytes, st)) return r;
+    EventPool pool((size_t)steps * 3 + 2);
     (void)hipDeviceSynchronize();
     (void)hipEventRecord(pool.ev[0], (hipStream_t)st);
     for (int i = 0; i < steps; ++i) {
-        // the fill_xdh pre-pass of the W144 path is not timed: the event pair
-        // brackets the GEMM kernel itself
-        bq_time_next_launch(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
-        if (int r = bq_try_mmq(ys, ws, 1, M, xq, xd, xs, xdh, nullptr, 0, st)) return r;
+        hipEvent_t* e = &pool.ev[2 + 3 * (size_t)i];
+        bq_time_next_launch(e[0], e[1]);
+        if (int r = bq_try_mmq(ys, ws, 1, M, xq, xd, xs, xdh, work, work_bytes, st)) return r;
+        (void)hipEventRecord(e[2], (hipStream_t)st);
     }
     (void)hipEventRecord(pool.ev[1], (hipStream_t)st);
     (void)hipDeviceSynchronize();
     out[0] = elapsed(pool.ev[0], pool.ev[1]);
-    double k = 0;
-    for (int i = 0; i < steps; ++i) k += elapsed(pool.ev[2 + 2 * i], pool.ev[3 + 2 * i]);
+    double k = 0, c = 0;
+    for (int i = 0; i < steps; ++i) {
+        const hipEvent_t* e = &pool.ev[2 + 3 * (size_t)i];
+        k += elapsed(e[0], e[1]);
+        c += elapsed(e[0], e[2]);
+    }
     out[1] = k;
+    out[2] = c;
     return 0;
 }
 

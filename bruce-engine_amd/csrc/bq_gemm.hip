@@ -55,6 +55,51 @@ BQ_DEV bool map_tile(int b, int ntm, int ntn, TileMap& t) {
     return true;
 }
 
+// Leftover-tile K split.  A launch of T tiles on C CUs runs for as long as its
+// busiest CU, which gets ceil(T / C) tiles; with T = q * C + L (0 < L < C)
+// every CU but L of them idles for the last tile's duration.  The tail split
+// runs the first q * C tiles whole and cuts each of the L leftover tiles into
+// k K slices, so the leftover work spreads over L * k pieces; the slices'
+// partial tiles go to the caller's workspace [slice][leftover tile][TM][128]
+// and k_sum_tail adds them in slice order.  k == 1: no tail split (the
+// uniform K split, blockIdx.y, or no split at all).
+struct TailSplit {
+    int k = 1;        // slices per leftover tile
+    int nfull = 0;    // tiles run whole (tile indices 0 .. nfull-1)
+    int gridfull = 0; // blocks of the whole tiles (a multiple of the XCD count)
+    int nleft = 0;    // leftover tiles (indices nfull .. nfull+nleft-1)
+};
+
+// Block -> (tile, slice, slices).  Returns false for a block with no work.
+// XCD-major over the whole tiles as map_tile; a leftover tile's k slices are
+// consecutive blocks.
+BQ_DEV bool map_tile_tail(int b, int ntm, int ntn, const TailSplit& ts, TileMap& t, int& kc, int& ks, int& left) {
+    left = -1;
+    if (ts.k <= 1) {
+        kc = blockIdx.y;
+        return map_tile(b, ntm, ntn, t);
+    }
+    if (b < ts.gridfull) {
+        const int per = ts.gridfull / kXcds;
+        const int idx = (b % kXcds) * per + b / kXcds;
+        if (idx >= ts.nfull) return false;
+        t.mt = idx % ntm;
+        t.nt = idx / ntm;
+        kc = 0;
+        ks = 1;
+        return true;
+    }
+    const int j = b - ts.gridfull;
+    if (j >= ts.nleft * ts.k) return false;
+    left = j / ts.k;
+    kc = j % ts.k;
+    ks = ts.k;
+    const int idx = ts.nfull + left;
+    t.mt = idx % ntm;
+    t.nt = idx / ntm;
+    return true;
+}
+
 // offset of slice kc, part p in the K-split workspace [slice][part][rows][N[part]]
 BQ_DEV size_t split_offset(const PartTable& pt, int p, int kc, int rows) {
     size_t ntot = 0, off = 0;
@@ -149,19 +194,19 @@ template <int TM>
 __global__ void __launch_bounds__(256, TM == 32 ? 3 : 2)
 k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
               const float* __restrict__ xd, const int32_t* __restrict__ xsum, int ksplit,
-              float* __restrict__ part) {
+              float* __restrict__ part, TailSplit ts) {
     using G = TileGeo<TM>;
     __shared__ __attribute__((aligned(16))) Smem<TM> sm;
     TileMap tm;
-    if (!map_tile(blockIdx.x, ntm, ntn, tm)) return;
+    int kc, left;
+    if (!map_tile_tail(blockIdx.x, ntm, ntn, ts, tm, kc, ksplit, left)) return;
     int nbase = tm.nt * kTN;
     const int p = part_of_ntile(pt, nbase);
     const int Nloc = pt.N[p];
     const uint8_t* __restrict__ W = (const uint8_t*)pt.W[p];
     const int m0 = tm.mt * TM;
     const int nb = K >> 5, nst = K >> 7, nsb = K >> 8;
-    // K split (blockIdx.y of ksplit): stages [s0, s1) of this slice
-    const int kc = blockIdx.y;
+    // K split (slice kc of ksplit): stages [s0, s1) of this slice
     const int s0 = kc * nst / ksplit, s1 = (kc + 1) * nst / ksplit;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -321,8 +366,19 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
     }
 
     // ---- epilogue: Y[m][n], lane owns token column l32, rows 8*rg + 4*lh + 0..3
-    // K split: slice kc's partial sums go to part[kc][part p: rows x N[p]]
-    float* __restrict__ Y = ksplit > 1 ? part + split_offset(pt, p, kc, rows) : pt.Y[p];
+    // K split: slice kc's partial sums go to part[kc][part p: rows x N[p]];
+    // a leftover tile's slice to its own [TM][128] block of the workspace
+    float* __restrict__ Y = pt.Y[p];
+    size_t ld = (size_t)Nloc;
+    int mo = 0, no = nbase;
+    if (left >= 0) {
+        Y = part + ((size_t)kc * ts.nleft + left) * (size_t)(kTN * TM);
+        ld = kTN;
+        mo = m0;
+        no = 0;
+    } else if (ksplit > 1) {
+        Y = part + split_offset(pt, p, kc, rows);
+    }
 #pragma unroll
     for (int mt = 0; mt < G::MT; ++mt) {
         const int m = m0 + t0 + mt * 32 + l32;
@@ -331,10 +387,10 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
         for (int nt = 0; nt < G::NT; ++nt)
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
-                const int n = nbase + n0 + nt * 32 + 8 * rg + 4 * lh;
+                const int n = no + n0 + nt * 32 + 8 * rg + 4 * lh;
                 const f32x4 v = {acc[nt][mt][4 * rg], acc[nt][mt][4 * rg + 1], acc[nt][mt][4 * rg + 2],
                                  acc[nt][mt][4 * rg + 3]};
-                *(f32x4*)(Y + (size_t)m * Nloc + n) = v;
+                *(f32x4*)(Y + (size_t)(m - mo) * ld + n) = v;
             }
     }
 }
@@ -510,12 +566,14 @@ BQ_DEV void mmq144_stage_any(const SmemStage<TM>& sb, f32x16 (&acc)[TileGeo<TM>:
 template <int TM>
 __global__ void __launch_bounds__(256, TM == 32 ? 3 : 2)
 k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
-           const float* __restrict__ xd, const uint16_t* __restrict__ xdh, int ksplit, float* __restrict__ part) {
+           const float* __restrict__ xd, const uint16_t* __restrict__ xdh, int ksplit, float* __restrict__ part,
+           TailSplit ts) {
     using G = TileGeo<TM>;
     __shared__ __attribute__((aligned(16))) SmemStage<TM> sm0;
     __shared__ __attribute__((aligned(16))) SmemStage<TM> sm1;
     TileMap tm;
-    if (!map_tile(blockIdx.x, ntm, ntn, tm)) return;
+    int kc, left;
+    if (!map_tile_tail(blockIdx.x, ntm, ntn, ts, tm, kc, ksplit, left)) return;
     int nbase = tm.nt * kTN;
     const int p = part_of_ntile(pt, nbase);
     const int Nloc = pt.N[p];
@@ -527,8 +585,7 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
     const int n0 = (wave / G::WM) * G::NT * 32, t0 = (wave % G::WM) * G::MT * 32;
     const int l32 = lane & 31, lh = lane >> 5;
     auto wsrc = [&](int s) { return W + ((size_t)s * Nloc + nbase) * kW144; };
-    // K split (blockIdx.y of ksplit): stage pairs [s0, s1) of this slice
-    const int kc = blockIdx.y;
+    // K split (slice kc of ksplit): stage pairs [s0, s1) of this slice
     const int s0 = 2 * (kc * (nst / 2) / ksplit), s1 = 2 * ((kc + 1) * (nst / 2) / ksplit);
     Mmq144Dma dof;
     dof.tok_hi = lane >> 3;
@@ -583,8 +640,19 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
         mmq144_stage_any<TM>(sm1, acc, n0, t0, l32, lh);
     }
 
-    // K split: slice kc's partial sums go to part[kc][part p: rows x N[p]]
-    float* __restrict__ Y = ksplit > 1 ? part + split_offset(pt, p, kc, rows) : pt.Y[p];
+    // K split: slice kc's partial sums go to part[kc][part p: rows x N[p]];
+    // a leftover tile's slice to its own [TM][128] block of the workspace
+    float* __restrict__ Y = pt.Y[p];
+    size_t ld = (size_t)Nloc;
+    int mo = 0, no = nbase;
+    if (left >= 0) {
+        Y = part + ((size_t)kc * ts.nleft + left) * (size_t)(kTN * TM);
+        ld = kTN;
+        mo = m0;
+        no = 0;
+    } else if (ksplit > 1) {
+        Y = part + split_offset(pt, p, kc, rows);
+    }
 #pragma unroll
     for (int mt = 0; mt < G::MT; ++mt) {
         const int m = m0 + t0 + mt * 32 + l32;
@@ -593,12 +661,34 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
         for (int nt = 0; nt < G::NT; ++nt)
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
-                const int n = nbase + n0 + nt * 32 + 8 * rg + 4 * lh;
+                const int n = no + n0 + nt * 32 + 8 * rg + 4 * lh;
                 const f32x4 v = {acc[nt][mt][4 * rg], acc[nt][mt][4 * rg + 1], acc[nt][mt][4 * rg + 2],
                                  acc[nt][mt][4 * rg + 3]};
-                *(f32x4*)(Y + (size_t)m * Nloc + n) = v;
+                *(f32x4*)(Y + (size_t)(m - mo) * ld + n) = v;
             }
     }
+}
+
+// y of the leftover tiles = the sum of their k slices (fixed slice order), one
+// float4 per thread: thread i -> tile i / (TM * 32), token row, 4 columns
+template <int TM>
+__global__ void __launch_bounds__(256) k_sum_tail(const float* __restrict__ ws, PartTable pt, int ntm, int rows,
+                                                  TailSplit ts) {
+    const size_t per = (size_t)TM * (kTN / 4);
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= per * ts.nleft) return;
+    const int left = (int)(i / per);
+    const int e = (int)(i % per), ml = e / (kTN / 4), c4 = e % (kTN / 4);
+    const int idx = ts.nfull + left;
+    const int m = (idx % ntm) * TM + ml;
+    if (m >= rows) return;
+    int nbase = (idx / ntm) * kTN;
+    const int p = part_of_ntile(pt, nbase);
+    const size_t slice = (size_t)ts.nleft * kTN * TM;
+    const f32x4* src = (const f32x4*)(ws + (size_t)left * kTN * TM) + e;
+    f32x4 v = src[0];
+    for (int k = 1; k < ts.k; ++k) v = v + src[k * (slice / 4)];
+    *(f32x4*)(pt.Y[p] + (size_t)m * pt.N[p] + nbase + 4 * c4) = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -887,11 +977,71 @@ static hipError_t sum_splits(const PartTable& pt, int ks, int rows, const float*
     return hipGetLastError();
 }
 
+// The leftover-tile split for `ntiles` tiles of `tm` tokens whose K has
+// `units` slice units: the k (2..4) that minimises the busiest CU's work,
+// floor(ntiles / CUs) + ceil(nleft * k / CUs) / k tiles, if that beats the
+// unsplit ceil(ntiles / CUs) by at least half a tile and the slices fit the
+// workspace; else k = 1.  Measured (9216 x 3072 W144, eager launches, µs,
+// unsplit -> split): 2048 rows (k = 2, 0.5 tile) 181.5 -> 168.5; smaller
+// gains did not pay for the shorter slices and the summing launch (2560 rows,
+// k = 3 for 0.33 tile: 216 -> 218), nor did more than 4 slices (2304 rows,
+// k = 8: 220 -> 227).
+constexpr int kMaxTailSplit = 4;
+TailSplit mmq_tail_split(int ntiles, int units, size_t ws_floats, int tm) {
+    TailSplit ts;
+    const int cus = g_mmq_cus;
+    const int q = ntiles / cus, nleft = ntiles % cus;
+    if (q == 0 || nleft == 0) return ts;
+    float best = (float)(q + 1);
+    int bk = 1;
+    for (int k = 2; k <= std::min(kMaxTailSplit, units); ++k) {
+        if ((size_t)nleft * k * kTN * tm > ws_floats) break;
+        const float load = (float)q + (float)((nleft * k + cus - 1) / cus) / (float)k;
+        if (load < best - 1e-6f) {
+            best = load;
+            bk = k;
+        }
+    }
+    if (bk == 1 || best > (float)(q + 1) - 0.5f) return ts;
+    ts.k = bk;
+    ts.nleft = nleft;
+    ts.nfull = ntiles - nleft;
+    ts.gridfull = (ts.nfull + kXcds - 1) / kXcds * kXcds;
+    return ts;
+}
+
+// Workspace floats the leftover-tile split of either Q5_K tier can use for
+// this shape (the larger of the two tile heights), at most kTailMaxFloats (32 MiB).
+constexpr size_t kTailMaxFloats = (size_t)8 << 20;
+size_t mmq_tail_ws_floats(int rows, int K, int ntot) {
+    size_t need = 0;
+    for (const int tm : {128, 32}) {
+        const int ntiles = ((rows + tm - 1) / tm) * (ntot / kTN);
+        if (mmq_ksplit(rows, K, ntot, false, (size_t)-1, tm) > 1) continue;
+        for (const int units : {K >> 8, K >> 7}) {  // W144 (stage pairs), raw tier (stages)
+            const TailSplit ts = mmq_tail_split(ntiles, units, kTailMaxFloats, tm);
+            if (ts.k > 1) need = std::max(need, (size_t)ts.nleft * ts.k * kTN * tm);
+        }
+    }
+    return need;
+}
+
 template <int TM>
-static void launch_w144_tm(const PartTable& pt, int ntm, int ntn, int ks, int rows, int K, const int8_t* xq,
-                           const float* xd, const uint16_t* xdh, hipStream_t st, float* ws) {
+static hipError_t launch_w144_tm(const PartTable& pt, int ntm, int ntn, int ks, const TailSplit& ts, int rows,
+                                 int K, const int8_t* xq, const float* xd, const uint16_t* xdh, hipStream_t st,
+                                 float* ws) {
+    if (ts.k > 1) {
+        launch_kernel(k_mmq_w144<TM>, dim3(ts.gridfull + ts.nleft * ts.k), dim3(256), 0, st, pt, ntm, ntn, rows, K,
+                      xq, xd, xdh, 1, ws, ts);
+        const size_t n4 = (size_t)ts.nleft * TM * (kTN / 4);
+        launch_kernel(k_sum_tail<TM>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (const float*)ws, pt,
+                      ntm, rows, ts);
+        return hipGetLastError();
+    }
     const dim3 grid(mmq_grid(ntm, ntn).x, ks);
-    launch_kernel(k_mmq_w144<TM>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xdh, ks, ws);
+    launch_kernel(k_mmq_w144<TM>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xdh, ks, ws, ts);
+    if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
+    return hipGetLastError();
 }
 
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
@@ -901,10 +1051,24 @@ hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, c
     const int ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
     const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, tm);
-    if (tm == 32)
-        launch_w144_tm<32>(pt, ntm, ntn, ks, rows, K, xq, xd, xdh, st, ws);
-    else
-        launch_w144_tm<128>(pt, ntm, ntn, ks, rows, K, xq, xd, xdh, st, ws);
+    const TailSplit ts = ks > 1 ? TailSplit{} : mmq_tail_split(ntm * ntn, K >> 8, ws ? ws_floats : 0, tm);
+    if (tm == 32) return launch_w144_tm<32>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xdh, st, ws);
+    return launch_w144_tm<128>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xdh, st, ws);
+}
+
+template <int TM>
+static hipError_t launch_raw_tm(const PartTable& pt, int ntm, int ntn, int ks, const TailSplit& ts, int rows, int K,
+                                const int8_t* xq, const float* xd, const int32_t* xsum, hipStream_t st, float* ws) {
+    if (ts.k > 1) {
+        launch_kernel(k_mmq_q5k_raw<TM>, dim3(ts.gridfull + ts.nleft * ts.k), dim3(256), 0, st, pt, ntm, ntn, rows,
+                      K, xq, xd, xsum, 1, ws, ts);
+        const size_t n4 = (size_t)ts.nleft * TM * (kTN / 4);
+        launch_kernel(k_sum_tail<TM>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (const float*)ws, pt,
+                      ntm, rows, ts);
+        return hipGetLastError();
+    }
+    const dim3 grid(mmq_grid(ntm, ntn).x, ks);
+    launch_kernel(k_mmq_q5k_raw<TM>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xsum, ks, ws, ts);
     if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
     return hipGetLastError();
 }
@@ -915,13 +1079,9 @@ hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, c
     const int ntm = (rows + tm - 1) / tm, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
     const int ks = mmq_ksplit(rows, K, ntotal(pt), true, ws ? ws_floats : 0, tm);
-    const dim3 grid(mmq_grid(ntm, ntn).x, ks);
-    if (tm == 32)
-        launch_kernel(k_mmq_q5k_raw<32>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xsum, ks, ws);
-    else
-        launch_kernel(k_mmq_q5k_raw<128>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xsum, ks, ws);
-    if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
-    return hipGetLastError();
+    const TailSplit ts = ks > 1 ? TailSplit{} : mmq_tail_split(ntm * ntn, K >> 7, ws ? ws_floats : 0, tm);
+    if (tm == 32) return launch_raw_tm<32>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xsum, st, ws);
+    return launch_raw_tm<128>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xsum, st, ws);
 }
 
 hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,

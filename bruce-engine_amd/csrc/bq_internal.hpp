@@ -80,6 +80,7 @@ hipError_t launch_repack_q6k(const void* raw, int K, int N, void* w160, hipStrea
 // (stage_units: the raw tier, which splits at 128-value stages; tm: the
 // token-tile height, 128 or the W144 kernel's 32).
 int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, int tm = 128);
+size_t mmq_tail_ws_floats(int rows, int K, int ntot);  // workspace of the Q5_K leftover-tile split
 void mmq_set_cus(int cus);  // the device's CU count (workgroup slots of the split choice)
 hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                               const int32_t* xsum, hipStream_t st, float* ws = nullptr, size_t ws_floats = 0);

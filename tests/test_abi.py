@@ -96,7 +96,11 @@ def test_workspace_bytes():
     # slots, evened to 6 over the raw tier's 24 stages (4 each); the 32-token
     # tile (144 tiles, 768 slots) takes 5: the larger is reserved
     assert L.bq_gemm_workspace_bytes(64, 3072, 9216) == 6 * 64 * 9216 * 4
-    assert L.bq_gemm_workspace_bytes(2048, 3072, 9216) == 0      # 1152 tiles fill the GPU
+    # 1152 tiles = 4 x 256 + 128 leftover tiles: the W144 tier cuts each
+    # leftover tile into 2 K slices of 128 x 128 fp32 partial tiles
+    assert L.bq_gemm_workspace_bytes(2048, 3072, 9216) == 128 * 2 * 128 * 128 * 4
+    assert L.bq_gemm_workspace_bytes(4096, 3072, 9216) == 0      # 2304 tiles = 9 x 256: no leftover
     assert L.bq_gemm_workspace_bytes(0, 3072, 9216) == 0
-    worst = max(L.bq_gemm_workspace_bytes(r, 3072, n) for r in range(1, 600, 7) for n in (128, 1024, 9216, 36864))
+    worst = max(L.bq_gemm_workspace_bytes(r, 3072, n) for r in list(range(1, 600, 7)) + list(range(600, 9000, 97))
+                for n in (128, 1024, 9216, 36864))
     assert worst <= 32 << 20

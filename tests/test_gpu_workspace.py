@@ -113,3 +113,67 @@ def test_gemm_b_graph_capture(bq, oracle, rows):
         torch.cuda.synchronize()
         assert np.array_equal(host(y).view(np.uint32), eager.view(np.uint32)), rep
     del graph
+
+
+@pytest.mark.parametrize("prepacked", [True, False])
+@pytest.mark.parametrize("M,Ns", [(1536, [9216]), (2048, [9216]), (2304, [9216]), (2048, [9216, 2048])])
+def test_q5k_leftover_tile_split(bq, oracle, M, Ns, prepacked):
+    """Q5_K prefill GEMM (W144 and raw tiers) with more tiles than CUs and a
+    remainder (M = 2048 on 9216 rows: 1152 tiles = 4 x 256 + 128): the leftover tiles run as K
+    slices into the workspace and one more launch sums them.  Equal calls give
+    equal bits; against the unsplit launch (no workspace) the outputs differ
+    only by fp32 summation order; rows of the last token tile (whose tiles
+    include leftover ones) are checked against the oracle."""
+    import torch
+    K = 3072
+    print(f"q5k leftover split M={M} Ns={Ns} prepacked={prepacked}", flush=True)
+    assert bq.workspace_bytes(M, K, sum(Ns)) > 0
+    raws, ws = _parts(bq, 2700 + M, Ns, K, prepacked)
+    x, _ = acts(2750 + M, M, K)
+    xq, xd, xs = oracle.q8_rows(x)
+    gq, gd, gs = dev(xq), dev(xd), dev(xs)
+    xdh = torch.empty((M, K // 32), dtype=torch.int16, device="cuda")
+    outs = []
+    for work in ("auto", "auto", None):
+        ys = [torch.full((M, n), float("nan"), device="cuda") for n in Ns]
+        assert bq.try_mmq(ys, ws, M, gq, gd, gs, xdh, work=work) == bq.BQ_OK
+        torch.cuda.synchronize()
+        outs.append([host(y) for y in ys])
+    for i, n in enumerate(Ns):
+        a, b, c = outs[0][i], outs[1][i], outs[2][i]
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert np.isfinite(a).all()
+        scale = np.abs(c).max(axis=1, keepdims=True)
+        assert (np.abs(a - c) <= 1e-5 * scale).all(), f"part {i}: split vs unsplit"
+        rows = np.arange(M - 12, M)                      # the last token tile's rows
+        ref = _ref(oracle, raws[i], K, n, xq[rows], xd[rows], xs[rows], prepacked)
+        check(oracle, a[rows], ref, what=f"part {i} last rows")
+
+
+def test_w144_leftover_split_graph_capture(bq, oracle):
+    """The leftover-tile split (two launches) captured in a HIP graph replays
+    bit-identically to the eager call."""
+    import torch
+    K, N, M = 3072, 9216, 2048
+    raws, ws = _parts(bq, 2800, [N], K, True)
+    x, _ = acts(2801, M, K)
+    xq, xd, xs = oracle.q8_rows(x)
+    gq, gd, gs = dev(xq), dev(xd), dev(xs)
+    xdh = torch.empty((M, K // 32), dtype=torch.int16, device="cuda")
+    work = bq.workspace(M, K, N)
+    y = torch.full((M, N), float("nan"), device="cuda")
+    assert bq.try_mmq([y], ws, M, gq, gd, gs, xdh, work=work) == bq.BQ_OK
+    torch.cuda.synchronize()
+    eager = host(y).copy()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        assert bq.try_mmq([y], ws, M, gq, gd, gs, xdh, work=work) == bq.BQ_OK
+    for rep in range(3):
+        y.fill_(float("nan"))
+        work.fill_(float("nan"))
+        torch.randn(1 << 20, device="cuda").sum()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(y).view(np.uint32), eager.view(np.uint32)), rep
+    del graph
