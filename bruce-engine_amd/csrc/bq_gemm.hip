@@ -928,14 +928,31 @@ int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, in
 // the 32-token tile (the 128-token tile costs the same at any row count up
 // to 128); at a few hundred to a few thousand rows it depends on how evenly
 // the tiles fill the workgroup slots.
-int mmq_tile_rows(int rows, int K, int ntot, bool stage_units, size_t ws_floats, float e32) {
+TailSplit mmq_tail_split(int ntiles, int units, size_t ws_floats, int tm, float e = 1.f);
+constexpr float kTailMinSaving = 384.f;  // see mmq_tail_split
+
+// tail: the kernel takes the leftover-tile split (both Q5_K tiers), so the
+// busiest CU's count is the split one
+int mmq_tile_rows(int rows, int K, int ntot, bool stage_units, size_t ws_floats, float e32, bool tail) {
     float best = 0.f;
     int pick = 128;
     for (const int tm : {128, 32}) {
         const int ks = mmq_ksplit(rows, K, ntot, stage_units, ws_floats, tm);
         const long long ctas = (long long)((rows + tm - 1) / tm) * (ntot / kTN) * ks;
-        const int per = ((stage_units ? K >> 7 : K >> 8) + ks - 1) / ks;
-        const float est = (float)((ctas + g_mmq_cus - 1) / g_mmq_cus) * tm * per * (tm == 32 ? e32 : 1.f);
+        const int units = stage_units ? K >> 7 : K >> 8;
+        const int per = (units + ks - 1) / ks;
+        float load = (float)((ctas + g_mmq_cus - 1) / g_mmq_cus);
+        bool split = ks > 1;
+        if (tail && ks == 1) {
+            const TailSplit ts = mmq_tail_split((int)ctas, units, ws_floats, tm, tm == 32 ? e32 : 1.f);
+            if (ts.k > 1) {
+                load = (float)(ctas / g_mmq_cus) +
+                       (float)((ts.nleft * ts.k + g_mmq_cus - 1) / g_mmq_cus) / (float)ts.k;
+                split = true;
+            }
+        }
+        // a split launch also pays its summing launch and partial-tile traffic
+        const float est = load * tm * per * (tm == 32 ? e32 : 1.f) + (split ? kTailMinSaving : 0.f);
         if (tm == 128 || est < best) {
             best = est;
             pick = tm;
@@ -986,12 +1003,19 @@ static hipError_t sum_splits(const PartTable& pt, int ks, int rows, const float*
 // gains did not pay for the shorter slices and the summing launch (2560 rows,
 // k = 3 for 0.33 tile: 216 -> 218), nor did more than 4 slices (2304 rows,
 // k = 8: 220 -> 227).
+// It must also save at least kTailMinSaving tile-token-units (tm x K units x
+// e, e = the tile height's relative cost per output) on the busiest CU: about
+// 8 us on these kernels, against the ~5 us of the summing launch and the
+// partial tiles' traffic (9216 x 3072 W144 at 512 rows: a 32-token tile split
+// saving half a tile measured 59.8 -> 63 us).
 constexpr int kMaxTailSplit = 4;
-TailSplit mmq_tail_split(int ntiles, int units, size_t ws_floats, int tm) {
+TailSplit mmq_tail_split(int ntiles, int units, size_t ws_floats, int tm, float e) {
     TailSplit ts;
     const int cus = g_mmq_cus;
     const int q = ntiles / cus, nleft = ntiles % cus;
-    if (q == 0 || nleft == 0) return ts;
+    // with one whole tile per CU each runs alone on its CU and the leftover
+    // slices lose (512 x 9216 W144, 128-token tiles: 62 -> 67 us)
+    if (q < 2 || nleft == 0) return ts;
     float best = (float)(q + 1);
     int bk = 1;
     for (int k = 2; k <= std::min(kMaxTailSplit, units); ++k) {
@@ -1003,6 +1027,7 @@ TailSplit mmq_tail_split(int ntiles, int units, size_t ws_floats, int tm) {
         }
     }
     if (bk == 1 || best > (float)(q + 1) - 0.5f) return ts;
+    if (((float)(q + 1) - best) * (float)tm * (float)units * e < kTailMinSaving) return ts;
     ts.k = bk;
     ts.nleft = nleft;
     ts.nfull = ntiles - nleft;
@@ -1019,7 +1044,7 @@ size_t mmq_tail_ws_floats(int rows, int K, int ntot) {
         const int ntiles = ((rows + tm - 1) / tm) * (ntot / kTN);
         if (mmq_ksplit(rows, K, ntot, false, (size_t)-1, tm) > 1) continue;
         for (const int units : {K >> 8, K >> 7}) {  // W144 (stage pairs), raw tier (stages)
-            const TailSplit ts = mmq_tail_split(ntiles, units, kTailMaxFloats, tm);
+            const TailSplit ts = mmq_tail_split(ntiles, units, kTailMaxFloats, tm, tm == 32 ? 1.33f : 1.f);
             if (ts.k > 1) need = std::max(need, (size_t)ts.nleft * ts.k * kTN * tm);
         }
     }
@@ -1046,12 +1071,13 @@ static hipError_t launch_w144_tm(const PartTable& pt, int ntm, int ntn, int ks, 
 
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                               const uint16_t* xdh, hipStream_t st, float* ws, size_t ws_floats) {
-    const int tm = mmq_tile_rows(rows, K, ntotal(pt), false, ws ? ws_floats : 0, 1.115f);
+    const int tm = mmq_tile_rows(rows, K, ntotal(pt), false, ws ? ws_floats : 0, 1.115f, true);
     const int ntm = (rows + tm - 1) / tm;
     const int ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
     const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, tm);
-    const TailSplit ts = ks > 1 ? TailSplit{} : mmq_tail_split(ntm * ntn, K >> 8, ws ? ws_floats : 0, tm);
+    const TailSplit ts =
+        ks > 1 ? TailSplit{} : mmq_tail_split(ntm * ntn, K >> 8, ws ? ws_floats : 0, tm, tm == 32 ? 1.115f : 1.f);
     if (tm == 32) return launch_w144_tm<32>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xdh, st, ws);
     return launch_w144_tm<128>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xdh, st, ws);
 }
@@ -1075,18 +1101,19 @@ static hipError_t launch_raw_tm(const PartTable& pt, int ntm, int ntn, int ks, c
 
 hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                               const int32_t* xsum, hipStream_t st, float* ws, size_t ws_floats) {
-    const int tm = mmq_tile_rows(rows, K, ntotal(pt), true, ws ? ws_floats : 0, 1.33f);
+    const int tm = mmq_tile_rows(rows, K, ntotal(pt), true, ws ? ws_floats : 0, 1.33f, true);
     const int ntm = (rows + tm - 1) / tm, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
     const int ks = mmq_ksplit(rows, K, ntotal(pt), true, ws ? ws_floats : 0, tm);
-    const TailSplit ts = ks > 1 ? TailSplit{} : mmq_tail_split(ntm * ntn, K >> 7, ws ? ws_floats : 0, tm);
+    const TailSplit ts =
+        ks > 1 ? TailSplit{} : mmq_tail_split(ntm * ntn, K >> 7, ws ? ws_floats : 0, tm, tm == 32 ? 1.33f : 1.f);
     if (tm == 32) return launch_raw_tm<32>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xsum, st, ws);
     return launch_raw_tm<128>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xsum, st, ws);
 }
 
 hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                           hipStream_t st, float* ws, size_t ws_floats) {
-    const int tm = mmq_tile_rows(rows, K, ntotal(pt), false, ws ? ws_floats : 0, 1.06f);
+    const int tm = mmq_tile_rows(rows, K, ntotal(pt), false, ws ? ws_floats : 0, 1.06f, false);
     const int ntm = (rows + tm - 1) / tm, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
     const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, tm);
