@@ -929,7 +929,10 @@ int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, in
 // to 128); at a few hundred to a few thousand rows it depends on how evenly
 // the tiles fill the workgroup slots.
 TailSplit mmq_tail_split(int ntiles, int units, size_t ws_floats, int tm, float e = 1.f);
-constexpr float kTailMinSaving = 384.f;  // see mmq_tail_split
+constexpr float kTailMinSaving = 192.f;  // see mmq_tail_split
+// the fixed cost of a split launch (its summing launch and partial-tile
+// traffic, about 8 us) in the tile-height estimate's units
+constexpr float kSplitCost = 384.f;
 
 // tail: the kernel takes the leftover-tile split (both Q5_K tiers), so the
 // busiest CU's count is the split one
@@ -952,7 +955,7 @@ int mmq_tile_rows(int rows, int K, int ntot, bool stage_units, size_t ws_floats,
             }
         }
         // a split launch also pays its summing launch and partial-tile traffic
-        const float est = load * tm * per * (tm == 32 ? e32 : 1.f) + (split ? kTailMinSaving : 0.f);
+        const float est = load * tm * per * (tm == 32 ? e32 : 1.f) + (split ? kSplitCost : 0.f);
         if (tm == 128 || est < best) {
             best = est;
             pick = tm;
@@ -1004,10 +1007,8 @@ static hipError_t sum_splits(const PartTable& pt, int ks, int rows, const float*
 // k = 3 for 0.33 tile: 216 -> 218), nor did more than 4 slices (2304 rows,
 // k = 8: 220 -> 227).
 // It must also save at least kTailMinSaving tile-token-units (tm x K units x
-// e, e = the tile height's relative cost per output) on the busiest CU: about
-// 8 us on these kernels, against the ~5 us of the summing launch and the
-// partial tiles' traffic (9216 x 3072 W144 at 512 rows: a 32-token tile split
-// saving half a tile measured 59.8 -> 63 us).
+// e, e = the tile height's relative cost per output) on the busiest CU, about
+// half of what the summing launch and the partial tiles cost.
 constexpr int kMaxTailSplit = 4;
 TailSplit mmq_tail_split(int ntiles, int units, size_t ws_floats, int tm, float e) {
     TailSplit ts;
