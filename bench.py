@@ -462,8 +462,8 @@ def gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out):
         mq, md, ms_, mh = bq.quantize_q8(xm, with_xdh=True)
         ym = torch.empty((M, FF), device="cuda")
         res = {}
-        # the caller's K-split workspace, sized as INTEGRATION.md asks
-        # (bq_gemm_workspace_bytes); the call time runs from the GEMM kernel's
+        # the caller's K-split workspace, sized by bq_gemm_workspace_bytes as
+        # an engine caller allocates it; the call time runs from the GEMM kernel's
         # start to the end of the call, so a leftover-tile sum is included
         work = bq.workspace(M, K, FF)
         wptr, wbytes = (ptr(work), work.numel() * 4) if work is not None else (None, 0)
@@ -481,7 +481,7 @@ def gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out):
         del work
         # bytes of one launch (weights as streamed: W144 + Dm or GGUF; q8 X
         # with xd, xsum, xdh; fp32 Y) over the time, against 8 TB/s: the GEMM
-        # is near the int8 ridge at M = 512 (SURVEY config 4)
+        # is near the int8 ridge at M = 512
         xbytes = M * K + M * (K // 32) * 10
         for name, wb in (("w144", gw144.nbytes + gdm.nbytes), ("raw", g_gate.nbytes)):
             res[name]["hbm_frac"] = round((wb + xbytes + 4 * M * FF) / (res[name]["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)

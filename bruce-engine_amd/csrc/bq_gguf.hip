@@ -1,5 +1,5 @@
 // bq_gguf.hip -- GGUF v3 reader and streaming weight loader feeding the
-// repacks (SURVEY §8f rank 3).  Host code only; the device work is
+// repacks.  Host code only; the device work is
 // hipMemcpyAsync plus the repack / conversion kernels of this library.
 //
 // Format (what engine/src/gguf.h:146-312 parses): little-endian

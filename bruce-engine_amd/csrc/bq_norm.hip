@@ -1,5 +1,5 @@
 // bq_norm.hip -- the q8 producers: row L2 norms that emit the q8 activations
-// the GEMVs consume, in the same pass (SURVEY §8f rank 2).
+// the GEMVs consume, in the same pass.
 //
 // Reference kernels (bruce.cu), all "elementwise op -> L2 norm -> q8_emit":
 //   k_norm :541 / k_norm_rows :1110            t = src
