@@ -116,17 +116,18 @@ def test_gemm_b_graph_capture(bq, oracle, rows):
 
 
 @pytest.mark.parametrize("prepacked", [True, False])
-@pytest.mark.parametrize("M,Ns", [(1536, [9216]), (2048, [9216]), (2304, [9216]), (2048, [9216, 2048])])
-def test_q5k_leftover_tile_split(bq, oracle, M, Ns, prepacked):
+@pytest.mark.parametrize("M,Ns,K", [(1536, [9216], 3072), (2048, [9216], 3072), (2304, [9216], 3072),
+                                    (2048, [9216, 2048], 3072), (2048, [7168], 2560)])
+def test_q5k_leftover_tile_split(bq, oracle, M, Ns, K, prepacked):
     """Q5_K prefill GEMM (W144 and raw tiers) with more tiles than CUs and a
-    remainder (M = 2048 on 9216 rows: 1152 tiles = 4 x 256 + 128): the leftover tiles run as K
+    remainder (M = 2048 on 9216 rows: 1152 tiles = 4 x 256 + 128; the reference
+    model's 7168 x 2560 gate/up: 896 = 3 x 256 + 128): the leftover tiles run as K
     slices into the workspace and one more launch sums them.  Equal calls give
     equal bits; against the unsplit launch (no workspace) the outputs differ
     only by fp32 summation order; rows of the last token tile (whose tiles
     include leftover ones) are checked against the oracle."""
     import torch
-    K = 3072
-    print(f"q5k leftover split M={M} Ns={Ns} prepacked={prepacked}", flush=True)
+    print(f"q5k leftover split M={M} Ns={Ns} K={K} prepacked={prepacked}", flush=True)
     assert bq.workspace_bytes(M, K, sum(Ns)) > 0
     raws, ws = _parts(bq, 2700 + M, Ns, K, prepacked)
     x, _ = acts(2750 + M, M, K)
