@@ -40,7 +40,8 @@ EXPORTS = [
     "bq_quantize_q8s_host", "bq_gemv_q8s", "bq_norm_q8", "bq_add_norm_q8", "bq_resid_q8",
     "bq_gate_norm_q8", "bq_silu_mul_norm_q8", "bq_gguf_open", "bq_gguf_close", "bq_gguf_n_tensors",
     "bq_gguf_find", "bq_gguf_tensor_info", "bq_gguf_kv_num", "bq_gguf_kv_str", "bq_gguf_read", "bq_gguf_load",
-    "bq_gemv_norm_fused", "bq_gate_up_silu", "bq_gemm_workspace_bytes", "bq_gemm_b_fused_noalloc",
+    "bq_gemv_norm_fused", "bq_gate_up_silu", "bq_gemm_workspace_bytes", "bq_gemm_workspace_bytes_cus",
+    "bq_gemm_b_fused_noalloc",
     "bq_noalloc_scratch_bytes", "bq_decode_enqueue", "bq_decode_graph_create", "bq_decode_graph_launch",
     "bq_decode_graph_destroy",
 ]
@@ -119,6 +120,7 @@ def load(path=LIB_PATH):
         "bq_gemm_q6k_dp": (I, [P, WP, I, P, P, I, P]),
         "bq_gemm_q6k_raw": (I, [P, WP, I, P, P, I, P]),
         "bq_gemm_workspace_bytes": (S, [I, I, I]),
+        "bq_gemm_workspace_bytes_cus": (S, [I, I, I, I]),
         "bq_try_mmq": (I, [P, P, I, I, P, P, P, P, P, S, P]),
         "bq_gemm_q6k_mma": (I, [P, WP, I, P, P, P, S, P]),
         "bq_gemm_b": (I, [P, WP, I, P, P, P, P, P, S, P]),
@@ -315,13 +317,26 @@ def workspace(rows, K, n_total, device="cuda"):
     return torch.empty(n // 4, dtype=torch.float32, device=device) if n else None
 
 
+_ws_cache = {}  # (device, stream) -> the largest workspace handed out there so far
+
+
 def _work(work, rows, K, n_total):
-    """work="auto": a fresh workspace sized for the full split (torch's
-    caching allocator keeps it stream-ordered); None: no split; a tensor: used
-    as given.  Returns (pointer, bytes, tensor kept alive by the caller)."""
+    """work="auto": a workspace sized for the full split, one per (device,
+    stream) reused by every call there (calls on one stream are ordered, so
+    they can share it) and grown when a shape needs more; None: no split; a
+    tensor: used as given.  Returns (pointer, bytes, tensor kept alive by the
+    caller)."""
     if isinstance(work, str):
         assert work == "auto"
-        work = workspace(rows, K, n_total)
+        import torch
+        n = workspace_bytes(rows, K, n_total)
+        if n == 0:
+            return None, 0, None
+        key = (torch.cuda.current_device(), torch.cuda.current_stream().cuda_stream)
+        work = _ws_cache.get(key)
+        if work is None or work.numel() * 4 < n:
+            work = torch.empty(n // 4, dtype=torch.float32, device="cuda")
+            _ws_cache[key] = work
     if work is None:
         return None, 0, None
     return _ptr(work), work.numel() * work.element_size(), work

@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <atomic>
 #include <mutex>
 
 #include "../../include/bq.h"
@@ -20,30 +21,46 @@ using namespace bq;
 
 namespace {
 
+// Properties of each device the library runs on, read on the first call
+// made with that device current: the per-block LDS limit (GEMV row chunks)
+// and the CU count (the prefill GEMMs' split choices, the logits head's grid).
 struct DevInfo {
     size_t lds_per_block = 65536;
     int cus = 256;
+    int status = BQ_OK;
+    std::atomic<bool> ready{false};
 };
 
-std::once_flag g_once;
-DevInfo g_dev;
-int g_init_status = BQ_OK;
+constexpr int kMaxDevices = 64;
+std::mutex g_dev_mu;
+DevInfo g_devs[kMaxDevices];
+thread_local const DevInfo* t_dev = nullptr;  // the current device's entry (set by ensure_init)
 
 int from_hip(hipError_t e) { return e == hipSuccess ? BQ_OK : -(int)e; }
 int scratch_ptr(void** out);  // bq_gemm_b_fused_noalloc's scratch (below)
 
+// Every entry point that touches a device calls this first: it looks up (on
+// first use, queries) the current device's properties and points t_dev at them.
 int ensure_init() {
-    std::call_once(g_once, [] {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess) { g_init_status = -(int)hipErrorNoDevice; return; }
-        hipDeviceProp_t prop;
-        if (hipGetDeviceProperties(&prop, dev) != hipSuccess) { g_init_status = -(int)hipErrorNoDevice; return; }
-        g_dev.lds_per_block = prop.sharedMemPerBlock;
-        g_dev.cus = prop.multiProcessorCount;
-        q8s_set_cus(g_dev.cus);
-        mmq_set_cus(g_dev.cus);
-    });
-    return g_init_status;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return -(int)hipErrorNoDevice;
+    if (dev < 0 || dev >= kMaxDevices) return BQ_UNSUPPORTED;
+    DevInfo& d = g_devs[dev];
+    if (!d.ready.load(std::memory_order_acquire)) {
+        std::lock_guard<std::mutex> lk(g_dev_mu);
+        if (!d.ready.load(std::memory_order_relaxed)) {
+            hipDeviceProp_t prop;
+            if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+                d.status = -(int)hipErrorNoDevice;
+            } else {
+                d.lds_per_block = prop.sharedMemPerBlock;
+                d.cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+            }
+            d.ready.store(true, std::memory_order_release);
+        }
+    }
+    t_dev = &d;
+    return d.status;
 }
 
 // try_launch_mmq's row threshold (bruce.cu:7369: rows >= 96)
@@ -67,8 +84,8 @@ int gemv_rows(GemvKind kind, PartTable pt, int rows, int K, const int8_t* xq, co
     int r0 = 0;
     while (r0 < rows) {
         int c = std::min(rows - r0, (int)BQ_MAX_ROWS);
-        while (c > 1 && gemv_lds_bytes(kind, c, K) > g_dev.lds_per_block) --c;
-        if (gemv_lds_bytes(kind, c, K) > g_dev.lds_per_block) return BQ_UNSUPPORTED;
+        while (c > 1 && gemv_lds_bytes(kind, c, K) > t_dev->lds_per_block) --c;
+        if (gemv_lds_bytes(kind, c, K) > t_dev->lds_per_block) return BQ_UNSUPPORTED;
         PartTable q = pt;
         for (int p = 0; p < pt.nparts; ++p) q.Y[p] = pt.Y[p] + (size_t)r0 * pt.N[p];
         const int nb = K / 32;
@@ -379,10 +396,10 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
         }
         hipError_t e = launch_fill_xdh(xd, xsum, rows * (K / 32), xdh, s);
         if (e != hipSuccess) return from_hip(e);
-        return from_hip(launch_mmq_q5k_144(pt, rows, K, xq, xd, xdh, s, wf, wn));
+        return from_hip(launch_mmq_q5k_144(pt, rows, K, xq, xd, xdh, s, t_dev->cus, wf, wn));
     }
     for (int p = 0; p < nparts; ++p) pt.W[p] = ws[p]->raw;
-    return from_hip(launch_mmq_q5k_raw(pt, rows, K, xq, xd, xsum, s, wf, wn));
+    return from_hip(launch_mmq_q5k_raw(pt, rows, K, xq, xd, xsum, s, t_dev->cus, wf, wn));
 }
 
 // bq_gemm_b / bq_gemm_b_fused: the 8-row GEMV chunks stream the weights once
@@ -393,13 +410,23 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
 constexpr int kGemmBMmqMin = 9;
 }  // namespace
 
-size_t bq_gemm_workspace_bytes(int rows, int K, int n_total) {
-    if (rows <= 0 || K <= 0 || n_total <= 0) return 0;
-    // the largest split any tier / tile height takes for this shape
-    const int ks = std::max(mmq_ksplit(rows, K, n_total, true, (size_t)-1, 128),
-                            mmq_ksplit(rows, K, n_total, true, (size_t)-1, 32));
+size_t bq_gemm_workspace_bytes_cus(int rows, int K, int n_total, int cus) {
+    if (rows <= 0 || K <= 0 || n_total <= 0 || cus <= 0) return 0;
+    // The largest split any tier or tile height takes for this shape: the
+    // caller sizes one workspace per shape before it knows which tier a call
+    // takes (the raw tier, which splits at 128-value stages, can take more
+    // slices than the W144 and Q6_K kernels, which split at 256).
+    const int ks = std::max(mmq_ksplit(rows, K, n_total, true, (size_t)-1, 128, cus),
+                            mmq_ksplit(rows, K, n_total, true, (size_t)-1, 32, cus));
     const size_t split = ks > 1 ? (size_t)ks * rows * n_total * sizeof(float) : 0;
-    return std::max(split, mmq_tail_ws_floats(rows, K, n_total) * sizeof(float));
+    return std::max(split, mmq_tail_ws_floats(rows, K, n_total, cus) * sizeof(float));
+}
+
+size_t bq_gemm_workspace_bytes(int rows, int K, int n_total) {
+    // sized for the current device (0 when there is none: no split is taken
+    // without a workspace, so a call still runs, unsplit)
+    if (ensure_init() != BQ_OK) return 0;
+    return bq_gemm_workspace_bytes_cus(rows, K, n_total, t_dev->cus);
 }
 
 int bq_try_mmq(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
@@ -415,7 +442,7 @@ int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, co
     if (!weight_ok(w) || !y || !xq || !xd || rows < 1) return BQ_EINVAL;
     if (!al16(y) || !al16(xq) || !al16(xd) || !al16(work) || !weight_al16(w)) return BQ_EINVAL;
     if (w->ggml_type != BQ_TYPE_Q6_K || !w->rep || (w->N % 128) != 0) return BQ_UNSUPPORTED;
-    return from_hip(launch_mmq_q6k(one_part(y, w->rep, w->N), rows, w->K, xq, xd, (hipStream_t)st, (float*)work,
+    return from_hip(launch_mmq_q6k(one_part(y, w->rep, w->N), rows, w->K, xq, xd, (hipStream_t)st, t_dev->cus, (float*)work,
                                    work ? work_bytes / sizeof(float) : 0));
 }
 
@@ -467,7 +494,6 @@ constexpr size_t kScratchBytes = 16u << 20;
 constexpr size_t kScratchXdh = 4u << 20;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
-constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices];
 
@@ -515,10 +541,19 @@ int bq_gemm_b_fused_noalloc(float* const* ys, const bq_weight* const* ws, int np
     if (rows == 0) return BQ_OK;
     const int K = ws[0]->K;
     if (K <= 0 || (K % 32) != 0) return BQ_EINVAL;
-    // xdh [rows][K/32] fp16 must fit its region
-    if ((size_t)rows * (size_t)(K / 32) * 2 > kScratchXdh) return BQ_ETOOBIG;
+    // Only the prepacked (W144) tier reads xdh: every part Q5_K with its
+    // repack, K % 512 == 0, N % 128 == 0 and more than 8 rows.  Such a call
+    // needs xdh [rows][K/32] fp16 to fit its region; any other call passes no
+    // xdh and takes the whole scratch as its K-split workspace.
+    bool w144 = rows > BQ_MAX_ROWS && (K % 512) == 0;
+    for (int p = 0; p < nparts && w144; ++p) {
+        const bq_weight* w = ws[p];
+        w144 = w && w->ggml_type == BQ_TYPE_Q5_K && w->rep && w->rep_min && (w->N % 128) == 0;
+    }
+    if (w144 && (size_t)rows * (size_t)(K / 32) * 2 > kScratchXdh) return BQ_ETOOBIG;
     void* base = nullptr;
     if (int r = scratch_ptr(&base)) return r;
+    if (!w144) return bq_gemm_b_fused(ys, ws, nparts, rows, xq, xd, xsum, nullptr, base, kScratchBytes, st);
     uint16_t* xdh = (uint16_t*)base;
     void* work = (uint8_t*)base + kScratchXdh;
     return bq_gemm_b_fused(ys, ws, nparts, rows, xq, xd, xsum, xdh, work, kScratchBytes - kScratchXdh, st);
@@ -701,7 +736,7 @@ int bq_gemv_q8s(float* y, const void* w, const int8_t* xq, const float* xd, int 
     if (!y || !w || !xq || !xd || K <= 0 || N <= 0 || (K % 256) != 0) return BQ_EINVAL;
     if (!al16(w) || !al16(xq) || !al16(xd)) return BQ_EINVAL;
     if (rows < 1 || rows > BQ_MAX_ROWS || K > kQ8SMaxK) return BQ_UNSUPPORTED;
-    return from_hip(launch_gemv_q8s(w, K, N, rows, xq, xd, rs, y, (hipStream_t)st));
+    return from_hip(launch_gemv_q8s(w, K, N, rows, xq, xd, rs, y, (hipStream_t)st, t_dev->cus));
 }
 
 }  // extern "C"

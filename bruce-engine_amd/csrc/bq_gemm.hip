@@ -137,45 +137,65 @@ struct PairOps {
     i32x4 a[NT][2], b[MT][2];  // [nt|mt][group of the pair]
 };
 
+// int32 -> fp32 on the matrix core.  An int8 dot accumulated onto the bit
+// pattern of -1.5 * 2^23 (0xCB400000) is, read as a float, -(12582912 + D)
+// for |D| < 2^22 (a 32-value group: |D| <= 32 * 31 * 127 = 125984): adding D
+// to the bits moves the value by D units of the binade [2^23, 2^24), whose
+// spacing is 1.  One bf16 MFMA whose A and B are the same register r, with
+// r[k] = 2048 for k = 0, 1, 2 (lanes 0-31, elements 0-2) and 0 elsewhere, adds
+// sum_k r[k] * r[k] = 3 * 2^22 = 12582912 and returns -D, exactly (every term
+// is an integer below 2^24).  This replaces the 16 v_cvt_f32_i32 per 32 x 32
+// tile and group with one MFMA, which (unlike an fp32 MFMA) runs alongside
+// VALU work; the epilogue negates the scale.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+struct MfmaCvt {
+    i32x16 bias;
+    bf16x8 r;
+};
+BQ_DEV MfmaCvt mfma_cvt_init(int lane) {
+    MfmaCvt c;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) c.bias[i] = (int)0xCB400000u;
+    const __bf16 v = lane < 32 ? (__bf16)2048.f : (__bf16)0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c.r[i] = i < 3 ? v : (__bf16)0.f;
+    return c;
+}
+// -D as fp32 from the biased int8 dot
+BQ_DEV f32x16 mfma_cvt_neg(const MfmaCvt& c, const i32x16& d) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(c.r, c.r, __builtin_bit_cast(f32x16, d), 0, 0, 0);
+}
+
 // One 128-value stage (two group pairs) of a wave's 2 x 2 tiles of 32 x 32,
-// software pipelined over its eight (group pair, tile) units u: the int8 dots
-// of unit u + 1 are issued before unit u's epilogue (one convert and one FMA
-// per output and group), into the other of two result buffers, so the matrix
-// core computes them while the VALU works on unit u.  Each unit first issues
-// the two-block fp32 outer product of its scales (lanes 0-31: group 2qp,
-// lanes 32-63: group 2qp+1), which the epilogue waits for.  The second pair's
-// operands are read once unit 3's dots (the last to read the first pair's)
-// have been issued, behind unit 2's epilogue.
+// as eight (group pair, tile) units u.  A unit issues its two int8 dots onto
+// the conversion bias, the two-block fp32 outer product of its scales (lanes
+// 0-31: group 2qp, lanes 32-63: group 2qp+1) and the two conversions, then
+// one FMA per output and group.  The two waves per SIMD overlap each other's
+// matrix and VALU work (a software-pipelined form that also issued unit u + 1's
+// dots before unit u's FMAs needs more than the 256 registers two waves per
+// SIMD allow, and spilled).
 //   load_ops(PairOps<2, 2>&, qp)  reads a pair's operands from LDS;
 //   scale(qp, nt, mt, lh) -> float2 {ds, xd} for the lane's group of the pair.
 template <class LoadOps, class Scale>
-BQ_DEV void stage_pipe_2x2(f32x16 (&acc)[2][2], int lh, LoadOps&& load_ops, Scale&& scale) {
+BQ_DEV void stage_units_2x2(f32x16 (&acc)[2][2], int lh, const MfmaCvt& cv, LoadOps&& load_ops, Scale&& scale) {
     PairOps<2, 2> o;
-    load_ops(o, 0);
-    const i32x16 zi = {0};
     const f32x32 zf = {0.f};
-    i32x16 d[2][2];  // [buffer][group of the pair]
-    d[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[0][0], o.b[0][0], zi, 0, 0, 0);
-    d[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[0][1], o.b[0][1], zi, 0, 0, 0);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-        const int qp = u >> 2, nt = (u >> 1) & 1, mt = u & 1, cb = u & 1;
+        const int qp = u >> 2, nt = (u >> 1) & 1, mt = u & 1;
+        if ((u & 3) == 0) load_ops(o, qp);
+        __builtin_amdgcn_sched_barrier(0);
+        const i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[nt][0], o.b[mt][0], cv.bias, 0, 0, 0);
+        const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[nt][1], o.b[mt][1], cv.bias, 0, 0, 0);
         const float2 sv = scale(qp, nt, mt, lh);
         const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(sv.x, sv.y, zf, 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        if (u + 1 < 8) {
-            const int ntn = ((u + 1) >> 1) & 1, mtn = (u + 1) & 1;
-            d[cb ^ 1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[ntn][0], o.b[mtn][0], zi, 0, 0, 0);
-            d[cb ^ 1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[ntn][1], o.b[mtn][1], zi, 0, 0, 0);
-            if (u == 2) load_ops(o, 1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        const f32x16 f0 = mfma_cvt_neg(cv, d0);
+        const f32x16 f1 = mfma_cvt_neg(cv, d1);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            acc[nt][mt][r] = __builtin_fmaf(sc[r], (float)d[cb][0][r], acc[nt][mt][r]);
-            acc[nt][mt][r] = __builtin_fmaf(sc[16 + r], (float)d[cb][1][r], acc[nt][mt][r]);
+            acc[nt][mt][r] = __builtin_fmaf(-sc[r], f0[r], acc[nt][mt][r]);
+            acc[nt][mt][r] = __builtin_fmaf(-sc[16 + r], f1[r], acc[nt][mt][r]);
         }
-        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -408,10 +428,11 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
 //     DMA of stage s+1 runs while stage s is computed, one barrier per stage.
 //   * Per group pair and 32x32 tile: two v_mfma_i32_32x32x32_i8 dots, the
 //     scale products ds[n]*xd[m] of both groups from one two-block fp32
-//     outer-product MFMA, then one convert + one FMA per output and group.
-//     (Measured on gfx950: int8 MFMAs overlap independent VALU work, fp32
-//     MFMAs do not, so the outer product costs VALU time; a one-block-per-group
-//     variant with the MFMAs of the next unit issued ahead was slower.)
+//     outer-product MFMA, then one convert + one FMA per output and group
+//     (the 128-token tile converts on the matrix core instead: mfma_cvt_neg).
+//     (Measured on gfx950: int8 and bf16 MFMAs overlap independent VALU work,
+//     fp32 MFMAs do not, so the outer product costs VALU time; a one-block-
+//     per-group variant with the MFMAs of the next unit issued ahead was slower.)
 // ---------------------------------------------------------------------------
 constexpr int kXS = 128;  // token row stride in LDS (bytes)
 
@@ -424,14 +445,17 @@ struct SmemStage {
 
 // Direct-to-LDS 16-byte load: lane i's 16 bytes from gbase + voff land at
 // LDS address lds + 16 * i.  Issued through asm so that the compiler does not
-// treat LDS reads of the other stage buffer as dependent on it (it would wait
-// for vmcnt(0) before them); the kernel orders the copies itself (vmcnt(0) +
-// barrier before a buffer is read).  An untracked VMEM op can only make the
-// compiler's own vmcnt waits stricter, never looser.  m0 is written here; the compiler
-// warns that it reserves m0 and will not preserve it around the asm, which
-// is safe because on gfx9 no other instruction of these kernels uses m0 (LDS
-// instructions do not; the kernels have no other direct-to-LDS loads or
-// indirect register indexing).
+// treat LDS reads of the other stage buffer, or the min term's global loads,
+// as dependent on it (with __builtin_amdgcn_global_load_lds it waits for
+// vmcnt(0) before them: 9216 x 3072 at M = 512 / 2048 / 8192 took 75 / 202 /
+// 765 us against 66 / 198 / 750 us with this asm); the kernel orders the
+// copies itself (vmcnt(0) + barrier before a buffer is read).  An untracked
+// VMEM op can only make the compiler's own vmcnt waits stricter, never looser.
+// m0 is written here; the compiler warns that it reserves m0 and will not
+// preserve it around the asm, which is safe because no other instruction of
+// these kernels reads or writes m0 (LDS instructions do not on gfx9; the
+// kernels have no other direct-to-LDS loads, s_sendmsg, or relative register
+// indexing).  tests/test_isa_m0.py checks that on the built code object.
 BQ_DEV void dma16(const void* gbase, uint32_t voff, const void* lds) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
@@ -530,35 +554,31 @@ BQ_DEV void mmq144_stage(const SmemStage<TM>& sb, f32x16 (&acc)[TileGeo<TM>::NT]
     }
 }
 
-// The same stage for the 2 x 2 tiles of a 128-token tile's wave, through the
-// software pipeline stage_pipe_2x2.
+// The same stage for the 2 x 2 tiles of a 128-token tile's wave, through
+// stage_units_2x2 (matrix-core conversions; each unit reads its two scales
+// from LDS where it needs them: lane half lh takes group 2qp + lh).
 template <int TM>
-BQ_DEV void mmq144_stage_pipe(const SmemStage<TM>& sb, f32x16 (&acc)[TileGeo<TM>::NT][TileGeo<TM>::MT], int n0,
-                              int t0, int l32, int lh) {
+BQ_DEV void mmq144_stage_units(const SmemStage<TM>& sb, f32x16 (&acc)[TileGeo<TM>::NT][TileGeo<TM>::MT], int n0,
+                               int t0, int l32, int lh, const MfmaCvt& cv) {
     using G = TileGeo<TM>;
     static_assert(G::NT == 2 && G::MT == 2, "four tiles per wave");
-    f32x4 wsq[2], xsq[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) wsq[nt] = *(const f32x4*)(sb.w + (n0 + nt * 32 + l32) * kW144 + 128);
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) xsq[mt] = *(const f32x4*)(sb.xs + 4 * (t0 + mt * 32 + l32));
-    stage_pipe_2x2(
-        acc, lh, [&](PairOps<2, 2>& o, int qp) { mmq144_ops<TM>(o, sb, qp, n0, t0, l32, lh); },
-        [&](int qp, int nt, int mt, int h) {
-            const float w = qp ? (h ? wsq[nt][3] : wsq[nt][2]) : (h ? wsq[nt][1] : wsq[nt][0]);
-            const float x = qp ? (h ? xsq[mt][3] : xsq[mt][2]) : (h ? xsq[mt][1] : xsq[mt][0]);
-            return make_float2(w, x);
+    const float* wsr = (const float*)(sb.w + (n0 + l32) * kW144 + 128) + lh;
+    const float* xsr = sb.xs + 4 * (t0 + l32) + lh;
+    stage_units_2x2(
+        acc, lh, cv, [&](PairOps<2, 2>& o, int qp) { mmq144_ops<TM>(o, sb, qp, n0, t0, l32, lh); },
+        [&](int qp, int nt, int mt, int) {
+            return make_float2(wsr[nt * 32 * (kW144 / 4) + 2 * qp], xsr[mt * 32 * 4 + 2 * qp]);
         });
 }
 
-// The 128-token tile takes the pipelined stage (measured 2-3% faster at
-// M = 512 / 2048 / 8192 on 9216 x 3072); the 32-token tile has one tile per
-// wave and nothing to overlap within it.
+// The 128-token tile takes stage_units_2x2 (with its matrix-core conversions
+// measured 1-2% faster than converts on the VALU at M = 2048 / 8192); the
+// 32-token tile has one tile per wave.
 template <int TM>
 BQ_DEV void mmq144_stage_any(const SmemStage<TM>& sb, f32x16 (&acc)[TileGeo<TM>::NT][TileGeo<TM>::MT], int n0,
-                             int t0, int l32, int lh) {
+                             int t0, int l32, int lh, const MfmaCvt& cv) {
     if constexpr (TileGeo<TM>::NT * TileGeo<TM>::MT == 4)
-        mmq144_stage_pipe<TM>(sb, acc, n0, t0, l32, lh);
+        mmq144_stage_units<TM>(sb, acc, n0, t0, l32, lh, cv);
     else
         mmq144_stage<TM>(sb, acc, n0, t0, l32, lh);
 }
@@ -594,6 +614,7 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
     dof.xd_off = (uint32_t)lane * (uint32_t)(nb * 4);
 
     mmq144_dma<TM>(sm0, wsrc(s0), xq, xd, dof, m0, rows, K, nb, s0, wave, lane);
+    const MfmaCvt cv = mfma_cvt_init(lane);
 
     f32x16 acc[G::NT][G::MT];
 #pragma unroll
@@ -603,26 +624,38 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
     // min term: sum_g f16(Dm[n][g]) * f16(xdh[m][g]) on fp16 MFMA, K/32 % 16 == 0
-    // (the first K slice only)
+    // (the first K slice only).  The operands of up to kMinBatch 16-group
+    // chunks are loaded before the first of their MFMAs, so a tile waits for
+    // one global-load latency per batch instead of one per chunk (the MFMA
+    // order, and so the sum, is the chunk order either way).
     if (kc == 0) {
+        constexpr int kMinBatch = 6;
         const uint16_t* __restrict__ Dm = (const uint16_t*)pt.aux[p];
-        for (int g0 = 0; g0 < nb; g0 += 16) {
-            f16x8 a[G::NT], b[G::MT];
+        for (int g0 = 0; g0 < nb; g0 += 16 * kMinBatch) {
+            f16x8 a[kMinBatch][G::NT], b[kMinBatch][G::MT];
 #pragma unroll
-            for (int nt = 0; nt < G::NT; ++nt) {
-                const int n = nbase + n0 + nt * 32 + l32;
-                a[nt] = *(const f16x8*)(Dm + (size_t)n * nb + g0 + 8 * lh);
+            for (int c = 0; c < kMinBatch; ++c) {
+                const int g = min(g0 + 16 * c, nb - 16);
+#pragma unroll
+                for (int nt = 0; nt < G::NT; ++nt) {
+                    const int n = nbase + n0 + nt * 32 + l32;
+                    a[c][nt] = *(const f16x8*)(Dm + (size_t)n * nb + g + 8 * lh);
+                }
+#pragma unroll
+                for (int mt = 0; mt < G::MT; ++mt) {
+                    const int m = min(m0 + t0 + mt * 32 + l32, rows - 1);
+                    b[c][mt] = *(const f16x8*)(xdh + (size_t)m * nb + g + 8 * lh);
+                }
             }
 #pragma unroll
-            for (int mt = 0; mt < G::MT; ++mt) {
-                const int m = min(m0 + t0 + mt * 32 + l32, rows - 1);
-                b[mt] = *(const f16x8*)(xdh + (size_t)m * nb + g0 + 8 * lh);
+            for (int c = 0; c < kMinBatch; ++c) {
+                if (g0 + 16 * c >= nb) break;
+#pragma unroll
+                for (int nt = 0; nt < G::NT; ++nt)
+#pragma unroll
+                    for (int mt = 0; mt < G::MT; ++mt)
+                        acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c][nt], b[c][mt], acc[nt][mt], 0, 0, 0);
             }
-#pragma unroll
-            for (int nt = 0; nt < G::NT; ++nt)
-#pragma unroll
-                for (int mt = 0; mt < G::MT; ++mt)
-                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[nt], b[mt], acc[nt][mt], 0, 0, 0);
         }
     }
 
@@ -631,13 +664,13 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (s + 1 < s1) mmq144_dma<TM>(sm1, wsrc(s + 1), xq, xd, dof, m0, rows, K, nb, s + 1, wave, lane);
-        mmq144_stage_any<TM>(sm0, acc, n0, t0, l32, lh);
+        mmq144_stage_any<TM>(sm0, acc, n0, t0, l32, lh, cv);
         if (s + 1 >= s1) break;
         BQ_WAIT_VM(0);
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (s + 2 < s1) mmq144_dma<TM>(sm0, wsrc(s + 2), xq, xd, dof, m0, rows, K, nb, s + 2, wave, lane);
-        mmq144_stage_any<TM>(sm1, acc, n0, t0, l32, lh);
+        mmq144_stage_any<TM>(sm1, acc, n0, t0, l32, lh, cv);
     }
 
     // K split: slice kc's partial sums go to part[kc][part p: rows x N[p]];
@@ -902,15 +935,13 @@ static dim3 mmq_grid(int ntm, int ntn) {
 // captured in a graph) and give equal bits.
 constexpr int kMaxKSplit = 8;
 
-// CUs of the device (set by the library's init; MI355X: 256)
-static int g_mmq_cus = 256;
-void mmq_set_cus(int cus) { g_mmq_cus = cus > 0 ? cus : 256; }
-
-int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, int tm) {
+// `cus` below: the CU count of the device the launch runs on (MI355X: 256),
+// which sets the workgroup slots every split and tile-height choice counts.
+int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, int tm, int cus) {
     const int ntiles = ((rows + tm - 1) / tm) * (ntot / kTN);
     if (ntiles <= 0) return 1;
     const int units = stage_units ? (K >> 7) : (K >> 8);
-    const int slots = (tm == 32 ? 3 : 2) * g_mmq_cus;  // workgroups resident at once (3 or 2 per CU)
+    const int slots = (tm == 32 ? 3 : 2) * cus;  // workgroups resident at once (3 or 2 per CU)
     int ks = std::min(kMaxKSplit, std::max(1, slots / ntiles));
     while (ks > 1 && ((size_t)ks * rows * ntot > ws_floats || units < ks)) --ks;
     // the fewest slices with the same longest slice (fewer partial outputs)
@@ -928,7 +959,7 @@ int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, in
 // the 32-token tile (the 128-token tile costs the same at any row count up
 // to 128); at a few hundred to a few thousand rows it depends on how evenly
 // the tiles fill the workgroup slots.
-TailSplit mmq_tail_split(int ntiles, int units, size_t ws_floats, int tm, float e = 1.f);
+TailSplit mmq_tail_split(int ntiles, int units, size_t ws_floats, int tm, float e, int cus);
 constexpr float kTailMinSaving = 192.f;  // see mmq_tail_split
 // the fixed cost of a split launch (its summing launch and partial-tile
 // traffic, about 8 us) in the tile-height estimate's units
@@ -936,21 +967,20 @@ constexpr float kSplitCost = 384.f;
 
 // tail: the kernel takes the leftover-tile split (both Q5_K tiers), so the
 // busiest CU's count is the split one
-int mmq_tile_rows(int rows, int K, int ntot, bool stage_units, size_t ws_floats, float e32, bool tail) {
+int mmq_tile_rows(int rows, int K, int ntot, bool stage_units, size_t ws_floats, float e32, bool tail, int cus) {
     float best = 0.f;
     int pick = 128;
     for (const int tm : {128, 32}) {
-        const int ks = mmq_ksplit(rows, K, ntot, stage_units, ws_floats, tm);
+        const int ks = mmq_ksplit(rows, K, ntot, stage_units, ws_floats, tm, cus);
         const long long ctas = (long long)((rows + tm - 1) / tm) * (ntot / kTN) * ks;
         const int units = stage_units ? K >> 7 : K >> 8;
         const int per = (units + ks - 1) / ks;
-        float load = (float)((ctas + g_mmq_cus - 1) / g_mmq_cus);
+        float load = (float)((ctas + cus - 1) / cus);
         bool split = ks > 1;
         if (tail && ks == 1) {
-            const TailSplit ts = mmq_tail_split((int)ctas, units, ws_floats, tm, tm == 32 ? e32 : 1.f);
+            const TailSplit ts = mmq_tail_split((int)ctas, units, ws_floats, tm, tm == 32 ? e32 : 1.f, cus);
             if (ts.k > 1) {
-                load = (float)(ctas / g_mmq_cus) +
-                       (float)((ts.nleft * ts.k + g_mmq_cus - 1) / g_mmq_cus) / (float)ts.k;
+                load = (float)(ctas / cus) + (float)((ts.nleft * ts.k + cus - 1) / cus) / (float)ts.k;
                 split = true;
             }
         }
@@ -1010,9 +1040,8 @@ static hipError_t sum_splits(const PartTable& pt, int ks, int rows, const float*
 // e, e = the tile height's relative cost per output) on the busiest CU, about
 // half of what the summing launch and the partial tiles cost.
 constexpr int kMaxTailSplit = 4;
-TailSplit mmq_tail_split(int ntiles, int units, size_t ws_floats, int tm, float e) {
+TailSplit mmq_tail_split(int ntiles, int units, size_t ws_floats, int tm, float e, int cus) {
     TailSplit ts;
-    const int cus = g_mmq_cus;
     const int q = ntiles / cus, nleft = ntiles % cus;
     // with one whole tile per CU each runs alone on its CU and the leftover
     // slices lose (512 x 9216 W144, 128-token tiles: 62 -> 67 us)
@@ -1039,13 +1068,13 @@ TailSplit mmq_tail_split(int ntiles, int units, size_t ws_floats, int tm, float 
 // Workspace floats the leftover-tile split of either Q5_K tier can use for
 // this shape (the larger of the two tile heights), at most kTailMaxFloats (32 MiB).
 constexpr size_t kTailMaxFloats = (size_t)8 << 20;
-size_t mmq_tail_ws_floats(int rows, int K, int ntot) {
+size_t mmq_tail_ws_floats(int rows, int K, int ntot, int cus) {
     size_t need = 0;
     for (const int tm : {128, 32}) {
         const int ntiles = ((rows + tm - 1) / tm) * (ntot / kTN);
-        if (mmq_ksplit(rows, K, ntot, false, (size_t)-1, tm) > 1) continue;
+        if (mmq_ksplit(rows, K, ntot, false, (size_t)-1, tm, cus) > 1) continue;
         for (const int units : {K >> 8, K >> 7}) {  // W144 (stage pairs), raw tier (stages)
-            const TailSplit ts = mmq_tail_split(ntiles, units, kTailMaxFloats, tm, tm == 32 ? 1.33f : 1.f);
+            const TailSplit ts = mmq_tail_split(ntiles, units, kTailMaxFloats, tm, tm == 32 ? 1.33f : 1.f, cus);
             if (ts.k > 1) need = std::max(need, (size_t)ts.nleft * ts.k * kTN * tm);
         }
     }
@@ -1071,14 +1100,14 @@ static hipError_t launch_w144_tm(const PartTable& pt, int ntm, int ntn, int ks, 
 }
 
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                              const uint16_t* xdh, hipStream_t st, float* ws, size_t ws_floats) {
-    const int tm = mmq_tile_rows(rows, K, ntotal(pt), false, ws ? ws_floats : 0, 1.115f, true);
+                              const uint16_t* xdh, hipStream_t st, int cus, float* ws, size_t ws_floats) {
+    const int tm = mmq_tile_rows(rows, K, ntotal(pt), false, ws ? ws_floats : 0, 1.115f, true, cus);
     const int ntm = (rows + tm - 1) / tm;
     const int ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, tm);
-    const TailSplit ts =
-        ks > 1 ? TailSplit{} : mmq_tail_split(ntm * ntn, K >> 8, ws ? ws_floats : 0, tm, tm == 32 ? 1.115f : 1.f);
+    const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, tm, cus);
+    const TailSplit ts = ks > 1 ? TailSplit{}
+                                : mmq_tail_split(ntm * ntn, K >> 8, ws ? ws_floats : 0, tm, tm == 32 ? 1.115f : 1.f, cus);
     if (tm == 32) return launch_w144_tm<32>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xdh, st, ws);
     return launch_w144_tm<128>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xdh, st, ws);
 }
@@ -1101,23 +1130,23 @@ static hipError_t launch_raw_tm(const PartTable& pt, int ntm, int ntn, int ks, c
 }
 
 hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                              const int32_t* xsum, hipStream_t st, float* ws, size_t ws_floats) {
-    const int tm = mmq_tile_rows(rows, K, ntotal(pt), true, ws ? ws_floats : 0, 1.33f, true);
+                              const int32_t* xsum, hipStream_t st, int cus, float* ws, size_t ws_floats) {
+    const int tm = mmq_tile_rows(rows, K, ntotal(pt), true, ws ? ws_floats : 0, 1.33f, true, cus);
     const int ntm = (rows + tm - 1) / tm, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    const int ks = mmq_ksplit(rows, K, ntotal(pt), true, ws ? ws_floats : 0, tm);
-    const TailSplit ts =
-        ks > 1 ? TailSplit{} : mmq_tail_split(ntm * ntn, K >> 7, ws ? ws_floats : 0, tm, tm == 32 ? 1.33f : 1.f);
+    const int ks = mmq_ksplit(rows, K, ntotal(pt), true, ws ? ws_floats : 0, tm, cus);
+    const TailSplit ts = ks > 1 ? TailSplit{}
+                                : mmq_tail_split(ntm * ntn, K >> 7, ws ? ws_floats : 0, tm, tm == 32 ? 1.33f : 1.f, cus);
     if (tm == 32) return launch_raw_tm<32>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xsum, st, ws);
     return launch_raw_tm<128>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xsum, st, ws);
 }
 
 hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                          hipStream_t st, float* ws, size_t ws_floats) {
-    const int tm = mmq_tile_rows(rows, K, ntotal(pt), false, ws ? ws_floats : 0, 1.06f, false);
+                          hipStream_t st, int cus, float* ws, size_t ws_floats) {
+    const int tm = mmq_tile_rows(rows, K, ntotal(pt), false, ws ? ws_floats : 0, 1.06f, false, cus);
     const int ntm = (rows + tm - 1) / tm, ntn = ntile_count(pt);
     if (ntm == 0 || ntn == 0) return hipSuccess;
-    const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, tm);
+    const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, tm, cus);
     const dim3 grid(mmq_grid(ntm, ntn).x, ks);
     if (tm == 32)
         launch_kernel(k_mmq_q6k_dma<32>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, ks, ws);

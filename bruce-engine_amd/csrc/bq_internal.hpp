@@ -78,23 +78,24 @@ hipError_t launch_repack_q6k(const void* raw, int K, int N, void* w160, hipStrea
 // prefill GEMMs (128-row weight tiles, int8 MFMA).  ws / ws_floats: the K-split
 // workspace (nullptr: no split); mmq_ksplit gives the split a launch takes
 // (stage_units: the raw tier, which splits at 128-value stages; tm: the
-// token-tile height, 128 or the W144 kernel's 32).
-int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, int tm = 128);
-size_t mmq_tail_ws_floats(int rows, int K, int ntot);  // workspace of the Q5_K leftover-tile split
-void mmq_set_cus(int cus);  // the device's CU count (workgroup slots of the split choice)
+// token-tile height, 128 or the W144 kernel's 32).  cus: the CU count of the
+// device the launch runs on (the workgroup slots every split choice counts).
+int mmq_ksplit(int rows, int K, int ntot, bool stage_units, size_t ws_floats, int tm, int cus);
+size_t mmq_tail_ws_floats(int rows, int K, int ntot, int cus);  // workspace of the Q5_K leftover-tile split
 hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                              const int32_t* xsum, hipStream_t st, float* ws = nullptr, size_t ws_floats = 0);
+                              const int32_t* xsum, hipStream_t st, int cus, float* ws = nullptr,
+                              size_t ws_floats = 0);
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                              const uint16_t* xdh, hipStream_t st, float* ws = nullptr, size_t ws_floats = 0);
+                              const uint16_t* xdh, hipStream_t st, int cus, float* ws = nullptr,
+                              size_t ws_floats = 0);
 hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                          hipStream_t st, float* ws = nullptr, size_t ws_floats = 0);
+                          hipStream_t st, int cus, float* ws = nullptr, size_t ws_floats = 0);
 
 // Q8_0 logits head (Q8S: 8 fp16 scales + 256 int8 per row and 256 values)
 constexpr int kQ8SMaxK = 4096;  // the GEMV keeps K/1024 activation chunks per lane in registers
 hipError_t launch_quant_q8s(const uint16_t* src, int K, int N, uint8_t* dst, hipStream_t st);
-void q8s_set_cus(int cus);
 hipError_t launch_gemv_q8s(const void* W, int K, int N, int rows, const int8_t* xq, const float* xd,
-                           const float* rs, float* y, hipStream_t st);
+                           const float* rs, float* y, hipStream_t st, int cus);
 
 // q8 producers: elementwise op -> L2 norm -> q8 (op: 0 norm, 1 add, 2 resid,
 // 3 gate, 4 silu*mul); n % 32 == 0, n <= kNormMaxN

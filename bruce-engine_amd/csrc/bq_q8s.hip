@@ -148,11 +148,9 @@ hipError_t launch_quant_q8s(const uint16_t* src, int K, int N, uint8_t* dst, hip
 }
 
 namespace {
-int g_cus = 256;
-
 template <int M, int CPL>
 hipError_t launch_q8s_mc(const uint8_t* W, int K, int N, const int8_t* xq, const float* xd, const float* rs,
-                         float* y, hipStream_t st) {
+                         float* y, hipStream_t st, int cus) {
     // rows per wave iteration: enough 16-byte loads in flight per wave while
     // the activation registers (M*CPL*5 VGPRs) grow with M.  At 7..8 rows the
     // occupancy is 3 waves/SIMD either way and two rows per wave keep more
@@ -171,38 +169,36 @@ hipError_t launch_q8s_mc(const uint8_t* W, int K, int N, const int8_t* xq, const
         per_cu = n;
     }
     const long long want = ((long long)N + 4 * R - 1) / (4 * R);
-    const int blocks = (int)std::min<long long>(want, (long long)g_cus * per_cu);
+    const int blocks = (int)std::min<long long>(want, (long long)cus * per_cu);
     launch_kernel((k_gemv_q8s<M, R, CPL>), dim3(blocks), dim3(256), 0, st, W, K, N, xq, xd, rs, y);
     return hipGetLastError();
 }
 
 template <int M>
 hipError_t launch_q8s_m(int cpl, const uint8_t* W, int K, int N, const int8_t* xq, const float* xd,
-                        const float* rs, float* y, hipStream_t st) {
+                        const float* rs, float* y, hipStream_t st, int cus) {
     switch (cpl) {
-        case 1: return launch_q8s_mc<M, 1>(W, K, N, xq, xd, rs, y, st);
-        case 2: return launch_q8s_mc<M, 2>(W, K, N, xq, xd, rs, y, st);
-        case 3: return launch_q8s_mc<M, 3>(W, K, N, xq, xd, rs, y, st);
-        default: return launch_q8s_mc<M, 4>(W, K, N, xq, xd, rs, y, st);
+        case 1: return launch_q8s_mc<M, 1>(W, K, N, xq, xd, rs, y, st, cus);
+        case 2: return launch_q8s_mc<M, 2>(W, K, N, xq, xd, rs, y, st, cus);
+        case 3: return launch_q8s_mc<M, 3>(W, K, N, xq, xd, rs, y, st, cus);
+        default: return launch_q8s_mc<M, 4>(W, K, N, xq, xd, rs, y, st, cus);
     }
 }
 }  // namespace
 
-void q8s_set_cus(int cus) { g_cus = cus > 0 ? cus : 256; }
-
 hipError_t launch_gemv_q8s(const void* W, int K, int N, int rows, const int8_t* xq, const float* xd,
-                           const float* rs, float* y, hipStream_t st) {
+                           const float* rs, float* y, hipStream_t st, int cus) {
     const int cpl = (K / 16 + 63) / 64;
     const uint8_t* w = (const uint8_t*)W;
     switch (rows) {
-        case 1: return launch_q8s_m<1>(cpl, w, K, N, xq, xd, rs, y, st);
-        case 2: return launch_q8s_m<2>(cpl, w, K, N, xq, xd, rs, y, st);
-        case 3: return launch_q8s_m<3>(cpl, w, K, N, xq, xd, rs, y, st);
-        case 4: return launch_q8s_m<4>(cpl, w, K, N, xq, xd, rs, y, st);
-        case 5: return launch_q8s_m<5>(cpl, w, K, N, xq, xd, rs, y, st);
-        case 6: return launch_q8s_m<6>(cpl, w, K, N, xq, xd, rs, y, st);
-        case 7: return launch_q8s_m<7>(cpl, w, K, N, xq, xd, rs, y, st);
-        default: return launch_q8s_m<8>(cpl, w, K, N, xq, xd, rs, y, st);
+        case 1: return launch_q8s_m<1>(cpl, w, K, N, xq, xd, rs, y, st, cus);
+        case 2: return launch_q8s_m<2>(cpl, w, K, N, xq, xd, rs, y, st, cus);
+        case 3: return launch_q8s_m<3>(cpl, w, K, N, xq, xd, rs, y, st, cus);
+        case 4: return launch_q8s_m<4>(cpl, w, K, N, xq, xd, rs, y, st, cus);
+        case 5: return launch_q8s_m<5>(cpl, w, K, N, xq, xd, rs, y, st, cus);
+        case 6: return launch_q8s_m<6>(cpl, w, K, N, xq, xd, rs, y, st, cus);
+        case 7: return launch_q8s_m<7>(cpl, w, K, N, xq, xd, rs, y, st, cus);
+        default: return launch_q8s_m<8>(cpl, w, K, N, xq, xd, rs, y, st, cus);
     }
 }
 

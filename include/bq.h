@@ -199,11 +199,18 @@ int bq_gemv_norm_fused(float* const* ys, const bq_weight* const* ws, int nparts,
  * paths and give equal bits.  work = NULL (or too small) means a smaller or no
  * split.  bq_gemm_workspace_bytes gives the size that allows the full split of
  * a launch of `rows` activation rows over matrices of n_total = sum N_p rows
- * (0: that launch never splits); it is at most 32 MiB for any shape.  work
- * must be 16-byte aligned.  Calls that share a workspace must be ordered
- * (one stream, or events): the workspace holds one call's partials at a time.
- * No counterpart in the reference (its 128x128 GEMM never splits K). */
+ * (0: that launch never splits); on 256 CUs it is at most 32 MiB for any
+ * shape (in general at most the larger of 32 MiB and CUs x 128 KiB).  The
+ * size is the largest any tier (W144, raw Q5_K, Q6_K) takes for the shape, so
+ * one workspace serves every call of that shape.  The split counts the
+ * workgroup slots of the device, so the size is for the current device (0
+ * when there is none); bq_gemm_workspace_bytes_cus gives it for a device of
+ * `cus` compute units (MI355X: 256).  work must be 16-byte aligned.  Calls
+ * that share a workspace must be ordered (one stream, or events): the
+ * workspace holds one call's partials at a time.  No counterpart in the
+ * reference (its 128x128 GEMM never splits K). */
 size_t bq_gemm_workspace_bytes(int rows, int K, int n_total);
+size_t bq_gemm_workspace_bytes_cus(int rows, int K, int n_total, int cus);
 
 /* Y_p[M][N_p] for nparts (1..4) Q5_K matrices, 128x128 tiles on int8 MFMA.
  * Replaces try_launch_mmq (bruce.cu:7366-7419).  rows >= 96 (the reference's
@@ -244,10 +251,13 @@ int bq_gemm_b_fused(float* const* ys, const bq_weight* const* ws, int nparts, in
  * rows and the K-split workspace live in a 16 MiB static device array of the
  * library (4 MiB for xdh, 12 MiB of workspace), which each GPU the library
  * runs on holds until the process ends; the caller passes only inputs and
- * outputs.  Results equal bq_gemm_b_fused given its own xdh and a 12 MiB
- * workspace, bit for bit.  rows * (K/32) * 2 > 4 MiB returns BQ_ETOOBIG
- * (nothing enqueued).  Every call on one GPU shares that GPU's array and it
- * keeps the last call's contents (nothing in it needs clearing: each call
+ * outputs.  A call that takes the W144 tier (every part Q5_K with
+ * rep/rep_min, K % 512 == 0, N_p % 128 == 0, rows > 8) needs
+ * rows * (K/32) * 2 <= 4 MiB of xdh, else BQ_ETOOBIG (nothing enqueued), and
+ * equals bq_gemm_b_fused given its own xdh and a 12 MiB workspace, bit for
+ * bit; any other call uses no xdh and the whole 16 MiB as its workspace, and
+ * equals bq_gemm_b_fused given a 16 MiB workspace.  Every call on one GPU
+ * shares that GPU's array and it keeps the last call's contents (nothing in it needs clearing: each call
  * writes what it reads): calls that overlap on one GPU (other streams, other
  * host threads, graphs replayed concurrently) race, so order them. */
 int bq_gemm_b_fused_noalloc(float* const* ys, const bq_weight* const* ws, int nparts, int rows,
@@ -275,9 +285,11 @@ size_t bq_q8s_bytes(int K, int N);            /* N*(K/256)*272 */
 /* BF16 [N][K] (bit patterns) -> Q8S on the device.  Replaces k_bf16_to_q8
  * (bruce.cu:5159-5184).  Per 32 values d = amax*(1/127), id = d>0 ? 1/d : 0,
  * q = clamp(rint(v*id), -127, 127), scale = half_rn(d).  Bit-exact with the
- * reference for finite inputs (a group with 0 < amax < 127/FLT_MAX has
- * id = inf and saturates to +-127, as __float2int_rn does; the reference's host
- * loop leaves that case to lrintf(inf)).  bf16 and dst 16-byte aligned. */
+ * reference for finite inputs.  A group with 0 < amax < 127/FLT_MAX has
+ * id = inf: its zero values (0 * inf = NaN) give code 0 and its other values
+ * +-127, as __float2int_rn does on the device; the reference's host loop
+ * leaves that case to lrintf(inf), which differs.  bf16 and dst 16-byte
+ * aligned. */
 int bq_quantize_q8s(const uint16_t* bf16, int K, int N, void* dst, bq_stream_t st);
 /* Host version: q8k_quant_host (bruce.cu:4843-4867), same bytes. */
 int bq_quantize_q8s_host(const uint16_t* bf16, int K, int N, void* dst);

@@ -87,20 +87,45 @@ def test_q8s_sizes_and_rejects():
     assert L.bq_quantize_q8s_host(None, 256, 1, buf) == bq.BQ_EINVAL
 
 
+def _has_gpu():
+    import torch
+    return torch.cuda.is_available()
+
+
 def test_workspace_bytes():
-    """bq_gemm_workspace_bytes (host arithmetic only): the K-split workspace
-    of the prefill GEMMs, at most 32 MiB for any shape."""
+    """bq_gemm_workspace_bytes_cus (host arithmetic only): the K-split
+    workspace of the prefill GEMMs for a device of `cus` CUs, at most 32 MiB
+    for any shape; bq_gemm_workspace_bytes sizes it for the current device,
+    and without one (this CPU run) it is 0."""
     import bq
     L = bq.load()
-    # one token tile of a 9216-row matrix: 72 tiles -> 7 slices for the 512
-    # slots, evened to 6 over the raw tier's 24 stages (4 each); the 32-token
-    # tile (144 tiles, 768 slots) takes 5: the larger is reserved
-    assert L.bq_gemm_workspace_bytes(64, 3072, 9216) == 6 * 64 * 9216 * 4
+    W = L.bq_gemm_workspace_bytes_cus
+    # one token tile of a 9216-row matrix on 256 CUs: 72 tiles -> 7 slices for
+    # the 512 slots, evened to 6 over the raw tier's 24 stages (4 each); the
+    # 32-token tile (144 tiles, 768 slots) takes 5: the larger is reserved
+    assert W(64, 3072, 9216, 256) == 6 * 64 * 9216 * 4
     # 1152 tiles = 4 x 256 + 128 leftover tiles: the W144 tier cuts each
     # leftover tile into 2 K slices of 128 x 128 fp32 partial tiles
-    assert L.bq_gemm_workspace_bytes(2048, 3072, 9216) == 128 * 2 * 128 * 128 * 4
-    assert L.bq_gemm_workspace_bytes(4096, 3072, 9216) == 0      # 2304 tiles = 9 x 256: no leftover
-    assert L.bq_gemm_workspace_bytes(0, 3072, 9216) == 0
-    worst = max(L.bq_gemm_workspace_bytes(r, 3072, n) for r in list(range(1, 600, 7)) + list(range(600, 9000, 97))
-                for n in (128, 1024, 9216, 36864))
-    assert worst <= 32 << 20
+    assert W(2048, 3072, 9216, 256) == 128 * 2 * 128 * 128 * 4
+    assert W(4096, 3072, 9216, 256) == 0      # 2304 tiles = 9 x 256: no leftover
+    assert W(0, 3072, 9216, 256) == 0
+    assert W(64, 3072, 9216, 0) == 0
+    # the split follows the CU count.  On 304 CUs the 128-token tile's 1152
+    # tiles are 3 x 304 + 240 and no leftover split beats 4 rounds by half a
+    # tile; the 32-token tile's 4608 are 15 x 304 + 48, whose 48 leftover tiles
+    # take 4 K slices of 128 x 32 partials each
+    assert W(2048, 3072, 9216, 304) == 48 * 4 * 128 * 32 * 4
+    # 80 CUs: 72 tiles fill 160 slots twice over at most -> 2 slices, evened
+    # over 24 stages (12 each)
+    assert W(64, 3072, 9216, 80) == 2 * 64 * 9216 * 4
+    # at most 32 MiB on 256 CUs; in general the uniform split fills the
+    # device's slots with 128 x 128 fp32 partial tiles (CUs x 128 KiB) and the
+    # leftover split is capped at 32 MiB
+    for c in (80, 256, 304):
+        worst = max(W(r, 3072, n, c) for r in list(range(1, 600, 7)) + list(range(600, 9000, 97))
+                    for n in (128, 1024, 9216, 36864))
+        assert worst <= max(32 << 20, c * (128 << 10)), c
+        if c == 256:
+            assert worst <= 32 << 20
+    if not _has_gpu():
+        assert L.bq_gemm_workspace_bytes(64, 3072, 9216) == 0
