@@ -178,3 +178,14 @@ def test_w144_leftover_split_graph_capture(bq, oracle):
         torch.cuda.synchronize()
         assert np.array_equal(host(y).view(np.uint32), eager.view(np.uint32)), rep
     del graph
+
+
+def test_workspace_bytes_follow_the_device(bq):
+    """bq_gemm_workspace_bytes sizes the split for the current device: it
+    equals bq_gemm_workspace_bytes_cus at the device's CU count."""
+    import torch
+    L = bq.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for rows, n in ((64, 9216), (2048, 9216), (600, 18432), (16, 3072), (4096, 9216)):
+        assert L.bq_gemm_workspace_bytes(rows, 3072, n) == L.bq_gemm_workspace_bytes_cus(rows, 3072, n, cus), \
+            (rows, n, cus)
