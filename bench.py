@@ -193,15 +193,16 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
     # library's captured decode step (bq_decode_graph_*, one graph per token)
     g = torch.Generator(device="cuda").manual_seed(SEED + 15)
     vec = lambda n: torch.rand(n, generator=g, device="cuda") * 0.5 + 0.25
-    fb = {"x": torch.randn(K, generator=g, device="cuda"), "aout": torch.randn(KO, generator=g, device="cuda"),
-          "qkv": torch.empty(NQKV, device="cuda"), "proj": torch.empty(K, device="cuda"),
-          "fg": torch.empty(FF, device="cuda"), "fu": torch.empty(FF, device="cuda"),
-          "logits": torch.empty(VOCAB, device="cuda"), "alpha": vec(K), "alpha2": vec(K), "sgate": vec(KO),
+    R = 8   # buffers for up to 8 token rows (the verify steps)
+    fb = {"x": torch.randn((R, K), generator=g, device="cuda"), "aout": torch.randn((R, KO), generator=g, device="cuda"),
+          "qkv": torch.empty((R, NQKV), device="cuda"), "proj": torch.empty((R, K), device="cuda"),
+          "fg": torch.empty((R, FF), device="cuda"), "fu": torch.empty((R, FF), device="cuda"),
+          "logits": torch.empty((R, VOCAB), device="cuda"), "alpha": vec(K), "alpha2": vec(K), "sgate": vec(KO),
           "sg": vec(FF), "su": vec(FF)}
-    qb = [torch.empty(FF, dtype=torch.int8, device="cuda"), torch.empty(FF // 32, device="cuda"),
-          torch.empty(FF // 32, dtype=torch.int32, device="cuda")]
-    xq0, xd0, xs0 = bq.quantize_q8(fb["x"].view(1, K))
-    qb[0][:K].copy_(xq0.view(-1)); qb[1][:K // 32].copy_(xd0.view(-1)); qb[2][:K // 32].copy_(xs0.view(-1))
+    qb = [torch.empty(R * FF, dtype=torch.int8, device="cuda"), torch.empty(R * FF // 32, device="cuda"),
+          torch.empty(R * FF // 32, dtype=torch.int32, device="cuda")]
+    xq0, xd0, xs0 = bq.quantize_q8(fb["x"])
+    qb[0][:R * K].copy_(xq0.view(-1)); qb[1][:R * K // 32].copy_(xd0.view(-1)); qb[2][:R * K // 32].copy_(xs0.view(-1))
     qout = (ctypes.c_void_p * 1)(fb["qkv"].data_ptr())
     blocks = (bq.DecodeBlock * (2 * LAYERS))()
     for l in range(LAYERS):
@@ -215,9 +216,11 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
         f.s_gate, f.s_up, f.n_ff = fb["sg"].data_ptr(), fb["su"].data_ptr(), FF
     blocks[2 * LAYERS - 1].norm_after = 1
     chain = {}
-    for fold in (0, 1):
+    # (rows, fold): the one-token step unfolded and folded, and the verify
+    # steps over 2 / 4 / 8 token rows (one graph per row count)
+    for rows, fold in ((1, 0), (1, 1), (2, 0), (4, 0), (8, 0)):
         stp = bq.DecodeStep()
-        stp.n_blocks, stp.blocks, stp.n_embd, stp.fold = 2 * LAYERS, blocks, K, fold
+        stp.n_blocks, stp.blocks, stp.n_embd, stp.fold, stp.rows = 2 * LAYERS, blocks, K, fold, rows
         stp.x, stp.xq, stp.xd, stp.xsum = fb["x"].data_ptr(), qb[0].data_ptr(), qb[1].data_ptr(), qb[2].data_ptr()
         stp.proj, stp.ffn_g, stp.ffn_u = fb["proj"].data_ptr(), fb["fg"].data_ptr(), fb["fu"].data_ptr()
         stp.head, stp.logits = ctypes.pointer(lmw), fb["logits"].data_ptr()
@@ -231,9 +234,11 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
             dg.launch()
         e1.record()
         torch.cuda.synchronize()
-        chain[fold] = e0.elapsed_time(e1) / steps
+        chain[(rows, fold)] = e0.elapsed_time(e1) / steps
         dg.close()
-    chain_ms, folded_ms = chain[0], chain[1]
+    chain_ms, folded_ms = chain[(1, 0)], chain[(1, 1)]
+    verify = {f"rows{r}": {"ms_per_step": round(chain[(r, 0)], 4), "ms_per_token": round(chain[(r, 0)] / r, 4),
+                           "step_vs_one_row": round(chain[(r, 0)] / chain_ms, 3)} for r in (2, 4, 8)}
     del fb, qb
     wbytes = LAYERS * sum(a.nbytes for a in (w_qkv, w_o, w_gate, w_up, w_down)) + lm.numel()
     act = LAYERS * (2 * (4 * K + q8_bytes(1, K)) + (4 * KO + q8_bytes(1, KO)) + (4 * FF + q8_bytes(1, FF))) \
@@ -256,7 +261,12 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
                                             "silu*mul in the gate+up epilogue (bq_gate_up_silu) and its norm -> q8 "
                                             "inside the down GEMV (bq_gemv_norm_fused)",
                                     "ms_per_token": round(folded_ms, 4), "GBps": round(gbs(tot, folded_ms), 1),
-                                    "launches_per_token": 6 * LAYERS + 2}}
+                                    "launches_per_token": 6 * LAYERS + 2},
+            "decode_chain_verify": {"what": "the same step (fold = 0) over 2 / 4 / 8 token rows, the speculative-"
+                                            "verify step with every row's logits (forward_batch_impl with "
+                                            "all_logits, bruce.cu:7610-7843; one captured graph per row count as "
+                                            "capture_verify_graphs, :7877-7900); ms_per_token = step / rows",
+                                    **verify}}
 
 
 def q8s_head(B, bq, torch, sp, ptr, steps=50):

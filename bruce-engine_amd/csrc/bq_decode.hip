@@ -3,10 +3,13 @@
 //
 // Mirrors the reference's forward_launch (engine/src/bruce.cu:7902-8037), the
 // per-block launch sequence of one decoded token, and capture_graph
-// (:8046-8055) / the graph replay of bruce_decode_step (:8246-8252).  The
-// reference's attention kernels (:7940-7970) are outside this library: a
-// caller hook enqueues them between the QKV projection and the gate norm, so
-// they land in the same graph.
+// (:8046-8055) / the graph replay of bruce_decode_step (:8246-8252); with
+// rows 2..8 its speculative-verify form, forward_batch_impl over `rows` tokens
+// with all logits (:7610-7843), captured once per row count as
+// capture_verify_graphs does (:7877-7900) and replayed by verify_launch
+// (:7862-7875).  The reference's attention kernels (:7940-7970, :7716-7737)
+// are outside this library: a caller hook enqueues them between the QKV
+// projection and the gate norm, so they land in the same graph.
 #include <string.h>
 
 #include "../../include/bq.h"
@@ -16,11 +19,23 @@ namespace {
 
 bool dims_ok(const bq_decode_step* s) {
     return s && s->n_blocks >= 0 && (s->n_blocks == 0 || s->blocks) && s->x && s->xq && s->xd && s->xsum &&
-           s->proj && s->n_embd > 0 && (s->n_embd % 32) == 0;
+           s->proj && s->n_embd > 0 && (s->n_embd % 32) == 0 && s->rows >= 0 && s->rows <= BQ_MAX_ROWS;
 }
 
-// one attention block: bruce.cu:7915-7993 (QKV, attention, gate norm, O)
-int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, bq_stream_t st) {
+// tokens per step: 0 means 1
+int rows_of(const bq_decode_step* s) { return s->rows > 0 ? s->rows : 1; }
+
+// y [rows][N] of a k-quant weight over the q8 rows: the single-row GEMV at one
+// row (launch_gemv, :7982 / :8008), the multi-row kernels through the
+// prompt-batch dispatcher at 2..8 (launch_gemm_b, :7750 / :7800)
+int gemv_rows_of(float* y, const bq_weight* w, int rows, const bq_decode_step* s, bq_stream_t st) {
+    if (rows == 1) return bq_gemv(y, w, s->xq, s->xd, s->xsum, st);
+    return bq_gemm_b(y, w, rows, s->xq, s->xd, s->xsum, nullptr, nullptr, 0, st);
+}
+
+// one attention block: bruce.cu:7915-7993 (QKV, attention, gate norm, O);
+// rows 2..8: :7636-7757
+int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, int rows, bq_stream_t st) {
     if (b.n_qkv < 1 || b.n_qkv > BQ_MAX_PARTS || !b.qkv || !b.qkv_out || !b.o || !b.attn_out || !b.attn_gate ||
         !b.sgate || b.n_attn <= 0 || (b.n_attn % 32) != 0)
         return BQ_EINVAL;
@@ -36,31 +51,34 @@ int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, bq_str
             yp[nf++] = b.qkv_out[p];
         }
     if (nf > 0) {
-        const int r = bq_verify_fused(yp, wp, nf, 1, s->xq, s->xd, s->xsum, 0, st);
+        const int r = bq_verify_fused(yp, wp, nf, rows, s->xq, s->xd, s->xsum, 0, st);
         if (r != BQ_OK && r != BQ_UNSUPPORTED) return r;
         if (r == BQ_UNSUPPORTED)
             for (int p = 0; p < nf; ++p)
-                if (int e = bq_gemv(yp[p], wp[p], s->xq, s->xd, s->xsum, st)) return e;
+                if (int e = gemv_rows_of(yp[p], wp[p], rows, s, st)) return e;
     }
     for (int p = 0; p < b.n_qkv; ++p)
         if (b.qkv[p].ggml_type != BQ_TYPE_Q5_K)
-            if (int e = bq_gemv(b.qkv_out[p], &b.qkv[p], s->xq, s->xd, s->xsum, st)) return e;
+            if (int e = gemv_rows_of(b.qkv_out[p], &b.qkv[p], rows, s, st)) return e;
     if (s->attention) s->attention(s->user, bi, st);
-    // gate norm -> q8, then O (k_gate_norm :7975-7978, launch_gemv :7982);
-    // folded: the gate norm runs inside the O GEMV (bq_gemv_norm_fused)
+    // gate norm -> q8, then O (k_gate_norm :7975-7978, launch_gemv :7982;
+    // rows: k_gate_norm_vec4 :7740, launch_gemm_b :7757); folded: the gate
+    // norm runs inside the O GEMV (bq_gemv_norm_fused, one row)
     if (s->fold) {
         float* yo[1] = {s->proj};
         const bq_weight* po[1] = {b.o};
         return bq_gemv_norm_fused(yo, po, 1, BQ_OP_GATE, nullptr, b.attn_out, b.attn_gate, b.sgate, nullptr,
                                   nullptr, nullptr, nullptr, st);
     }
-    if (int e = bq_gate_norm_q8(nullptr, b.attn_out, b.attn_gate, b.sgate, 1, b.n_attn, s->xq, s->xd, s->xsum, st))
+    if (int e = bq_gate_norm_q8(nullptr, b.attn_out, b.attn_gate, b.sgate, rows, b.n_attn, s->xq, s->xd, s->xsum,
+                                st))
         return e;
-    return bq_gemv(s->proj, b.o, s->xq, s->xd, s->xsum, st);
+    return gemv_rows_of(s->proj, b.o, rows, s, st);
 }
 
-// one FFN block: bruce.cu:7994-8012 (gate+up, silu*mul norm, down)
-int ffn_block(const bq_decode_step* s, const bq_decode_block& b, bq_stream_t st) {
+// one FFN block: bruce.cu:7994-8012 (gate+up, silu*mul norm, down); rows
+// 2..8: :7759-7800
+int ffn_block(const bq_decode_step* s, const bq_decode_block& b, int rows, bq_stream_t st) {
     if (!b.gate || !b.up || !b.down || !b.s_gate || !b.s_up || !s->ffn_g || b.n_ff <= 0 || (b.n_ff % 32) != 0)
         return BQ_EINVAL;
     if (s->fold) {
@@ -74,16 +92,16 @@ int ffn_block(const bq_decode_step* s, const bq_decode_block& b, bq_stream_t st)
     if (!s->ffn_u) return BQ_EINVAL;
     float* y2[2] = {s->ffn_g, s->ffn_u};
     const bq_weight* p2[2] = {b.gate, b.up};
-    int r = bq_verify_fused(y2, p2, 2, 1, s->xq, s->xd, s->xsum, 0, st);
+    int r = bq_verify_fused(y2, p2, 2, rows, s->xq, s->xd, s->xsum, 0, st);
     if (r == BQ_UNSUPPORTED) {
-        if ((r = bq_gemv(s->ffn_g, b.gate, s->xq, s->xd, s->xsum, st))) return r;
-        r = bq_gemv(s->ffn_u, b.up, s->xq, s->xd, s->xsum, st);
+        if ((r = gemv_rows_of(s->ffn_g, b.gate, rows, s, st))) return r;
+        r = gemv_rows_of(s->ffn_u, b.up, rows, s, st);
     }
     if (r) return r;
-    if (int e = bq_silu_mul_norm_q8(nullptr, s->ffn_g, s->ffn_u, b.s_gate, b.s_up, 1, b.n_ff, s->xq, s->xd,
+    if (int e = bq_silu_mul_norm_q8(nullptr, s->ffn_g, s->ffn_u, b.s_gate, b.s_up, rows, b.n_ff, s->xq, s->xd,
                                     s->xsum, st))
         return e;
-    return bq_gemv(s->proj, b.down, s->xq, s->xd, s->xsum, st);
+    return gemv_rows_of(s->proj, b.down, rows, s, st);
 }
 
 }  // namespace
@@ -97,33 +115,35 @@ extern "C" {
 int bq_decode_enqueue(const bq_decode_step* s, bq_stream_t st) {
     if (int r = bq_init()) return r;
     if (!dims_ok(s)) return BQ_EINVAL;
-    const int n = s->n_embd;
+    const int n = s->n_embd, rows = rows_of(s);
+    // the folded producers are one-row GEMV epilogues / prologues
+    if (s->fold && rows > 1) return BQ_UNSUPPORTED;
     for (int i = 0; i < s->n_blocks; ++i) {
         const bq_decode_block& b = s->blocks[i];
-        // loop start: x = norm(x + input_h) (k_add_norm, :7914)
+        // loop start: x = norm(x + input_h) (k_add_norm, :7914; rows: k_add_norm_rows :7633)
         if (b.norm_before) {
             if (!s->input_h) return BQ_EINVAL;
-            if (int e = bq_add_norm_q8(s->x, s->input_h, 1, n, s->xq, s->xd, s->xsum, st)) return e;
+            if (int e = bq_add_norm_q8(s->x, s->input_h, rows, n, s->xq, s->xd, s->xsum, st)) return e;
         }
-        const int r = b.kind == BQ_BLOCK_FFN ? ffn_block(s, b, st) : b.kind == BQ_BLOCK_ATTN
-                                                                       ? attn_block(s, b, i, st)
-                                                                       : BQ_EINVAL;
+        const int r = b.kind == BQ_BLOCK_FFN ? ffn_block(s, b, rows, st) : b.kind == BQ_BLOCK_ATTN
+                                                                             ? attn_block(s, b, i, rows, st)
+                                                                             : BQ_EINVAL;
         if (r) return r;
-        // x = resid(x, proj, alpha) -> q8 x (k_resid_vec4, :8017)
+        // x = resid(x, proj, alpha) -> q8 x (k_resid_vec4, :8017; rows: :7803-7815)
         if (!b.alpha) return BQ_EINVAL;
-        if (int e = bq_resid_q8(s->x, s->proj, b.alpha, 1, n, s->xq, s->xd, s->xsum, st)) return e;
-        // loop end: x = norm(x) (k_norm, :8022)
+        if (int e = bq_resid_q8(s->x, s->proj, b.alpha, rows, n, s->xq, s->xd, s->xsum, st)) return e;
+        // loop end: x = norm(x) (k_norm, :8022; rows: k_norm_rows :7818)
         if (b.norm_after)
-            if (int e = bq_norm_q8(s->x, s->x, 1, n, s->xq, s->xd, s->xsum, st)) return e;
+            if (int e = bq_norm_q8(s->x, s->x, rows, n, s->xq, s->xd, s->xsum, st)) return e;
     }
-    // logits from the last q8 row of x (:8026-8032)
+    // logits of every row from the q8 rows of x (:8026-8032; rows: launch_logits_b :7832)
     if (s->head_q8s) {
         if (!s->logits) return BQ_EINVAL;
-        return bq_gemv_q8s(s->logits, s->head_q8s, s->xq, s->xd, n, s->vocab, 1, s->head_rs, st);
+        return bq_gemv_q8s(s->logits, s->head_q8s, s->xq, s->xd, n, s->vocab, rows, s->head_rs, st);
     }
     if (s->head) {
         if (!s->logits) return BQ_EINVAL;
-        return bq_gemv(s->logits, s->head, s->xq, s->xd, s->xsum, st);
+        return gemv_rows_of(s->logits, s->head, rows, s, st);
     }
     return BQ_OK;
 }

@@ -349,25 +349,32 @@ int bq_gguf_load(bq_gguf* g, int64_t i, void* raw, void* rep, void* rep_min, bq_
  * The per-token decode launch sequence of the reference's forward_launch
  * (bruce.cu:7902-8037) over a caller's block list, eagerly or as one captured
  * HIP graph (capture_graph :8046-8055, replayed per token as bruce_decode_step
- * does, :8246-8252).  Per block, in the reference's order:
+ * does, :8246-8252).  With rows = 2..8 it is the speculative-verify step over
+ * `rows` tokens with every row's logits (forward_batch_impl :7610-7843 with
+ * all_logits), captured once per row count as capture_verify_graphs does
+ * (:7877-7900) and replayed by verify_launch (:7862-7875); the argmax that
+ * follows there is the caller's.  Per block, in the reference's order:
  *   norm_before: x = norm(x + input_h) -> q8                      (k_add_norm :7914)
- *   attention block: QKV GEMV over the q8 row (bq_verify_fused over the Q5_K
- *     parts, bq_gemv for others), the caller's attention hook, gate norm of
- *     attn_out by attn_gate -> q8, O GEMV -> proj                   (:7915-7993)
+ *   attention block: QKV GEMV over the q8 rows (bq_verify_fused over the Q5_K
+ *     parts, single-row / multi-row GEMVs for others), the caller's attention
+ *     hook, gate norm of attn_out by attn_gate -> q8, O GEMV -> proj (:7915-7993)
  *   FFN block: gate+up GEMV, silu*mul norm -> q8, down GEMV -> proj (:7994-8012)
  *   x = resid(x, proj, alpha) -> q8                               (k_resid :8017)
  *   norm_after: x = norm(x) -> q8                                 (k_norm :8022)
- * then the logits from the last q8 row: the Q8_0 head (head_q8s, bq_gemv_q8s
- * with head_rs) or a k-quant head (head, bq_gemv)                  (:8026-8032).
- * fold = 1 runs the gate norm inside the O GEMV and the silu*mul inside the
- * gate+up epilogue with its norm inside the down GEMV (bq_gemv_norm_fused,
- * bq_gate_up_silu; 2 launches fewer per block pair, outputs equal to rounding).
- * The attention kernels are the caller's: `attention(user, block, st)` must
- * enqueue them on st (and only there) and write attn_out; NULL leaves attn_out
- * as it is.  Scratch (caller-owned): xq/xd/xsum hold one q8 row of
- * max(n_embd, n_attn, n_ff) values, proj [n_embd], ffn_g and ffn_u [n_ff]
- * (ffn_u unused when fold = 1).  x is updated in place.  A graph captures the
- * pointers it is created with: replays read and write the same buffers. */
+ * then the logits of every row: the Q8_0 head (head_q8s, bq_gemv_q8s with
+ * head_rs) or a k-quant head (head)                                (:8026-8032).
+ * fold = 1 (rows = 1 only; BQ_UNSUPPORTED with more) runs the gate norm
+ * inside the O GEMV and the silu*mul inside the gate+up epilogue with its norm
+ * inside the down GEMV (bq_gemv_norm_fused, bq_gate_up_silu; 2 launches fewer
+ * per block pair, outputs equal to rounding).  The attention kernels are the
+ * caller's: `attention(user, block, st)` must enqueue them on st (and only
+ * there) and write attn_out; NULL leaves attn_out as it is.  Every buffer
+ * holds `rows` rows, row-major: x, input_h, proj [rows][n_embd]; attn_out,
+ * attn_gate [rows][n_attn]; qkv_out[p] [rows][N_p]; ffn_g, ffn_u [rows][n_ff]
+ * (ffn_u unused when fold = 1); logits [rows][vocab]; xq/xd/xsum hold the q8
+ * rows of the widest operand, rows x max(n_embd, n_attn, n_ff) values.  x is
+ * updated in place.  A graph captures the pointers and the row count it is
+ * created with: replays read and write the same buffers. */
 enum { BQ_BLOCK_ATTN = 0, BQ_BLOCK_FFN = 1 };
 typedef struct bq_decode_block {
     int kind;                     /* BQ_BLOCK_ATTN or BQ_BLOCK_FFN */
@@ -401,6 +408,7 @@ typedef struct bq_decode_step {
     const void* head_q8s; const float* head_rs; const bq_weight* head;  /* one of the two heads, or neither */
     int vocab;
     float* logits;
+    int rows;                     /* tokens per step, 1..8 (0 means 1) */
 } bq_decode_step;
 /* Enqueue one token's launch sequence on st (stream-ordered, allocates nothing). */
 int bq_decode_enqueue(const bq_decode_step* s, bq_stream_t st);
