@@ -322,6 +322,7 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
     };
 
     load_stage(s0);
+    const MfmaCvt cv = mfma_cvt_init(lane);
     for (int s = s0; s < s1; ++s) {
         __syncthreads();  // everyone is done reading the previous stage
         store_stage(s);
@@ -358,11 +359,23 @@ k_mmq_q5k_raw(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __r
                     const f32x32 sc = __builtin_amdgcn_mfma_f32_32x32x1f32(wsv[nt], xsv[mt], zero32, 0, 0, 0);
 #pragma unroll
                     for (int e = 0; e < 2; ++e) {
-                        const i32x16 zero = {0};
-                        const i32x16 dd = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[nt][e], b[mt][e], zero, 0, 0, 0);
+                        if constexpr (TM == 32) {
+                            // matrix-core conversion (mfma_cvt_neg): the 32-token
+                            // tile has the registers for it (M = 512: 94-96 ->
+                            // 90-91 us); the 128-token tile would spill
+                            const i32x16 dd =
+                                __builtin_amdgcn_mfma_i32_32x32x32_i8(a[nt][e], b[mt][e], cv.bias, 0, 0, 0);
+                            const f32x16 ff = mfma_cvt_neg(cv, dd);
 #pragma unroll
-                        for (int r = 0; r < 16; ++r)
-                            acc[nt][mt][r] = __builtin_fmaf(sc[16 * e + r], (float)dd[r], acc[nt][mt][r]);
+                            for (int r = 0; r < 16; ++r)
+                                acc[nt][mt][r] = __builtin_fmaf(-sc[16 * e + r], ff[r], acc[nt][mt][r]);
+                        } else {
+                            const i32x16 zero = {0};
+                            const i32x16 dd = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[nt][e], b[mt][e], zero, 0, 0, 0);
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                acc[nt][mt][r] = __builtin_fmaf(sc[16 * e + r], (float)dd[r], acc[nt][mt][r]);
+                        }
                     }
                 }
         }
