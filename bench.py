@@ -561,6 +561,8 @@ def main():
     ap.add_argument("--probe-only", action="store_true",
                     help="only the instruction issue-rate probes and the empty-kernel launch cost; "
                          "prints their JSON object")
+    ap.add_argument("--stack-only", action="store_true",
+                    help="only config 5 (the whole-stack decode and the decode-step chains); prints its JSON object")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the prefill GEMMs of config 4 and the Q6_K GEMM (for counter profiles); "
                          "prints their JSON object")
@@ -644,6 +646,10 @@ def main():
         return
     if args.gemm_only:
         print(json.dumps({"gemm": gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out)}), flush=True)
+        return
+    if args.stack_only:
+        print(json.dumps({"config5_whole_stack": whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr)}),
+              flush=True)
         return
 
     # ---------------------------------------------------------------- decode FFN step
