@@ -196,6 +196,7 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
     R = 8   # buffers for up to 8 token rows (the verify steps)
     fb = {"x": torch.randn((R, K), generator=g, device="cuda"), "aout": torch.randn((R, KO), generator=g, device="cuda"),
           "qkv": torch.empty((R, NQKV), device="cuda"), "proj": torch.empty((R, K), device="cuda"),
+          "xalt": torch.empty(K, device="cuda"),
           "fg": torch.empty((R, FF), device="cuda"), "fu": torch.empty((R, FF), device="cuda"),
           "logits": torch.empty((R, VOCAB), device="cuda"), "alpha": vec(K), "alpha2": vec(K), "sgate": vec(KO),
           "sg": vec(FF), "su": vec(FF)}
@@ -218,12 +219,13 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
     chain = {}
     # (rows, fold): the one-token step unfolded and folded, and the verify
     # steps over 2 / 4 / 8 token rows (one graph per row count)
-    for rows, fold in ((1, 0), (1, 1), (2, 0), (4, 0), (8, 0)):
+    for rows, fold in ((1, 0), (1, 1), (1, 2), (2, 0), (4, 0), (8, 0)):
         stp = bq.DecodeStep()
         stp.n_blocks, stp.blocks, stp.n_embd, stp.fold, stp.rows = 2 * LAYERS, blocks, K, fold, rows
         stp.x, stp.xq, stp.xd, stp.xsum = fb["x"].data_ptr(), qb[0].data_ptr(), qb[1].data_ptr(), qb[2].data_ptr()
         stp.proj, stp.ffn_g, stp.ffn_u = fb["proj"].data_ptr(), fb["fg"].data_ptr(), fb["fu"].data_ptr()
         stp.head, stp.logits = ctypes.pointer(lmw), fb["logits"].data_ptr()
+        stp.x_alt = fb["xalt"].data_ptr()
         dg = bq.DecodeGraph(stp)
         for _ in range(warmup):
             dg.launch()
@@ -236,7 +238,7 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
         torch.cuda.synchronize()
         chain[(rows, fold)] = e0.elapsed_time(e1) / steps
         dg.close()
-    chain_ms, folded_ms = chain[(1, 0)], chain[(1, 1)]
+    chain_ms, folded_ms, folded2_ms = chain[(1, 0)], chain[(1, 1)], chain[(1, 2)]
     verify = {f"rows{r}": {"ms_per_step": round(chain[(r, 0)], 4), "ms_per_token": round(chain[(r, 0)] / r, 4),
                            "step_vs_one_row": round(chain[(r, 0)] / chain_ms, 3)} for r in (2, 4, 8)}
     del fb, qb
@@ -262,6 +264,10 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
                                             "inside the down GEMV (bq_gemv_norm_fused)",
                                     "ms_per_token": round(folded_ms, 4), "GBps": round(gbs(tot, folded_ms), 1),
                                     "launches_per_token": 6 * LAYERS + 2},
+            "decode_chain_folded2": {"what": "fold = 2: as fold = 1, and each FFN block's resid -> q8 inside the "
+                                             "next layer's QKV GEMV (bq_gemv_norm_fused with BQ_OP_RESID)",
+                                     "ms_per_token": round(folded2_ms, 4), "GBps": round(gbs(tot, folded2_ms), 1),
+                                     "launches_per_token": 5 * LAYERS + 3},
             "decode_chain_verify": {"what": "the same step (fold = 0) over 2 / 4 / 8 token rows, the speculative-"
                                             "verify step with every row's logits (forward_batch_impl with "
                                             "all_logits, bruce.cu:7610-7843; one captured graph per row count as "

@@ -90,7 +90,8 @@ class DecodeStep(ctypes.Structure):
                 ("proj", ctypes.c_void_p), ("ffn_g", ctypes.c_void_p), ("ffn_u", ctypes.c_void_p),
                 ("attention", ATTN_HOOK), ("user", ctypes.c_void_p),
                 ("head_q8s", ctypes.c_void_p), ("head_rs", ctypes.c_void_p), ("head", ctypes.POINTER(Weight)),
-                ("vocab", ctypes.c_int), ("logits", ctypes.c_void_p), ("rows", ctypes.c_int)]
+                ("vocab", ctypes.c_int), ("logits", ctypes.c_void_p), ("rows", ctypes.c_int),
+                ("x_alt", ctypes.c_void_p)]
 
 
 _lib = None

@@ -17,9 +17,47 @@
 
 namespace {
 
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// fold = 2 launches the resid producer directly (flush below): its buffers
+// are checked here as the public producer entry points check theirs
+bool fold2_ok(const bq_decode_step* s) {
+    return s->x_alt && s->x_alt != s->x && al16(s->x) && al16(s->x_alt) && al16(s->proj) &&
+           al16(s->xq) && al16(s->xd) && al16(s->xsum) && s->n_embd <= bq::kNormMaxN;
+}
+
 bool dims_ok(const bq_decode_step* s) {
     return s && s->n_blocks >= 0 && (s->n_blocks == 0 || s->blocks) && s->x && s->xq && s->xd && s->xsum &&
-           s->proj && s->n_embd > 0 && (s->n_embd % 32) == 0 && s->rows >= 0 && s->rows <= BQ_MAX_ROWS;
+           s->proj && s->n_embd > 0 && (s->n_embd % 32) == 0 && s->rows >= 0 && s->rows <= BQ_MAX_ROWS &&
+           s->fold >= 0 && s->fold <= 2 && (s->fold < 2 || fold2_ok(s));
+}
+
+// fold = 2: the resid -> q8 (k_resid :8017) of a block followed by an
+// attention block runs inside that block's QKV GEMV (bq_gemv_norm_fused with
+// BQ_OP_RESID), which writes the new residual row to the other of x / x_alt:
+// every workgroup of that GEMV reads the old row, so it cannot be updated in
+// place.  `cur` is the buffer holding the residual row; a pending update is
+// materialised (flush) by the standalone producer into x wherever the QKV
+// GEMV cannot take it: before norm_before / norm_after, when the QKV has no
+// Q5_K part or the fused form refuses it, and at the end of the step, so that
+// x holds the step's result as in the other modes.  Before an FFN block the
+// update stays a launch of its own: inside the gate+up GEMV every one of its
+// ~1150 workgroups recomputes it from 36 KB of rows (about the matrix's own
+// byte count again through L2), which measured slower than the launch.
+struct Resid {
+    float* cur = nullptr;
+    const float* alpha = nullptr;  // non-null: an update of cur by proj is pending
+};
+
+float* other_of(const bq_decode_step* s, const float* cur) { return cur == s->x ? s->x_alt : s->x; }
+
+int flush(const bq_decode_step* s, Resid& rs, bq_stream_t st) {
+    if (!rs.alpha) return BQ_OK;
+    const hipError_t e = bq::launch_norm_q8(bq::kOpResid, s->x, rs.cur, s->proj, rs.alpha, nullptr, 1, s->n_embd,
+                                            s->xq, s->xd, s->xsum, (hipStream_t)st);
+    rs.cur = s->x;
+    rs.alpha = nullptr;
+    return e == hipSuccess ? BQ_OK : -(int)e;
 }
 
 // tokens per step: 0 means 1
@@ -35,7 +73,7 @@ int gemv_rows_of(float* y, const bq_weight* w, int rows, const bq_decode_step* s
 
 // one attention block: bruce.cu:7915-7993 (QKV, attention, gate norm, O);
 // rows 2..8: :7636-7757
-int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, int rows, bq_stream_t st) {
+int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, int rows, Resid& rs, bq_stream_t st) {
     if (b.n_qkv < 1 || b.n_qkv > BQ_MAX_PARTS || !b.qkv || !b.qkv_out || !b.o || !b.attn_out || !b.attn_gate ||
         !b.sgate || b.n_attn <= 0 || (b.n_attn % 32) != 0)
         return BQ_EINVAL;
@@ -50,7 +88,24 @@ int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, int ro
             wp[nf] = &b.qkv[p];
             yp[nf++] = b.qkv_out[p];
         }
-    if (nf > 0) {
+    bool qkv_done = false;
+    if (nf > 0 && rs.alpha) {
+        // the pending resid -> q8 inside the QKV GEMV; its q8 row is written
+        // out only for the parts that run as their own GEMVs
+        float* nx = other_of(s, rs.cur);
+        const bool q8out = nf < b.n_qkv;
+        const int r = bq_gemv_norm_fused(yp, wp, nf, BQ_OP_RESID, nx, rs.cur, s->proj, rs.alpha, nullptr,
+                                         q8out ? s->xq : nullptr, q8out ? s->xd : nullptr,
+                                         q8out ? s->xsum : nullptr, st);
+        if (r != BQ_OK && r != BQ_UNSUPPORTED) return r;
+        if (r == BQ_OK) {
+            rs.cur = nx;
+            rs.alpha = nullptr;
+            qkv_done = true;
+        }
+    }
+    if (int e = flush(s, rs, st)) return e;
+    if (nf > 0 && !qkv_done) {
         const int r = bq_verify_fused(yp, wp, nf, rows, s->xq, s->xd, s->xsum, 0, st);
         if (r != BQ_OK && r != BQ_UNSUPPORTED) return r;
         if (r == BQ_UNSUPPORTED)
@@ -78,9 +133,10 @@ int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, int ro
 
 // one FFN block: bruce.cu:7994-8012 (gate+up, silu*mul norm, down); rows
 // 2..8: :7759-7800
-int ffn_block(const bq_decode_step* s, const bq_decode_block& b, int rows, bq_stream_t st) {
+int ffn_block(const bq_decode_step* s, const bq_decode_block& b, int rows, Resid& rs, bq_stream_t st) {
     if (!b.gate || !b.up || !b.down || !b.s_gate || !b.s_up || !s->ffn_g || b.n_ff <= 0 || (b.n_ff % 32) != 0)
         return BQ_EINVAL;
+    if (int e = flush(s, rs, st)) return e;
     if (s->fold) {
         // silu*mul in the gate+up epilogue (h -> ffn_g), its norm + q8 inside the down GEMV
         if (int e = bq_gate_up_silu(s->ffn_g, b.gate, b.up, b.s_gate, b.s_up, s->xq, s->xd, s->xsum, st)) return e;
@@ -118,24 +174,38 @@ int bq_decode_enqueue(const bq_decode_step* s, bq_stream_t st) {
     const int n = s->n_embd, rows = rows_of(s);
     // the folded producers are one-row GEMV epilogues / prologues
     if (s->fold && rows > 1) return BQ_UNSUPPORTED;
+    Resid rs;
+    rs.cur = s->x;
     for (int i = 0; i < s->n_blocks; ++i) {
         const bq_decode_block& b = s->blocks[i];
         // loop start: x = norm(x + input_h) (k_add_norm, :7914; rows: k_add_norm_rows :7633)
         if (b.norm_before) {
+            if (int e = flush(s, rs, st)) return e;
             if (!s->input_h) return BQ_EINVAL;
             if (int e = bq_add_norm_q8(s->x, s->input_h, rows, n, s->xq, s->xd, s->xsum, st)) return e;
         }
-        const int r = b.kind == BQ_BLOCK_FFN ? ffn_block(s, b, rows, st) : b.kind == BQ_BLOCK_ATTN
-                                                                             ? attn_block(s, b, i, rows, st)
-                                                                             : BQ_EINVAL;
+        const int r = b.kind == BQ_BLOCK_FFN ? ffn_block(s, b, rows, rs, st) : b.kind == BQ_BLOCK_ATTN
+                                                                                 ? attn_block(s, b, i, rows, rs, st)
+                                                                                 : BQ_EINVAL;
         if (r) return r;
-        // x = resid(x, proj, alpha) -> q8 x (k_resid_vec4, :8017; rows: :7803-7815)
+        // x = resid(x, proj, alpha) -> q8 x (k_resid_vec4, :8017; rows: :7803-7815);
+        // fold = 2: left pending for the next block's QKV GEMV
         if (!b.alpha) return BQ_EINVAL;
-        if (int e = bq_resid_q8(s->x, s->proj, b.alpha, rows, n, s->xq, s->xd, s->xsum, st)) return e;
+        if (s->fold == 2) {
+            rs.alpha = b.alpha;
+            const bool to_qkv = i + 1 < s->n_blocks && s->blocks[i + 1].kind == BQ_BLOCK_ATTN;
+            if (!to_qkv)
+                if (int e = flush(s, rs, st)) return e;
+        } else if (int e = bq_resid_q8(s->x, s->proj, b.alpha, rows, n, s->xq, s->xd, s->xsum, st)) {
+            return e;
+        }
         // loop end: x = norm(x) (k_norm, :8022; rows: k_norm_rows :7818)
-        if (b.norm_after)
+        if (b.norm_after) {
+            if (int e = flush(s, rs, st)) return e;
             if (int e = bq_norm_q8(s->x, s->x, rows, n, s->xq, s->xd, s->xsum, st)) return e;
+        }
     }
+    if (int e = flush(s, rs, st)) return e;
     // logits of every row from the q8 rows of x (:8026-8032; rows: launch_logits_b :7832)
     if (s->head_q8s) {
         if (!s->logits) return BQ_EINVAL;

@@ -81,10 +81,18 @@ BQ_DEV uint32_t q5_codes(uint32_t qs, uint32_t qh, int j, bool hi) {
     return (rot & 0x10101010u) | nib;
 }
 
+// Row stride of the staged int8 activation rows: with several rows, K + 16,
+// so that the lanes of a multi-row block (lane = 4 * task + row), which read
+// the same 16 bytes of 4 rows, reach 4 different bank groups.  Unpadded, the
+// rows (K a multiple of 256) start on the same bank and every such read is a
+// 4-way conflict.
+__host__ __device__ constexpr int act_row_stride(int rows, int K) { return rows > 1 ? K + 16 : K; }
+
 struct ActLds {            // activations of MR rows staged in LDS
-    const int8_t* x;       // [MR][K] int8 codes
+    const int8_t* x;       // [MR][xr] int8 codes (row stride act_row_stride)
     const float* xd;       // [MR][K/32]
     const int32_t* xs;     // Q5_K only: xsum [MR][K/32]
+    int xr;                // row stride of x
 };
 
 // ---------------------------------------------------------------------------
@@ -140,7 +148,7 @@ struct FmtQ5K {
         const int g0 = (t >> 2) * 8 + j0;
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            const int8_t* xp = act.x + m * K + 32 * g0;
+            const int8_t* xp = act.x + m * act.xr + 32 * g0;
             const u32x4 x0 = *(const u32x4*)(xp), x1 = *(const u32x4*)(xp + 16);
             const u32x4 x2 = *(const u32x4*)(xp + 32), x3 = *(const u32x4*)(xp + 48);
             int s0 = 0, s1 = 0;
@@ -188,7 +196,7 @@ BQ_DEV void q5k_dot_mm(const FmtQ5K::Task& a, int t, const ActLds& act, int K, f
 #pragma unroll
     for (int ms = 0; ms < (MR + 3) / 4; ++ms) {
         const int m = 4 * ms + r;  // activation row fed as A by this lane
-        const int8_t* xp = act.x + (m < MR ? m : MR - 1) * K + 32 * g0;
+        const int8_t* xp = act.x + (m < MR ? m : MR - 1) * act.xr + 32 * g0;
         u32x4 x0 = *(const u32x4*)(xp), x1 = *(const u32x4*)(xp + 16);
         u32x4 x2 = *(const u32x4*)(xp + 32), x3 = *(const u32x4*)(xp + 48);
         // one accumulator chain per sub-block (split chains measured slower)
@@ -250,7 +258,7 @@ struct FmtQ6KRep {
             int s[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const u32x4 x = *(const u32x4*)(act.x + m * K + k0 + 16 * g);
+                const u32x4 x = *(const u32x4*)(act.x + m * act.xr + k0 + 16 * g);
                 int v = 0;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v = dot4((int)a.c[g][i], (int)x[i], v);
@@ -274,7 +282,7 @@ BQ_DEV void q6rep_dot_mm(const FmtQ6KRep::Task& a, int t, const ActLds& act, int
 #pragma unroll
     for (int ms = 0; ms < (MR + 3) / 4; ++ms) {
         const int m = 4 * ms + r;  // activation row fed as A by this lane
-        const int8_t* xp = act.x + (m < MR ? m : MR - 1) * K + k0;
+        const int8_t* xp = act.x + (m < MR ? m : MR - 1) * act.xr + k0;
         i32x4 c[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -368,7 +376,7 @@ struct FmtQ6KRaw {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int k = kb + 32 * u;
-                const u32x4 x = *(const u32x4*)(act.x + m * K + k);
+                const u32x4 x = *(const u32x4*)(act.x + m * act.xr + k);
                 int s = 0;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -414,7 +422,7 @@ struct FmtQ6KRaw {
 #pragma unroll
         for (int ms = 0; ms < (MR + 3) / 4; ++ms) {
             const int m = 4 * ms + r;
-            const int8_t* xp = act.x + (m < MR ? m : MR - 1) * K + kb;
+            const int8_t* xp = act.x + (m < MR ? m : MR - 1) * act.xr + kb;
             i32x4 c[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
@@ -453,7 +461,7 @@ template <> struct RowBytes<FmtQ6KRep> { static BQ_DEV size_t of(int K) { return
 // LDS bytes: MR staged activation rows + the K-slice partial sums
 template <class F>
 __host__ __device__ inline size_t act_lds_bytes(int rows, int K) {
-    size_t b = (size_t)rows * K + (size_t)rows * (K / 32) * 4;
+    size_t b = (size_t)rows * act_row_stride(rows, K) + (size_t)rows * (K / 32) * 4;
     if (std::is_same<F, FmtQ5K>::value) b += (size_t)rows * (K / 32) * 4;
     return b;
 }
@@ -730,8 +738,11 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     const int nb = K >> 5;
     // ---- 1. activations -> LDS (asynchronous), or this wave's fp32 chunks -> registers
     ActLds act;
+    constexpr int kXr0 = act_row_stride(MR, 0);  // 0 or 16: padding per row
+    const int xr = K + kXr0;
     act.x = (const int8_t*)smem;
-    act.xd = (const float*)(smem + MR * K);
+    act.xr = xr;
+    act.xd = (const float*)(smem + MR * xr);
     act.xs = (const int32_t*)(act.xd + MR * nb);
     float* part_sums = (float*)(smem + act_lds_bytes<F>(MR, K));  // [waves][MR][4]
     constexpr int QA = QN > 0 ? QN : 1;
@@ -743,10 +754,15 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     } else if constexpr (QN < 0) {
         fp_load(pin, fq, K, wave, lane);
     } else {
-        dma_to_lds(smem, xq, MR * K, wave, waves, lane);
-        dma_to_lds(smem + MR * K, xd, MR * nb * 4, wave, waves, lane);
+        if constexpr (kXr0 == 0) {
+            dma_to_lds(smem, xq, MR * K, wave, waves, lane);
+        } else {
+#pragma unroll
+            for (int r = 0; r < MR; ++r) dma_to_lds(smem + r * xr, xq + (size_t)r * K, K, wave, waves, lane);
+        }
+        dma_to_lds(smem + MR * xr, xd, MR * nb * 4, wave, waves, lane);
         if constexpr (std::is_same<F, FmtQ5K>::value)
-            dma_to_lds(smem + MR * K + MR * nb * 4, xsum, MR * nb * 4, wave, waves, lane);
+            dma_to_lds(smem + MR * xr + MR * nb * 4, xsum, MR * nb * 4, wave, waves, lane);
     }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);

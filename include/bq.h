@@ -366,14 +366,20 @@ int bq_gguf_load(bq_gguf* g, int64_t i, void* raw, void* rep, void* rep_min, bq_
  * fold = 1 (rows = 1 only; BQ_UNSUPPORTED with more) runs the gate norm
  * inside the O GEMV and the silu*mul inside the gate+up epilogue with its norm
  * inside the down GEMV (bq_gemv_norm_fused, bq_gate_up_silu; 2 launches fewer
- * per block pair, outputs equal to rounding).  The attention kernels are the
- * caller's: `attention(user, block, st)` must enqueue them on st (and only
- * there) and write attn_out; NULL leaves attn_out as it is.  Every buffer
- * holds `rows` rows, row-major: x, input_h, proj [rows][n_embd]; attn_out,
- * attn_gate [rows][n_attn]; qkv_out[p] [rows][N_p]; ffn_g, ffn_u [rows][n_ff]
- * (ffn_u unused when fold = 1); logits [rows][vocab]; xq/xd/xsum hold the q8
- * rows of the widest operand, rows x max(n_embd, n_attn, n_ff) values.  x is
- * updated in place.  A graph captures the pointers and the row count it is
+ * per block pair, outputs equal to rounding).  fold = 2 (rows = 1 only)
+ * also runs the resid -> q8 of each block that an attention block follows
+ * inside that block's QKV GEMV (bq_gemv_norm_fused with BQ_OP_RESID over its
+ * Q5_K parts; its q8 row is written out for any other part), which writes
+ * the new residual row to the other of x and x_alt; the other updates run as
+ * their own launches into x, so x holds the result as in the other modes
+ * (needs x_alt; 1 launch fewer per layer than fold = 1).  The attention
+ * kernels are the caller's: `attention(user, block, st)` must enqueue them
+ * on st (and only there) and write attn_out; NULL leaves attn_out as it is.
+ * Every buffer holds `rows` rows, row-major: x, input_h, proj
+ * [rows][n_embd]; attn_out, attn_gate [rows][n_attn]; qkv_out[p] [rows][N_p];
+ * ffn_g, ffn_u [rows][n_ff] (ffn_u unused when fold >= 1); logits
+ * [rows][vocab]; xq/xd/xsum hold the q8 rows of the widest operand, rows x
+ * max(n_embd, n_attn, n_ff) values.  x is updated in place.  A graph captures the pointers and the row count it is
  * created with: replays read and write the same buffers. */
 enum { BQ_BLOCK_ATTN = 0, BQ_BLOCK_FFN = 1 };
 typedef struct bq_decode_block {
@@ -409,6 +415,7 @@ typedef struct bq_decode_step {
     int vocab;
     float* logits;
     int rows;                     /* tokens per step, 1..8 (0 means 1) */
+    float* x_alt;                 /* fold = 2: a second residual row [n_embd], not x */
 } bq_decode_step;
 /* Enqueue one token's launch sequence on st (stream-ordered, allocates nothing). */
 int bq_decode_enqueue(const bq_decode_step* s, bq_stream_t st);

@@ -129,3 +129,56 @@ def test_workspace_bytes():
             assert worst <= 32 << 20
     if not _has_gpu():
         assert L.bq_gemm_workspace_bytes(64, 3072, 9216) == 0
+
+
+STRUCTS = [("bq_weight", "Weight"), ("bq_gguf_tensor", "GgufTensor"), ("bq_decode_block", "DecodeBlock"),
+           ("bq_decode_step", "DecodeStep")]
+
+
+def header_fields(name):
+    """Field names of `typedef struct name { ... } name;` in include/bq.h, in order."""
+    text = open(os.path.join(ROOT, "include", "bq.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), text, flags=re.S).group(1)
+    out = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        fp = re.search(r"\(\s*\*\s*(\w+)\s*\)", decl)           # function pointer
+        if fp:
+            out.append(fp.group(1))
+            continue
+        for part in decl.split(","):
+            out.append(re.findall(r"(\w+)\s*(?:\[\s*\d+\s*\])?\s*$", part.strip())[0])
+    return out
+
+
+def test_ctypes_structs_match_header(tmp_path):
+    """The ctypes mirrors in bq.py have the header's fields, in order, at the
+    offsets a C compiler gives them (a field missing from a mirror makes the
+    library read past the caller's struct)."""
+    import shutil
+    import subprocess
+    import bq
+    for cname, pyname in STRUCTS:
+        assert [f[0] for f in getattr(bq, pyname)._fields_] == header_fields(cname), cname
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        return
+    src = ['#include <stddef.h>', '#include <stdio.h>', '#include "bq.h"', 'int main(void) {']
+    for cname, _ in STRUCTS:
+        src.append('printf("%s size %%zu\\n", sizeof(%s));' % (cname, cname))
+        for f in header_fields(cname):
+            src.append('printf("%s %s %%zu\\n", offsetof(%s, %s));' % (cname, f, cname, f))
+    src.append("return 0; }")
+    (tmp_path / "off.c").write_text("\n".join(src))
+    exe = tmp_path / "off"
+    subprocess.run([cc, "-I", os.path.join(ROOT, "include"), str(tmp_path / "off.c"), "-o", str(exe)], check=True)
+    got = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                        check=True).stdout.splitlines())
+    for cname, pyname in STRUCTS:
+        S = getattr(bq, pyname)
+        assert int(got[f"{cname} size"]) == ctypes.sizeof(S), cname
+        for f, _ in S._fields_:
+            assert int(got[f"{cname} {f}"]) == getattr(S, f).offset, (cname, f)

@@ -22,10 +22,16 @@ down Q6_K) and a Q8_0 logits head are run eagerly and from the graph:
 * the logits match the oracle's Q8_0 head on the final q8 row within 1e-4;
 * the whole chain from x0 stays within 2e-4 of the oracle's whole chain, the
   oracle taking at each block the candidate rounding that the GPU's block
-  output matches;
+  output matches, and the GPU's q8 code of the block's input where the two
+  input rows (equal to ~2e-7) straddle a rounding boundary;
 * every graph replay is bit-identical to the eager run.
-The folded form (fold = 1: gate norm inside the O GEMV, silu*mul inside the
-gate+up epilogue, its norm inside the down GEMV) is checked the same way.
+The folded forms (fold = 1: gate norm inside the O GEMV, silu*mul inside the
+gate+up epilogue, its norm inside the down GEMV; fold = 2: also the resid ->
+q8 of each FFN block inside the next attention block's QKV GEMV, the
+residual row alternating between x and x_alt, the other updates as their own
+launches) are checked the same way, and with fold = 2 the row the QKV GEMV
+wrote must equal, bit for bit, the standalone producer's row that ended the
+shorter step.
 """
 import ctypes
 
@@ -97,18 +103,31 @@ def _gemv_candidates(gemv, q, flips):
         yield base + sum((deltas[j] for j in range(len(flips)) if mask >> j & 1), np.zeros_like(base))
 
 
-def _oracle_block(oracle, m, bi, x):
+def _oracle_block(oracle, m, bi, x, like=None):
     """Block bi (even: attention of layer bi // 2, odd: its FFN) of the
     reference's sequence applied to the fp32 row x, with the oracle's GEMVs
     (double precision over the q8 codes), norms and quantizer.  Returns the
     candidate new x rows (fp32), one per rounding of the block's requantized
-    row's ambiguous codes (_q8_flips), and the number of those codes."""
+    row's ambiguous codes (_q8_flips), and the number of those codes.
+    like (optional): the GPU's row that x stands for; where the q8 codes of
+    the two differ, each such code of x lies on a rounding boundary (checked)
+    and the block takes the GPU's code, as it takes the GPU's rounding of the
+    requantized row."""
     f32 = lambda a: np.asarray(a, np.float32)
     L = m["layers"][bi // 2]
     x = x[None]
     if bi == 0:
         x = f32(oracle.norm_rows("add", x, m["input_h"][None]))
     q = oracle.q8_rows(x)
+    if like is not None:
+        ql = oracle.q8_rows(like[None])
+        diff = np.nonzero(q[0][0] != ql[0][0])[0]
+        if len(diff):
+            amb = {i for i, _ in _q8_flips(oracle, x)[1]}
+            assert all(int(i) in amb for i in diff), ("input codes differ off a rounding boundary", diff)
+            xq = ql[0].copy()
+            xs = xq.reshape(1, -1, 32).astype(np.int32).sum(axis=2).astype(q[2].dtype)
+            q = (xq, q[1], xs)
     outs = []
     if bi % 2 == 0:
         ys = {}
@@ -181,13 +200,16 @@ def _gpu_step(bq, m, fold):
     xs = torch.empty(FF // 32, dtype=torch.int32, device="cuda")
     proj, fg, fu = torch.empty(E, device="cuda"), torch.empty(FF, device="cuda"), torch.empty(FF, device="cuda")
     logits = torch.empty(V, device="cuda")
-    keep += [x, xq, xd, xs, proj, fg, fu, logits, blocks]
+    xalt = torch.full((E,), float("nan"), device="cuda")
+    keep += [x, xalt, xq, xd, xs, proj, fg, fu, logits, blocks]
     st = bq.DecodeStep()
     st.n_blocks, st.blocks, st.n_embd, st.fold = 4, blocks, E, fold
     st.x, st.input_h = x.data_ptr(), ptr(D(m["input_h"]))
     st.xq, st.xd, st.xsum = xq.data_ptr(), xd.data_ptr(), xs.data_ptr()
     st.proj, st.ffn_g, st.ffn_u = proj.data_ptr(), fg.data_ptr(), fu.data_ptr()
     st.head_q8s, st.head_rs, st.vocab, st.logits = head.data_ptr(), ptr(D(m["rs"])), V, logits.data_ptr()
+    if fold == 2:
+        st.x_alt = xalt.data_ptr()
     x0 = D(m["x0"])
 
     def reset():
@@ -197,15 +219,15 @@ def _gpu_step(bq, m, fold):
         xd[:E // 32].copy_(q[1][0])
         xs[:E // 32].copy_(q[2][0])
         logits.fill_(float("nan"))
-    return st, keep, reset, x, logits
+    return st, keep, reset, x, logits, xalt
 
 
-@pytest.mark.parametrize("fold", [0, 1])
+@pytest.mark.parametrize("fold", [0, 1, 2])
 def test_decode_graph_vs_oracle(bq, oracle, fold):
     import torch
     print(f"decode step fold={fold}", flush=True)
     m = _model(bq, oracle)
-    st, keep, reset, x, logits = _gpu_step(bq, m, fold)
+    st, keep, reset, x, logits, xalt = _gpu_step(bq, m, fold)
     # block by block: the first nb - 1 blocks on the GPU, then block nb on the
     # GPU and in the oracle from the same fp32 row
     prev = m["x0"].copy()
@@ -221,6 +243,11 @@ def test_decode_graph_vs_oracle(bq, oracle, fold):
         print(f"  block {nb - 1}: x vs oracle {err:.2e} ({namb} codes within {AMBIG:g} of a rounding boundary, "
               f"unrounded-as-GPU error {oracle.normwise_err(got, cands[0].astype(np.float64)):.2e})", flush=True)
         assert err < 2e-4, (nb, err)
+        if fold == 2 and nb >= 3:
+            # x_alt holds block 1's residual row as block 2's QKV GEMV wrote it
+            # (the folded producer): bit-identical to the standalone
+            # producer's row that ended the 2-block step
+            assert np.array_equal(host(xalt).view(np.uint32), gpu_x[1].view(np.uint32)), nb
         gpu_x.append(got)
         prev = got
     el = host(logits).copy()
@@ -228,11 +255,13 @@ def test_decode_graph_vs_oracle(bq, oracle, fold):
     print(f"  logits vs oracle head on the final q8 row: {lerr:.2e}", flush=True)
     assert lerr < 1e-4
     # the whole chain in the oracle from x0, each block's ambiguous roundings
-    # taken as the GPU's block output shows them (without that choice a code
-    # that rounds the other way compounds over the blocks)
+    # (of its requantized row, and of its input row's q8 codes) taken as the
+    # GPU's block output shows them (without that choice a code that rounds
+    # the other way compounds over the blocks)
     rx = m["x0"].copy()
     for bi in range(4):
-        _, rx = _closest(oracle, gpu_x[bi], _oracle_block(oracle, m, bi, rx)[0])
+        e, rx = _closest(oracle, gpu_x[bi], _oracle_block(oracle, m, bi, rx, gpu_x[bi - 1] if bi else None)[0])
+        print(f"  chain block {bi}: closest candidate {e:.2e}", flush=True)
     cx, cl = oracle.normwise_err(prev, rx), oracle.normwise_err(el, _oracle_logits(oracle, m, rx))
     print(f"  whole chain vs oracle chain: x {cx:.2e}, logits {cl:.2e}", flush=True)
     assert cx < 2e-4 and cl < 2e-4
@@ -253,3 +282,27 @@ def test_decode_graph_vs_oracle(bq, oracle, fold):
 def test_decode_rejects(bq):
     st = bq.DecodeStep()
     assert bq.load().bq_decode_enqueue(ctypes.byref(st), bq._stream()) == bq.BQ_EINVAL
+
+
+def test_decode_fold2_rejects(bq):
+    """fold = 2 needs x_alt (16-byte aligned, not x) and one row."""
+    import torch
+    st = bq.DecodeStep()
+    blocks = (bq.DecodeBlock * 1)()
+    st.n_blocks, st.blocks, st.n_embd, st.fold = 0, blocks, 3072, 2
+    bufs = [torch.empty(8 * 3072, device="cuda") for _ in range(8)]
+    st.x, st.xq, st.xd, st.xsum, st.proj, st.ffn_g, st.ffn_u = [b.data_ptr() for b in bufs[:7]]
+    L = bq.load()
+    run = lambda: L.bq_decode_enqueue(ctypes.byref(st), bq._stream())
+    assert run() == bq.BQ_EINVAL                     # no x_alt
+    st.x_alt = st.x
+    assert run() == bq.BQ_EINVAL                     # x_alt is x
+    st.x_alt = bufs[7].data_ptr() + 4
+    assert run() == bq.BQ_EINVAL                     # misaligned
+    st.x_alt = bufs[7].data_ptr()
+    st.ffn_u = None
+    assert run() == bq.BQ_OK                         # an empty block list
+    st.rows = 2
+    assert run() == bq.BQ_UNSUPPORTED
+    st.rows, st.fold = 1, 3
+    assert run() == bq.BQ_EINVAL

@@ -11,7 +11,7 @@ import test_gpu_decode as D
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("fold", [0, 1])
+@pytest.mark.parametrize("fold", [0, 1, 2])
 def test_decode_graph_vs_oracle_reference_shapes(bq, oracle, fold):
     saved = (D.E, D.A, D.FF, D.PARTS)
     D.E, D.A, D.FF = 2560, 4096, 7168

@@ -25,6 +25,8 @@ CASES = [
     ("resid", "q5k", 5120, 512, 1),     # 5 chunks: a 16-wave workgroup
     ("silu", "q6k", 16384, 256, 1),     # the largest row
     ("norm", "q5k", 1280, 640, 3),
+    ("resid", "q5k", 2560, 7168, 2),    # gate+up at the reference model's hidden size (3 chunks, the last half full)
+    ("resid", "q5k", 2560, 4096, 3),    # q / k / gate parts at that size
 ]
 
 
