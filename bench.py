@@ -569,6 +569,8 @@ def main():
                          "prints their JSON object")
     ap.add_argument("--stack-only", action="store_true",
                     help="only config 5 (the whole-stack decode and the decode-step chains); prints its JSON object")
+    ap.add_argument("--no-stack", action="store_true",
+                    help="skip config 5 (the whole-stack decode and the decode-step graphs), e.g. for counter runs")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the prefill GEMMs of config 4 and the Q6_K GEMM (for counter profiles); "
                          "prints their JSON object")
@@ -721,7 +723,8 @@ def main():
         c1_obj = {"us": round(c1ms * 1e3, 2), "GBps": round(gbs(c1.nbytes + q8_bytes(1, K) + 4 * K, c1ms), 1)}
 
         # ------------------------------------------------------------ config 5: whole-stack token
-        stack_obj = whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr)
+        if not args.no_stack:
+            stack_obj = whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr)
 
         # ------------------------------------------------------------ Q8_0 logits head
         q8s_obj = q8s_head(B, bq, torch, sp, ptr)
