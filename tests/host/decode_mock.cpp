@@ -1,0 +1,151 @@
+// Host-only check of bq_decode_enqueue's call sequence (bq_decode.hip built
+// for the host alone): every entry point it calls is replaced by a recorder
+// that checks each pointer argument lies inside a registered buffer with room
+// for the elements the call touches, and counts the calls.  Run by
+// tests/test_decode_host.py; prints one line per (fold, blocks) step and the
+// number of bad arguments.
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+#include <hip/hip_runtime.h>
+#include "bq.h"
+#include "bq_internal.hpp"
+
+struct Buf { const char* name; size_t bytes; };
+static std::map<uintptr_t, Buf> g_bufs;
+static int g_bad = 0;
+static int g_calls = 0;
+static bool g_verbose = false;
+static void* reg(const char* name, size_t bytes) {
+    void* p = aligned_alloc(256, (bytes + 255) / 256 * 256);
+    g_bufs[(uintptr_t)p] = {name, bytes};
+    return p;
+}
+static void chk(const char* call, const char* arg, const void* p, size_t bytes) {
+    if (!p) { printf("  %s: %s NULL (needs %zu B)\n", call, arg, bytes); g_bad++; return; }
+    auto it = g_bufs.upper_bound((uintptr_t)p);
+    if (it == g_bufs.begin()) { printf("  %s: %s=%p not a buffer\n", call, arg, p); g_bad++; return; }
+    --it;
+    const size_t off = (uintptr_t)p - it->first;
+    if (off + bytes > it->second.bytes) {
+        printf("  %s: %s in %s off %zu + %zu > %zu\n", call, arg, it->second.name, off, bytes, it->second.bytes);
+        g_bad++;
+    }
+}
+static const char* nm(const void* p) {
+    if (!p) return "null";
+    auto it = g_bufs.upper_bound((uintptr_t)p); --it; return it->second.name;
+}
+static size_t wbytes(const bq_weight* w) { return (size_t)w->N * (w->K / 256) * (w->ggml_type == BQ_TYPE_Q5_K ? 176 : 210); }
+
+extern "C" {
+int bq_init(void) { return 0; }
+int bq_verify_fused(float* const* ys, const bq_weight* const* ws, int n, int rows, const int8_t* xq, const float* xd,
+                    const int32_t* xs, int, bq_stream_t) {
+    ++g_calls; if (g_verbose) printf("verify_fused n=%d rows=%d\n", n, rows);
+    for (int p = 0; p < n; ++p) { chk("verify", "y", ys[p], 4 * ws[p]->N * rows); chk("verify", "w", ws[p]->raw, wbytes(ws[p])); }
+    chk("verify", "xq", xq, ws[0]->K * rows); chk("verify", "xd", xd, ws[0]->K / 8 * rows); chk("verify", "xs", xs, ws[0]->K / 8 * rows);
+    return 0;
+}
+int bq_gemv(float* y, const bq_weight* w, const int8_t* xq, const float* xd, const int32_t* xs, bq_stream_t) {
+    ++g_calls; if (g_verbose) printf("gemv N=%d K=%d y=%s\n", w->N, w->K, nm(y));
+    chk("gemv", "y", y, 4 * w->N); chk("gemv", "w", w->raw, wbytes(w)); chk("gemv", "xq", xq, w->K);
+    chk("gemv", "xd", xd, w->K / 8); if (w->ggml_type == BQ_TYPE_Q5_K) chk("gemv", "xs", xs, w->K / 8);
+    return 0;
+}
+int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd, const int32_t* xs, uint16_t*, void*, size_t, bq_stream_t) {
+    ++g_calls; if (g_verbose) printf("gemm_b rows=%d\n", rows); chk("gemm_b", "y", y, 4 * w->N * rows); return 0;
+}
+int bq_gemv_norm_fused(float* const* ys, const bq_weight* const* ws, int nparts, int op, float* out, const float* a,
+                       const float* b, const float* c, const float* d, int8_t* xq, float* xd, int32_t* xsum, bq_stream_t) {
+    const int K = ws[0]->K;
+    ++g_calls; if (g_verbose) printf("norm_fused op=%d parts=%d K=%d out=%s a=%s b=%s c=%s d=%s xq=%s\n", op, nparts, K, nm(out), nm(a), nm(b), nm(c), nm(d), nm(xq));
+    for (int p = 0; p < nparts; ++p) { chk("nf", "y", ys[p], 4 * ws[p]->N); chk("nf", "w", ws[p]->raw, wbytes(ws[p])); }
+    chk("nf", "a", a, 4 * K);
+    if (op != BQ_OP_NORM) chk("nf", "b", b, 4 * K);
+    if (op >= BQ_OP_RESID) chk("nf", "c", c, 4 * K);
+    if (op == BQ_OP_SILU) chk("nf", "d", d, 4 * K);
+    if (out) chk("nf", "out", out, 4 * K);
+    if (xq) { chk("nf", "xq", xq, K); chk("nf", "xd", xd, K / 8); chk("nf", "xs", xsum, K / 8); }
+    if (out && (out == a || out == b)) { printf("  out aliases input\n"); g_bad++; }
+    return 0;
+}
+int bq_gate_up_silu(float* h, const bq_weight* wg, const bq_weight* wu, const float* sg, const float* su, const int8_t* xq, const float* xd, const int32_t* xs, bq_stream_t) {
+    ++g_calls; if (g_verbose) printf("gate_up_silu\n"); chk("gus", "h", h, 4 * wg->N); return 0;
+}
+static void nq(const char* op, float* out, const float* a, const float* b, const float* c, const float* d, int rows, int n, int8_t* xq, float* xd, int32_t* xs) {
+    ++g_calls; if (g_verbose) printf("%s n=%d out=%s a=%s b=%s c=%s\n", op, n, nm(out), nm(a), nm(b), nm(c));
+    if (out) chk(op, "out", out, 4 * n * rows); chk(op, "a", a, 4 * n * rows);
+    if (b) chk(op, "b", b, 4 * n * rows); if (c) chk(op, "c", c, 4 * n); if (d) chk(op, "d", d, 4 * n);
+    chk(op, "xq", xq, n * rows); chk(op, "xd", xd, n / 8 * rows); chk(op, "xs", xs, n / 8 * rows);
+}
+int bq_add_norm_q8(float* x, const float* h, int rows, int n, int8_t* xq, float* xd, int32_t* xs, bq_stream_t) { nq("add_norm", x, x, h, 0, 0, rows, n, xq, xd, xs); return 0; }
+int bq_resid_q8(float* x, const float* u, const float* al, int rows, int n, int8_t* xq, float* xd, int32_t* xs, bq_stream_t) { nq("resid", x, x, u, al, 0, rows, n, xq, xd, xs); return 0; }
+int bq_norm_q8(float* dst, const float* src, int rows, int n, int8_t* xq, float* xd, int32_t* xs, bq_stream_t) { nq("norm", dst, src, 0, 0, 0, rows, n, xq, xd, xs); return 0; }
+int bq_gate_norm_q8(float* dst, const float* a, const float* g, const float* sg, int rows, int n, int8_t* xq, float* xd, int32_t* xs, bq_stream_t) { nq("gate_norm", dst, a, g, sg, 0, rows, n, xq, xd, xs); return 0; }
+int bq_silu_mul_norm_q8(float* dst, const float* g, const float* u, const float* sg, const float* su, int rows, int n, int8_t* xq, float* xd, int32_t* xs, bq_stream_t) { nq("silu_norm", dst, g, u, sg, su, rows, n, xq, xd, xs); return 0; }
+int bq_gemv_q8s(float* y, const void* w, const int8_t* xq, const float* xd, int K, int N, int rows, const float* rs, bq_stream_t) {
+    ++g_calls; if (g_verbose) printf("gemv_q8s K=%d N=%d\n", K, N); chk("q8s", "y", y, 4 * N * rows); chk("q8s", "xq", xq, K * rows); chk("q8s", "xd", xd, K / 8 * rows); return 0;
+}
+}
+namespace bq {
+hipError_t launch_norm_q8(int op, float* out, const float* a, const float* b, const float* c, const float* d, int rows, int n, int8_t* xq, float* xd, int32_t* xs, hipStream_t) {
+    nq(op == 2 ? "launch_norm_q8(resid)" : "launch_norm_q8", out, a, b, c, d, rows, n, xq, xd, xs); return hipSuccess;
+}
+}
+
+int main(int argc, char** argv) {
+    g_verbose = argc > 1;
+    const int E = 3072, A = 4096, FF = 9216, V = 8192;
+    const int PN[4] = {A, 512, A, 512};
+    bq_decode_block blocks[4];
+    memset(blocks, 0, sizeof(blocks));
+    std::vector<bq_weight*> keep;
+    for (int l = 0; l < 2; ++l) {
+        bq_weight* qw = new bq_weight[4]();
+        float** outs = new float*[4];
+        for (int i = 0; i < 4; ++i) {
+            qw[i].K = E; qw[i].N = PN[i]; qw[i].ggml_type = i == 3 ? BQ_TYPE_Q6_K : BQ_TYPE_Q5_K;
+            qw[i].raw = reg("qkvw", (size_t)PN[i] * (E / 256) * (i == 3 ? 210 : 176));
+            outs[i] = (float*)reg("qkv_out", 4 * PN[i]);
+        }
+        bq_weight* wo = new bq_weight(); wo->K = A; wo->N = E; wo->ggml_type = BQ_TYPE_Q5_K; wo->raw = reg("wo", (size_t)E * (A / 256) * 176);
+        bq_weight* wg = new bq_weight(); wg->K = E; wg->N = FF; wg->ggml_type = BQ_TYPE_Q5_K; wg->raw = reg("wg", (size_t)FF * (E / 256) * 176);
+        bq_weight* wu = new bq_weight(); *wu = *wg; wu->raw = reg("wu", (size_t)FF * (E / 256) * 176);
+        bq_weight* wd = new bq_weight(); wd->K = FF; wd->N = E; wd->ggml_type = BQ_TYPE_Q6_K; wd->raw = reg("wd", (size_t)E * (FF / 256) * 210);
+        bq_decode_block& a = blocks[2 * l];
+        a.kind = BQ_BLOCK_ATTN; a.norm_before = l == 0; a.norm_after = 0;
+        a.alpha = (float*)reg("alpha_a", 4 * E);
+        a.qkv = qw; a.n_qkv = 4; a.qkv_out = outs;
+        a.attn_out = (float*)reg("attn_out", 4 * A); a.attn_gate = outs[2]; a.sgate = (float*)reg("sgate", 4 * A); a.n_attn = A;
+        a.o = wo;
+        bq_decode_block& f = blocks[2 * l + 1];
+        f.kind = BQ_BLOCK_FFN; f.norm_before = 0; f.norm_after = l == 1;
+        f.alpha = (float*)reg("alpha_f", 4 * E);
+        f.gate = wg; f.up = wu; f.down = wd;
+        f.s_gate = (float*)reg("sg", 4 * FF); f.s_up = (float*)reg("su", 4 * FF); f.n_ff = FF;
+    }
+    bq_decode_step st;
+    memset(&st, 0, sizeof(st));
+    st.blocks = blocks; st.n_embd = E;
+    st.x = (float*)reg("x", 4 * E); st.input_h = (float*)reg("input_h", 4 * E);
+    st.xq = (int8_t*)reg("xq", FF); st.xd = (float*)reg("xd", FF / 8); st.xsum = (int32_t*)reg("xsum", FF / 8);
+    st.proj = (float*)reg("proj", 4 * E); st.ffn_g = (float*)reg("fg", 4 * FF); st.ffn_u = (float*)reg("fu", 4 * FF);
+    st.head_q8s = reg("head", (size_t)V * E / 256 * 272); st.head_rs = (float*)reg("rs", 4 * V); st.vocab = V;
+    st.logits = (float*)reg("logits", 4 * V);
+    float* xalt = (float*)reg("x_alt", 4 * E);
+    for (int fold = 0; fold <= 2; ++fold)
+        for (int nb = 1; nb <= 4; ++nb) {
+            st.fold = fold; st.n_blocks = nb; st.x_alt = fold == 2 ? xalt : nullptr;
+            g_calls = 0;
+            const int bad0 = g_bad;
+            const int r = bq_decode_enqueue(&st, nullptr);
+            if (r) { printf("  returned %d\n", r); g_bad++; }
+            printf("fold %d blocks %d calls %d bad %d\n", fold, nb, g_calls, g_bad - bad0);
+        }
+    printf("bad = %d\n", g_bad);
+    return g_bad != 0;
+}

@@ -1,0 +1,46 @@
+"""The decode step's host logic on the CPU: bq_decode.hip built for the host
+alone and linked against recorders of every entry point it calls
+(tests/host/decode_mock.cpp).  For the two-layer model of the GPU decode tests
+(a Q6_K v part in the QKV, norm_before on the first block, norm_after on the
+last) and every fold mode and block count, each pointer a call receives must
+lie inside a buffer with room for what that call touches, no fused call may
+write a row that its workgroups also read, and the 4-block step issues the
+expected number of launches: 21 (fold 0), 17 (fold 1: the gate norm in O, the
+silu*mul in the gate+up epilogue, its norm in down) and 16 (fold 2: also the
+FFN block's residual update in the next QKV GEMV)."""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _hipcc():
+    for p in ("/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if p and os.path.exists(p):
+            return p
+    return None
+
+
+def test_decode_call_sequence(tmp_path):
+    hipcc = _hipcc()
+    if hipcc is None:
+        pytest.skip("hipcc not found")
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROOT, "bruce-engine_amd", "csrc")]
+    flags = ["--offload-host-only", "-std=c++17", "-O1"]
+    dec, mock, exe = tmp_path / "dec.o", tmp_path / "mock.o", tmp_path / "mock"
+    subprocess.run([hipcc, *flags, *inc, "-c", os.path.join(ROOT, "bruce-engine_amd", "csrc", "bq_decode.hip"),
+                    "-o", str(dec)], check=True, capture_output=True)
+    subprocess.run([hipcc, *flags, *inc, "-c", os.path.join(ROOT, "tests", "host", "decode_mock.cpp"),
+                    "-o", str(mock)], check=True, capture_output=True)
+    subprocess.run([hipcc, str(dec), str(mock), "-o", str(exe)], check=True, capture_output=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60).stdout
+    runs = {(int(f), int(b)): (int(c), int(bad))
+            for f, b, c, bad in re.findall(r"fold (\d) blocks (\d) calls (\d+) bad (\d+)", out)}
+    assert len(runs) == 12, out
+    assert all(bad == 0 for _, bad in runs.values()), out
+    assert runs[(0, 4)][0] == 21 and runs[(1, 4)][0] == 17 and runs[(2, 4)][0] == 16, runs
+    assert "bad = 0" in out
