@@ -394,9 +394,7 @@ int try_mmq_impl(float* const* ys, const bq_weight* const* ws, int nparts, int r
             pt.W[p] = ws[p]->rep;
             pt.aux[p] = ws[p]->rep_min;
         }
-        hipError_t e = launch_fill_xdh(xd, xsum, rows * (K / 32), xdh, s);
-        if (e != hipSuccess) return from_hip(e);
-        return from_hip(launch_mmq_q5k_144(pt, rows, K, xq, xd, xdh, s, t_dev->cus, wf, wn));
+        return from_hip(launch_mmq_q5k_144(pt, rows, K, xq, xd, xsum, xdh, s, t_dev->cus, wf, wn));
     }
     for (int p = 0; p < nparts; ++p) pt.W[p] = ws[p]->raw;
     return from_hip(launch_mmq_q5k_raw(pt, rows, K, xq, xd, xsum, s, t_dev->cus, wf, wn));

@@ -606,11 +606,29 @@ BQ_DEV void mmq144_stage_any(const SmemStage<TM>& sb, f32x16 (&acc)[TileGeo<TM>:
         mmq144_stage<TM>(sb, acc, n0, t0, l32, lh);
 }
 
-template <int TM>
+// Eight consecutive xdh values half(xd * xsum) of one token row.  The
+// product is rounded to fp32 first: the empty asm keeps the compiler from
+// fusing the multiply and the fp16 conversion into one single-rounding
+// v_fma_mix, and, not being volatile, it does not order the batch's loads.
+BQ_DEV f16x8 xdh8(const float* __restrict__ xd, const int32_t* __restrict__ xs) {
+    const f32x4 d0 = *(const f32x4*)xd, d1 = *(const f32x4*)(xd + 4);
+    const i32x4 s0 = *(const i32x4*)xs, s1 = *(const i32x4*)(xs + 4);
+    f16x8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float p = (i < 4 ? d0[i] : d1[i - 4]) * (float)(i < 4 ? s0[i] : s1[i - 4]);
+        asm("" : "+v"(p));
+        h[i] = (_Float16)p;
+    }
+    return h;
+}
+
+// XI: the tile forms xdh itself from xd and xsum (32-token tile only)
+template <int TM, bool XI = false>
 __global__ void __launch_bounds__(256, TM == 32 ? 3 : 2)
 k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __restrict__ xq,
-           const float* __restrict__ xd, const uint16_t* __restrict__ xdh, int ksplit, float* __restrict__ part,
-           TailSplit ts) {
+           const float* __restrict__ xd, const int32_t* __restrict__ xsum, const uint16_t* __restrict__ xdh,
+           int ksplit, float* __restrict__ part, TailSplit ts) {
     using G = TileGeo<TM>;
     __shared__ __attribute__((aligned(16))) SmemStage<TM> sm0;
     __shared__ __attribute__((aligned(16))) SmemStage<TM> sm1;
@@ -647,10 +665,15 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
     // min term: sum_g f16(Dm[n][g]) * f16(xdh[m][g]) on fp16 MFMA, K/32 % 16 == 0
-    // (the first K slice only).  The operands of up to kMinBatch 16-group
-    // chunks are loaded before the first of their MFMAs, so a tile waits for
-    // one global-load latency per batch instead of one per chunk (the MFMA
-    // order, and so the sum, is the chunk order either way).
+    // (the first K slice only).  xdh is filled by k_fill_xdh before the
+    // launch, except for calls of at most kXdhInlineRows rows (32-token tile
+    // only, XI), where that launch is a tenth of the call: there each
+    // tile forms xdh[m][g] = half(xd * xsum) itself, rounded as k_fill_xdh
+    // rounds it (bruce.cu:6598-6602: to fp32, then to fp16).  The
+    // operands of up to kMinBatch 16-group chunks are loaded before the first
+    // of their MFMAs, so a tile waits for one global-load latency per batch
+    // instead of one per chunk (the MFMA order, and so the sum, is the chunk
+    // order either way).
     if (kc == 0) {
         constexpr int kMinBatch = 6;
         const uint16_t* __restrict__ Dm = (const uint16_t*)pt.aux[p];
@@ -667,7 +690,10 @@ k_mmq_w144(PartTable pt, int ntm, int ntn, int rows, int K, const int8_t* __rest
 #pragma unroll
                 for (int mt = 0; mt < G::MT; ++mt) {
                     const int m = min(m0 + t0 + mt * 32 + l32, rows - 1);
-                    b[c][mt] = *(const f16x8*)(xdh + (size_t)m * nb + g + 8 * lh);
+                    if constexpr (XI)
+                        b[c][mt] = xdh8(xd + (size_t)m * nb + g + 8 * lh, xsum + (size_t)m * nb + g + 8 * lh);
+                    else
+                        b[c][mt] = *(const f16x8*)(xdh + (size_t)m * nb + g + 8 * lh);
                 }
             }
 #pragma unroll
@@ -1110,26 +1136,38 @@ size_t mmq_tail_ws_floats(int rows, int K, int ntot, int cus) {
     return need;
 }
 
-template <int TM>
+// Up to this many rows the 32-token W144 tile forms the min term's xdh
+// operand itself instead of a k_fill_xdh launch filling it first (9216 x
+// 3072: 16 / 32 rows 0.7-1.4 / 0.6-0.8 us faster per call, 48-95 rows
+// level; at 512 rows, with 16x the tiles each re-forming the operand, 9 us
+// slower).
+constexpr int kXdhInlineRows = 64;
+
+template <int TM, bool XI>
 static hipError_t launch_w144_tm(const PartTable& pt, int ntm, int ntn, int ks, const TailSplit& ts, int rows,
-                                 int K, const int8_t* xq, const float* xd, const uint16_t* xdh, hipStream_t st,
-                                 float* ws) {
+                                 int K, const int8_t* xq, const float* xd, const int32_t* xsum,
+                                 uint16_t* xdh, hipStream_t st, float* ws) {
+    if (!XI) {
+        const hipError_t e = launch_fill_xdh(xd, xsum, rows * (K / 32), xdh, st);
+        if (e != hipSuccess) return e;
+    }
     if (ts.k > 1) {
-        launch_kernel(k_mmq_w144<TM>, dim3(ts.gridfull + ts.nleft * ts.k), dim3(256), 0, st, pt, ntm, ntn, rows, K,
-                      xq, xd, xdh, 1, ws, ts);
+        launch_kernel(k_mmq_w144<TM, XI>, dim3(ts.gridfull + ts.nleft * ts.k), dim3(256), 0, st, pt, ntm, ntn, rows, K,
+                      xq, xd, xsum, xdh, 1, ws, ts);
         const size_t n4 = (size_t)ts.nleft * TM * (kTN / 4);
         launch_kernel(k_sum_tail<TM>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (const float*)ws, pt,
                       ntm, rows, ts);
         return hipGetLastError();
     }
     const dim3 grid(mmq_grid(ntm, ntn).x, ks);
-    launch_kernel(k_mmq_w144<TM>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xdh, ks, ws, ts);
+    launch_kernel(k_mmq_w144<TM, XI>, grid, dim3(256), 0, st, pt, ntm, ntn, rows, K, xq, xd, xsum, xdh, ks, ws, ts);
     if (ks > 1) return sum_splits(pt, ks, rows, ws, st);
     return hipGetLastError();
 }
 
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                              const uint16_t* xdh, hipStream_t st, int cus, float* ws, size_t ws_floats) {
+                              const int32_t* xsum, uint16_t* xdh, hipStream_t st, int cus, float* ws,
+                              size_t ws_floats) {
     const int tm = mmq_tile_rows(rows, K, ntotal(pt), false, ws ? ws_floats : 0, 1.115f, true, cus);
     const int ntm = (rows + tm - 1) / tm;
     const int ntn = ntile_count(pt);
@@ -1137,8 +1175,10 @@ hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, c
     const int ks = mmq_ksplit(rows, K, ntotal(pt), false, ws ? ws_floats : 0, tm, cus);
     const TailSplit ts = ks > 1 ? TailSplit{}
                                 : mmq_tail_split(ntm * ntn, K >> 8, ws ? ws_floats : 0, tm, tm == 32 ? 1.115f : 1.f, cus);
-    if (tm == 32) return launch_w144_tm<32>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xdh, st, ws);
-    return launch_w144_tm<128>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xdh, st, ws);
+    if (tm == 32 && rows <= kXdhInlineRows)
+        return launch_w144_tm<32, true>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xsum, xdh, st, ws);
+    if (tm == 32) return launch_w144_tm<32, false>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xsum, xdh, st, ws);
+    return launch_w144_tm<128, false>(pt, ntm, ntn, ks, ts, rows, K, xq, xd, xsum, xdh, st, ws);
 }
 
 template <int TM>

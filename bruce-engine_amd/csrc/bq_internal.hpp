@@ -86,7 +86,7 @@ hipError_t launch_mmq_q5k_raw(PartTable pt, int rows, int K, const int8_t* xq, c
                               const int32_t* xsum, hipStream_t st, int cus, float* ws = nullptr,
                               size_t ws_floats = 0);
 hipError_t launch_mmq_q5k_144(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
-                              const uint16_t* xdh, hipStream_t st, int cus, float* ws = nullptr,
+                              const int32_t* xsum, uint16_t* xdh, hipStream_t st, int cus, float* ws = nullptr,
                               size_t ws_floats = 0);
 hipError_t launch_mmq_q6k(PartTable pt, int rows, int K, const int8_t* xq, const float* xd,
                           hipStream_t st, int cus, float* ws = nullptr, size_t ws_floats = 0);

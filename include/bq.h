@@ -235,7 +235,9 @@ int bq_gemm_q6k_mma(float* y, const bq_weight* w, int rows, const int8_t* xq, co
  * whichever a work estimate for the launch's shape favours; the 8-row chunks
  * stream
  * the weights once per chunk); otherwise 8-row chunks of the multi-row
- * kernels.  (The reference sends rows 9..95 to a 64x64 MMA tile.)  Never returns
+ * kernels.  (The reference sends rows 9..95 to a 64x64 MMA tile.)  The W144
+ * tier needs xdh as bq_try_mmq does, but at 9..64 rows its tile forms the
+ * min term's half(xd*xsum) itself and xdh is not written.  Never returns
  * BQ_UNSUPPORTED for a Q5_K/Q6_K weight with K % 256 == 0. */
 int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd,
               const int32_t* xsum, uint16_t* xdh, void* work, size_t work_bytes, bq_stream_t st);

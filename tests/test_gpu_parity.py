@@ -535,6 +535,35 @@ def test_mmq_w144_ksplit(bq, oracle, rows):
     assert oracle.normwise_err(host(y1), ref) < TOL
 
 
+@pytest.mark.parametrize("rows", [9, 33, 96, 128, 129, 300])
+def test_w144_min_term_xdh(bq, oracle, rows):
+    """The W144 tier's fp16 min term alone (every super-block's d = 0, so
+    y = sum_g f16(Dm[n][g]) * f16(xdh[m][g])), through bq_gemm_b: up to 64
+    rows the 32-token tile forms xdh = half(xd * xsum) itself, above it
+    k_fill_xdh fills it first (bruce.cu:6598-6602).  Against the product of
+    the oracle's Dm and xdh in float64, at 2e-6 of the output's largest
+    value: one xdh value rounded the other way (2^-11 of its term) fails it."""
+    import torch
+    K, N = 1024, 256
+    raw = weights(1450 + rows, N, K, "q5k").copy()
+    raw.reshape(N, K // 256, 176)[:, :, 0:2] = 0          # d = 0: no sc*q term
+    _, (xq, xd, xs) = acts(1451 + rows, rows, K)
+    gq, gd, gs = _xq_dev(xq, xd, xs)
+    g5 = dev(raw)
+    w144, dm = bq.repack_q5k(g5, K, N)
+    xdh = torch.empty((rows, K // 32), dtype=torch.int16, device="cuda")
+    y = torch.full((rows, N), float("nan"), device="cuda")
+    bq.gemm_b(y, bq.make_weight(g5, bq.TYPE_Q5_K, K, N, rep=w144, rep_min=dm), rows, gq, gd, gs, xdh)
+    torch.cuda.synchronize()
+    _, rdm = oracle.repack_q5k_144(raw, K)
+    hx = oracle.fill_xdh(xd, xs).view(np.float16).astype(np.float64).reshape(rows, K // 32)
+    hd = np.asarray(rdm).view(np.float16).astype(np.float64).reshape(N, K // 32)
+    ref = hx @ hd.T
+    yh = host(y).astype(np.float64)
+    assert np.isfinite(yh).all()
+    assert np.abs(yh - ref).max() <= 2e-6 * np.abs(ref).max()
+
+
 # ---------------------------------------------------------------- dispatcher
 @pytest.mark.parametrize("rows", [3, 8, 9, 12, 16, 17, 20, 27, 28, 43, 60, 130, 1536, 1537])
 def test_gemm_b_dispatch(bq, oracle, rows):
