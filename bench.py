@@ -275,6 +275,105 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
                                     **verify}}
 
 
+def prompt_chunk(bq, synth, torch, w_gate, w_up, w_down, steps=10, warmup=2):
+    """A prompt chunk through the library's step (bq_decode_graph with rows = M
+    > 8): the reference's forward_batch_impl as bruce_prefill_chunk calls it
+    (bruce.cu:8274-8291, :7610-7843), here 4 layers of config 5's shapes (QKV
+    one Q5_K 5120x3072, O Q5_K 3072x4096, gate/up Q5_K 9216x3072 with their
+    W144 repacks; down Q6_K 3072x9216 with its W160 repack), each layer its
+    own weight copy, no logits (a chunk that is not the prompt's last), at M =
+    512 (the reference's largest chunk, MBUF) and 2048 (config 4's M).  Per
+    layer: the whole step (row producers, xdh fills, the prefill GEMMs and
+    their K-split sums; attention excluded, aout a fixed input) against the
+    same GEMM calls alone (bq_gemm_b / bq_gemm_b_fused, eager, events)."""
+    NL = 4
+    w_qkv = synth.quantize_q5k(synth.gaussian(SEED + 9, (NQKV, K), 0.02))
+    w_o = synth.quantize_q5k(synth.gaussian(SEED + 10, (K, KO), 0.02))
+    keep, ws = [], []
+    for l in range(NL):
+        lw = []
+        for a, kk, n in ((w_qkv, K, NQKV), (w_o, KO, K), (w_gate, K, FF), (w_up, K, FF)):
+            g = torch.from_numpy(a).cuda()
+            rep, dm = bq.repack_q5k(g, kk, n)
+            keep += [g, rep, dm]
+            lw.append(bq.make_weight(g, bq.TYPE_Q5_K, kk, n, rep=rep, rep_min=dm))
+        g = torch.from_numpy(w_down).cuda()
+        rep = bq.repack_q6k(g, FF, K)
+        keep += [g, rep]
+        lw.append(bq.make_weight(g, bq.TYPE_Q6_K, FF, K, rep=rep))
+        ws.append(lw)
+    gen = torch.Generator(device="cuda").manual_seed(SEED + 16)
+    vec = lambda n: torch.rand(n, generator=gen, device="cuda") * 0.5 + 0.25
+    alpha, alpha2, sgate, sg, su = vec(K), vec(K), vec(KO), vec(FF), vec(FF)
+    res = {}
+    for M in (512, 2048):
+        x = torch.randn((M, K), generator=gen, device="cuda")
+        aout = torch.randn((M, KO), generator=gen, device="cuda")
+        qkv, proj = torch.empty((M, NQKV), device="cuda"), torch.empty((M, K), device="cuda")
+        fg, fu = torch.empty((M, FF), device="cuda"), torch.empty((M, FF), device="cuda")
+        xq = torch.empty(M * FF, dtype=torch.int8, device="cuda")
+        xd = torch.empty(M * FF // 32, device="cuda")
+        xs = torch.empty(M * FF // 32, dtype=torch.int32, device="cuda")
+        xdh = torch.empty(M * FF // 32, dtype=torch.int16, device="cuda")
+        q = bq.quantize_q8(x)
+        xq[:M * K].copy_(q[0].view(-1)); xd[:M * K // 32].copy_(q[1].view(-1)); xs[:M * K // 32].copy_(q[2].view(-1))
+        wb = max(bq.workspace_bytes(M, kk, n) for kk, n in ((K, NQKV), (KO, K), (K, 2 * FF), (FF, K)))
+        work = torch.empty(max(wb, 16) // 4, device="cuda")
+        qout = (ctypes.c_void_p * 1)(qkv.data_ptr())
+        blocks = (bq.DecodeBlock * (2 * NL))()
+        for l in range(NL):
+            a, f = blocks[2 * l], blocks[2 * l + 1]
+            a.kind, a.alpha = bq.BLOCK_ATTN, alpha.data_ptr()
+            a.qkv, a.n_qkv, a.qkv_out = ctypes.pointer(ws[l][0]), 1, qout
+            a.attn_out, a.attn_gate, a.sgate, a.n_attn = aout.data_ptr(), qkv.data_ptr(), sgate.data_ptr(), KO
+            a.o = ctypes.pointer(ws[l][1])
+            f.kind, f.alpha = bq.BLOCK_FFN, alpha2.data_ptr()
+            f.gate, f.up, f.down = ctypes.pointer(ws[l][2]), ctypes.pointer(ws[l][3]), ctypes.pointer(ws[l][4])
+            f.s_gate, f.s_up, f.n_ff = sg.data_ptr(), su.data_ptr(), FF
+        blocks[2 * NL - 1].norm_after = 1
+        stp = bq.DecodeStep()
+        stp.n_blocks, stp.blocks, stp.n_embd, stp.fold, stp.rows = 2 * NL, blocks, K, 0, M
+        stp.x, stp.xq, stp.xd, stp.xsum = x.data_ptr(), xq.data_ptr(), xd.data_ptr(), xs.data_ptr()
+        stp.proj, stp.ffn_g, stp.ffn_u = proj.data_ptr(), fg.data_ptr(), fu.data_ptr()
+        stp.xdh, stp.work, stp.work_bytes = xdh.data_ptr(), work.data_ptr(), work.numel() * 4
+        dg = bq.DecodeGraph(stp)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(warmup):
+            dg.launch()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            dg.launch()
+        e1.record()
+        torch.cuda.synchronize()
+        step_ms = e0.elapsed_time(e1) / steps / NL
+        dg.close()
+
+        def gemms():
+            for l in range(NL):
+                bq.gemm_b(qkv, ws[l][0], M, xq, xd, xs, xdh, work)
+                bq.gemm_b(proj, ws[l][1], M, xq, xd, xs, xdh, work)
+                bq.gemm_b_fused([fg, fu], [ws[l][2], ws[l][3]], M, xq, xd, xs, xdh, work)
+                bq.gemm_b(proj, ws[l][4], M, xq, xd, xs, xdh, work)
+        for _ in range(warmup):
+            gemms()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            gemms()
+        e1.record()
+        torch.cuda.synchronize()
+        gemm_ms = e0.elapsed_time(e1) / steps / NL
+        ops = 2 * M * (K * (NQKV + 2 * FF) + KO * K + FF * K)
+        res[f"M{M}"] = {"ms_per_layer": round(step_ms, 4), "gemms_ms_per_layer": round(gemm_ms, 4),
+                        "rest_ms_per_layer": round(step_ms - gemm_ms, 4),
+                        "tops": round(ops / step_ms / 1e9, 1), "gemm_tops": round(ops / gemm_ms / 1e9, 1),
+                        "tokens_per_s_32_layers": round(M / (32 * step_ms / 1e3), 1)}
+        del x, aout, qkv, proj, fg, fu, xq, xd, xs, xdh, work, dg
+    del keep
+    return {"what": " ".join(prompt_chunk.__doc__.split()), **res}
+
+
 def q8s_head(B, bq, torch, sp, ptr, steps=50):
     """Q8_0 logits head (bruce.cu:4400-4449): Q8S 131072 x K GEMV, rows 1 and 8,
     at the BASELINE hidden size (K = 3072) and the reference model's (K = 2560).
@@ -571,6 +670,8 @@ def main():
                     help="only config 5 (the whole-stack decode and the decode-step chains); prints its JSON object")
     ap.add_argument("--no-stack", action="store_true",
                     help="skip config 5 (the whole-stack decode and the decode-step graphs), e.g. for counter runs")
+    ap.add_argument("--chunk-only", action="store_true",
+                    help="only the prompt-chunk step (bq_decode_graph over 512 / 2048 rows); prints its JSON object")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the prefill GEMMs of config 4 and the Q6_K GEMM (for counter profiles); "
                          "prints their JSON object")
@@ -655,6 +756,9 @@ def main():
     if args.gemm_only:
         print(json.dumps({"gemm": gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out)}), flush=True)
         return
+    if args.chunk_only:
+        print(json.dumps({"prompt_chunk": prompt_chunk(bq, synth, torch, w_gate, w_up, w_down)}), flush=True)
+        return
     if args.stack_only:
         print(json.dumps({"config5_whole_stack": whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr)}),
               flush=True)
@@ -688,7 +792,7 @@ def main():
     achieved = gbs(gu_bytes, gu_ms)
 
     gemm_obj, rows_res, c1_obj, stack_obj, q8s_obj, norm_obj, load_obj = None, None, None, None, None, None, None
-    ceil_obj, probe_obj = None, None
+    ceil_obj, probe_obj, chunk_obj = None, None, None
     if not args.decode_only:
         gemm_obj = gemm_section(B, bq, synth, torch, g_gate, g_down, sp, ptr, out)
         ceil_obj = stream_ceiling(B, torch, sp)
@@ -725,6 +829,9 @@ def main():
         # ------------------------------------------------------------ config 5: whole-stack token
         if not args.no_stack:
             stack_obj = whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr)
+
+        # ------------------------------------------------------------ prompt chunk (prefill step)
+        chunk_obj = prompt_chunk(bq, synth, torch, w_gate, w_up, w_down)
 
         # ------------------------------------------------------------ Q8_0 logits head
         q8s_obj = q8s_head(B, bq, torch, sp, ptr)
@@ -776,6 +883,7 @@ def main():
         "gemv_config1_3072x3072": c1_obj,
         "gemv_config3_9216x3072": rows_res,
         "config5_whole_stack": stack_obj,
+        "prompt_chunk": chunk_obj,
         "q8s_logits_head": q8s_obj,
         "q8_producers": norm_obj,
         "gguf_load": load_obj,

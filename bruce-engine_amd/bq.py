@@ -91,7 +91,8 @@ class DecodeStep(ctypes.Structure):
                 ("attention", ATTN_HOOK), ("user", ctypes.c_void_p),
                 ("head_q8s", ctypes.c_void_p), ("head_rs", ctypes.c_void_p), ("head", ctypes.POINTER(Weight)),
                 ("vocab", ctypes.c_int), ("logits", ctypes.c_void_p), ("rows", ctypes.c_int),
-                ("x_alt", ctypes.c_void_p)]
+                ("x_alt", ctypes.c_void_p), ("xdh", ctypes.c_void_p), ("work", ctypes.c_void_p),
+                ("work_bytes", ctypes.c_size_t)]
 
 
 _lib = None

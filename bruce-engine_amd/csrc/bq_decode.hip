@@ -7,7 +7,9 @@
 // rows 2..8 its speculative-verify form, forward_batch_impl over `rows` tokens
 // with all logits (:7610-7843), captured once per row count as
 // capture_verify_graphs does (:7877-7900) and replayed by verify_launch
-// (:7862-7875).  The reference's attention kernels (:7940-7970, :7716-7737)
+// (:7862-7875); with more rows a prompt chunk, forward_batch_impl as
+// bruce_prefill_chunk calls it (:8274-8291: the MMQ GEMMs, the last row's
+// logits only).  The reference's attention kernels (:7940-7970, :7716-7737)
 // are outside this library: a caller hook enqueues them between the QKV
 // projection and the gate norm, so they land in the same graph.
 #include <string.h>
@@ -28,8 +30,8 @@ bool fold2_ok(const bq_decode_step* s) {
 
 bool dims_ok(const bq_decode_step* s) {
     return s && s->n_blocks >= 0 && (s->n_blocks == 0 || s->blocks) && s->x && s->xq && s->xd && s->xsum &&
-           s->proj && s->n_embd > 0 && (s->n_embd % 32) == 0 && s->rows >= 0 && s->rows <= BQ_MAX_ROWS &&
-           s->fold >= 0 && s->fold <= 2 && (s->fold < 2 || fold2_ok(s));
+           s->proj && s->n_embd > 0 && (s->n_embd % 32) == 0 && s->rows >= 0 && s->rows <= BQ_MAX_STEP_ROWS &&
+           s->fold >= 0 && s->fold <= 2 && (s->fold < 2 || fold2_ok(s)) && (s->work || !s->work_bytes);
 }
 
 // fold = 2: the resid -> q8 (k_resid :8017) of a block followed by an
@@ -64,11 +66,27 @@ int flush(const bq_decode_step* s, Resid& rs, bq_stream_t st) {
 int rows_of(const bq_decode_step* s) { return s->rows > 0 ? s->rows : 1; }
 
 // y [rows][N] of a k-quant weight over the q8 rows: the single-row GEMV at one
-// row (launch_gemv, :7982 / :8008), the multi-row kernels through the
-// prompt-batch dispatcher at 2..8 (launch_gemm_b, :7750 / :7800)
+// row (launch_gemv, :7982 / :8008), the prompt-batch dispatcher above
+// (launch_gemm_b, :7750 / :7800: the multi-row kernels at 2..8 rows, the MMQ
+// GEMMs with the step's xdh and workspace above)
 int gemv_rows_of(float* y, const bq_weight* w, int rows, const bq_decode_step* s, bq_stream_t st) {
     if (rows == 1) return bq_gemv(y, w, s->xq, s->xd, s->xsum, st);
-    return bq_gemm_b(y, w, rows, s->xq, s->xd, s->xsum, nullptr, nullptr, 0, st);
+    return bq_gemm_b(y, w, rows, s->xq, s->xd, s->xsum, s->xdh, s->work, s->work_bytes, st);
+}
+
+// The Q5_K parts sharing the q8 rows in one launch where the kernels allow it:
+// the fused GEMV / verify kernel up to 8 rows (launch_verify_fused), one MMQ
+// launch over the parts above (launch_gemm_b_fused, :7421-7426); otherwise
+// one launch per part
+int parts_rows_of(float* const* ys, const bq_weight* const* ws, int n, int rows, const bq_decode_step* s,
+                  bq_stream_t st) {
+    if (rows > BQ_MAX_ROWS)
+        return bq_gemm_b_fused(ys, ws, n, rows, s->xq, s->xd, s->xsum, s->xdh, s->work, s->work_bytes, st);
+    const int r = bq_verify_fused(ys, ws, n, rows, s->xq, s->xd, s->xsum, 0, st);
+    if (r != BQ_UNSUPPORTED) return r;
+    for (int p = 0; p < n; ++p)
+        if (int e = gemv_rows_of(ys[p], ws[p], rows, s, st)) return e;
+    return BQ_OK;
 }
 
 // one attention block: bruce.cu:7915-7993 (QKV, attention, gate norm, O);
@@ -105,13 +123,8 @@ int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, int ro
         }
     }
     if (int e = flush(s, rs, st)) return e;
-    if (nf > 0 && !qkv_done) {
-        const int r = bq_verify_fused(yp, wp, nf, rows, s->xq, s->xd, s->xsum, 0, st);
-        if (r != BQ_OK && r != BQ_UNSUPPORTED) return r;
-        if (r == BQ_UNSUPPORTED)
-            for (int p = 0; p < nf; ++p)
-                if (int e = gemv_rows_of(yp[p], wp[p], rows, s, st)) return e;
-    }
+    if (nf > 0 && !qkv_done)
+        if (int e = parts_rows_of(yp, wp, nf, rows, s, st)) return e;
     for (int p = 0; p < b.n_qkv; ++p)
         if (b.qkv[p].ggml_type != BQ_TYPE_Q5_K)
             if (int e = gemv_rows_of(b.qkv_out[p], &b.qkv[p], rows, s, st)) return e;
@@ -148,12 +161,7 @@ int ffn_block(const bq_decode_step* s, const bq_decode_block& b, int rows, Resid
     if (!s->ffn_u) return BQ_EINVAL;
     float* y2[2] = {s->ffn_g, s->ffn_u};
     const bq_weight* p2[2] = {b.gate, b.up};
-    int r = bq_verify_fused(y2, p2, 2, rows, s->xq, s->xd, s->xsum, 0, st);
-    if (r == BQ_UNSUPPORTED) {
-        if ((r = gemv_rows_of(s->ffn_g, b.gate, rows, s, st))) return r;
-        r = gemv_rows_of(s->ffn_u, b.up, rows, s, st);
-    }
-    if (r) return r;
+    if (int r = parts_rows_of(y2, p2, 2, rows, s, st)) return r;
     if (int e = bq_silu_mul_norm_q8(nullptr, s->ffn_g, s->ffn_u, b.s_gate, b.s_up, rows, b.n_ff, s->xq, s->xd,
                                     s->xsum, st))
         return e;
@@ -206,13 +214,15 @@ int bq_decode_enqueue(const bq_decode_step* s, bq_stream_t st) {
         }
     }
     if (int e = flush(s, rs, st)) return e;
-    // logits of every row from the q8 rows of x (:8026-8032; rows: launch_logits_b :7832)
-    if (s->head_q8s) {
-        if (!s->logits) return BQ_EINVAL;
-        return bq_gemv_q8s(s->logits, s->head_q8s, s->xq, s->xd, n, s->vocab, rows, s->head_rs, st);
-    }
+    // logits from the q8 rows of x: every row up to 8 rows (:8026-8032; rows:
+    // launch_logits_b :7832), the last row of a prompt chunk (:7833-7836)
+    if ((s->head_q8s || s->head) && !s->logits) return BQ_EINVAL;
+    const int lr = rows > BQ_MAX_ROWS ? 1 : rows;
+    const size_t off = (size_t)(rows - lr) * n;
+    if (s->head_q8s)
+        return bq_gemv_q8s(s->logits, s->head_q8s, s->xq + off, s->xd + off / 32, n, s->vocab, lr, s->head_rs, st);
     if (s->head) {
-        if (!s->logits) return BQ_EINVAL;
+        if (lr == 1) return bq_gemv(s->logits, s->head, s->xq + off, s->xd + off / 32, s->xsum + off / 32, st);
         return gemv_rows_of(s->logits, s->head, rows, s, st);
     }
     return BQ_OK;

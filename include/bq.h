@@ -42,7 +42,7 @@ typedef struct ihipStream_t* bq_stream_t; /* == hipStream_t; NULL = default stre
 
 enum { BQ_OK = 0, BQ_UNSUPPORTED = 1, BQ_EINVAL = 2, BQ_ETOOBIG = 3 };
 enum { BQ_TYPE_Q5_K = 13, BQ_TYPE_Q6_K = 14 }; /* GGML type ids (gguf.h:29-30) */
-enum { BQ_MAX_PARTS = 4, BQ_MAX_ROWS = 8 };
+enum { BQ_MAX_PARTS = 4, BQ_MAX_ROWS = 8, BQ_MAX_STEP_ROWS = 8192 };
 
 /* Weight descriptor.  Mirrors `struct TensorW { d, dp, dm, type, K, N }`
  * (bruce.cu:78): raw = GGUF blocks, rep = W144 (Q5_K) or W160 (Q6_K) repack or
@@ -355,7 +355,12 @@ int bq_gguf_load(bq_gguf* g, int64_t i, void* raw, void* rep, void* rep_min, bq_
  * `rows` tokens with every row's logits (forward_batch_impl :7610-7843 with
  * all_logits), captured once per row count as capture_verify_graphs does
  * (:7877-7900) and replayed by verify_launch (:7862-7875); the argmax that
- * follows there is the caller's.  Per block, in the reference's order:
+ * follows there is the caller's.  With rows = 9..BQ_MAX_STEP_ROWS it is a
+ * prompt chunk, forward_batch_impl as bruce_prefill_chunk calls it
+ * (:8274-8291; the reference's chunks are at most MBUF = 512 rows, :1058):
+ * the projections run on the prefill GEMMs (bq_gemm_b_fused / bq_gemm_b with
+ * the step's xdh and work), and only the last row's logits are computed
+ * (:7833-7836), into logits [vocab].  Per block, in the reference's order:
  *   norm_before: x = norm(x + input_h) -> q8                      (k_add_norm :7914)
  *   attention block: QKV GEMV over the q8 rows (bq_verify_fused over the Q5_K
  *     parts, single-row / multi-row GEMVs for others), the caller's attention
@@ -380,9 +385,10 @@ int bq_gguf_load(bq_gguf* g, int64_t i, void* raw, void* rep, void* rep_min, bq_
  * Every buffer holds `rows` rows, row-major: x, input_h, proj
  * [rows][n_embd]; attn_out, attn_gate [rows][n_attn]; qkv_out[p] [rows][N_p];
  * ffn_g, ffn_u [rows][n_ff] (ffn_u unused when fold >= 1); logits
- * [rows][vocab]; xq/xd/xsum hold the q8 rows of the widest operand, rows x
- * max(n_embd, n_attn, n_ff) values.  x is updated in place.  A graph captures the pointers and the row count it is
- * created with: replays read and write the same buffers. */
+ * [rows][vocab] (a prompt chunk: [vocab]); xq/xd/xsum hold the q8 rows of the
+ * widest operand, rows x max(n_embd, n_attn, n_ff) values.  x is updated in
+ * place.  A graph captures the pointers and the row count it is created with:
+ * replays read and write the same buffers. */
 enum { BQ_BLOCK_ATTN = 0, BQ_BLOCK_FFN = 1 };
 typedef struct bq_decode_block {
     int kind;                     /* BQ_BLOCK_ATTN or BQ_BLOCK_FFN */
@@ -416,8 +422,13 @@ typedef struct bq_decode_step {
     const void* head_q8s; const float* head_rs; const bq_weight* head;  /* one of the two heads, or neither */
     int vocab;
     float* logits;
-    int rows;                     /* tokens per step, 1..8 (0 means 1) */
+    int rows;                     /* tokens per step, 1..BQ_MAX_STEP_ROWS (0 means 1) */
     float* x_alt;                 /* fold = 2: a second residual row [n_embd], not x */
+    /* rows > 8: the prefill GEMMs' xdh scratch [rows][max K/32] fp16 and K-split
+     * workspace (bq_gemm_b; NULL / 0: the raw-Q5_K tier / no split) */
+    uint16_t* xdh;
+    void* work;
+    size_t work_bytes;
 } bq_decode_step;
 /* Enqueue one token's launch sequence on st (stream-ordered, allocates nothing). */
 int bq_decode_enqueue(const bq_decode_step* s, bq_stream_t st);

@@ -56,8 +56,26 @@ int bq_gemv(float* y, const bq_weight* w, const int8_t* xq, const float* xd, con
     chk("gemv", "xd", xd, w->K / 8); if (w->ggml_type == BQ_TYPE_Q5_K) chk("gemv", "xs", xs, w->K / 8);
     return 0;
 }
-int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd, const int32_t* xs, uint16_t*, void*, size_t, bq_stream_t) {
-    ++g_calls; if (g_verbose) printf("gemm_b rows=%d\n", rows); chk("gemm_b", "y", y, 4 * w->N * rows); return 0;
+static void gemm_args(const char* call, int rows, int K, const int8_t* xq, const float* xd, const int32_t* xs,
+                      const uint16_t* xdh, const void* work, size_t work_bytes) {
+    chk(call, "xq", xq, (size_t)K * rows); chk(call, "xd", xd, (size_t)K / 8 * rows); chk(call, "xs", xs, (size_t)K / 8 * rows);
+    if (rows > BQ_MAX_ROWS && xdh) chk(call, "xdh", xdh, (size_t)K / 16 * rows);
+    if (work) chk(call, "work", work, work_bytes);
+}
+int bq_gemm_b(float* y, const bq_weight* w, int rows, const int8_t* xq, const float* xd, const int32_t* xs, uint16_t* xdh,
+              void* work, size_t work_bytes, bq_stream_t) {
+    ++g_calls; if (g_verbose) printf("gemm_b rows=%d N=%d y=%s\n", rows, w->N, nm(y));
+    chk("gemm_b", "y", y, 4 * (size_t)w->N * rows); chk("gemm_b", "w", w->raw, wbytes(w));
+    gemm_args("gemm_b", rows, w->K, xq, xd, xs, xdh, work, work_bytes);
+    return 0;
+}
+int bq_gemm_b_fused(float* const* ys, const bq_weight* const* ws, int n, int rows, const int8_t* xq, const float* xd,
+                    const int32_t* xs, uint16_t* xdh, void* work, size_t work_bytes, bq_stream_t) {
+    ++g_calls; if (g_verbose) printf("gemm_b_fused n=%d rows=%d\n", n, rows);
+    if (rows <= BQ_MAX_ROWS) { printf("  gemm_b_fused at %d rows\n", rows); g_bad++; }
+    for (int p = 0; p < n; ++p) { chk("gbf", "y", ys[p], 4 * (size_t)ws[p]->N * rows); chk("gbf", "w", ws[p]->raw, wbytes(ws[p])); }
+    gemm_args("gemm_b_fused", rows, ws[0]->K, xq, xd, xs, xdh, work, work_bytes);
+    return 0;
 }
 int bq_gemv_norm_fused(float* const* ys, const bq_weight* const* ws, int nparts, int op, float* out, const float* a,
                        const float* b, const float* c, const float* d, int8_t* xq, float* xd, int32_t* xsum, bq_stream_t) {
@@ -88,7 +106,7 @@ int bq_norm_q8(float* dst, const float* src, int rows, int n, int8_t* xq, float*
 int bq_gate_norm_q8(float* dst, const float* a, const float* g, const float* sg, int rows, int n, int8_t* xq, float* xd, int32_t* xs, bq_stream_t) { nq("gate_norm", dst, a, g, sg, 0, rows, n, xq, xd, xs); return 0; }
 int bq_silu_mul_norm_q8(float* dst, const float* g, const float* u, const float* sg, const float* su, int rows, int n, int8_t* xq, float* xd, int32_t* xs, bq_stream_t) { nq("silu_norm", dst, g, u, sg, su, rows, n, xq, xd, xs); return 0; }
 int bq_gemv_q8s(float* y, const void* w, const int8_t* xq, const float* xd, int K, int N, int rows, const float* rs, bq_stream_t) {
-    ++g_calls; if (g_verbose) printf("gemv_q8s K=%d N=%d\n", K, N); chk("q8s", "y", y, 4 * N * rows); chk("q8s", "xq", xq, K * rows); chk("q8s", "xd", xd, K / 8 * rows); return 0;
+    ++g_calls; if (g_verbose) printf("gemv_q8s K=%d N=%d rows=%d\n", K, N, rows); chk("q8s", "y", y, 4 * N * rows); chk("q8s", "xq", xq, K * rows); chk("q8s", "xd", xd, K / 8 * rows); return 0;
 }
 }
 namespace bq {
@@ -99,7 +117,7 @@ hipError_t launch_norm_q8(int op, float* out, const float* a, const float* b, co
 
 int main(int argc, char** argv) {
     g_verbose = argc > 1;
-    const int E = 3072, A = 4096, FF = 9216, V = 8192;
+    const int E = 3072, A = 4096, FF = 9216, V = 8192, R = 40;
     const int PN[4] = {A, 512, A, 512};
     bq_decode_block blocks[4];
     memset(blocks, 0, sizeof(blocks));
@@ -110,7 +128,7 @@ int main(int argc, char** argv) {
         for (int i = 0; i < 4; ++i) {
             qw[i].K = E; qw[i].N = PN[i]; qw[i].ggml_type = i == 3 ? BQ_TYPE_Q6_K : BQ_TYPE_Q5_K;
             qw[i].raw = reg("qkvw", (size_t)PN[i] * (E / 256) * (i == 3 ? 210 : 176));
-            outs[i] = (float*)reg("qkv_out", 4 * PN[i]);
+            outs[i] = (float*)reg("qkv_out", 4 * (size_t)PN[i] * R);
         }
         bq_weight* wo = new bq_weight(); wo->K = A; wo->N = E; wo->ggml_type = BQ_TYPE_Q5_K; wo->raw = reg("wo", (size_t)E * (A / 256) * 176);
         bq_weight* wg = new bq_weight(); wg->K = E; wg->N = FF; wg->ggml_type = BQ_TYPE_Q5_K; wg->raw = reg("wg", (size_t)FF * (E / 256) * 176);
@@ -120,7 +138,7 @@ int main(int argc, char** argv) {
         a.kind = BQ_BLOCK_ATTN; a.norm_before = l == 0; a.norm_after = 0;
         a.alpha = (float*)reg("alpha_a", 4 * E);
         a.qkv = qw; a.n_qkv = 4; a.qkv_out = outs;
-        a.attn_out = (float*)reg("attn_out", 4 * A); a.attn_gate = outs[2]; a.sgate = (float*)reg("sgate", 4 * A); a.n_attn = A;
+        a.attn_out = (float*)reg("attn_out", 4 * (size_t)A * R); a.attn_gate = outs[2]; a.sgate = (float*)reg("sgate", 4 * A); a.n_attn = A;
         a.o = wo;
         bq_decode_block& f = blocks[2 * l + 1];
         f.kind = BQ_BLOCK_FFN; f.norm_before = 0; f.norm_after = l == 1;
@@ -131,11 +149,11 @@ int main(int argc, char** argv) {
     bq_decode_step st;
     memset(&st, 0, sizeof(st));
     st.blocks = blocks; st.n_embd = E;
-    st.x = (float*)reg("x", 4 * E); st.input_h = (float*)reg("input_h", 4 * E);
-    st.xq = (int8_t*)reg("xq", FF); st.xd = (float*)reg("xd", FF / 8); st.xsum = (int32_t*)reg("xsum", FF / 8);
-    st.proj = (float*)reg("proj", 4 * E); st.ffn_g = (float*)reg("fg", 4 * FF); st.ffn_u = (float*)reg("fu", 4 * FF);
+    st.x = (float*)reg("x", 4 * E * R); st.input_h = (float*)reg("input_h", 4 * E * R);
+    st.xq = (int8_t*)reg("xq", FF * R); st.xd = (float*)reg("xd", FF / 8 * R); st.xsum = (int32_t*)reg("xsum", FF / 8 * R);
+    st.proj = (float*)reg("proj", 4 * E * R); st.ffn_g = (float*)reg("fg", 4 * FF * R); st.ffn_u = (float*)reg("fu", 4 * FF * R);
     st.head_q8s = reg("head", (size_t)V * E / 256 * 272); st.head_rs = (float*)reg("rs", 4 * V); st.vocab = V;
-    st.logits = (float*)reg("logits", 4 * V);
+    st.logits = (float*)reg("logits", 4 * V * 8);  // every row's logits up to 8 rows, the last row's above
     float* xalt = (float*)reg("x_alt", 4 * E);
     for (int fold = 0; fold <= 2; ++fold)
         for (int nb = 1; nb <= 4; ++nb) {
@@ -146,6 +164,24 @@ int main(int argc, char** argv) {
             if (r) { printf("  returned %d\n", r); g_bad++; }
             printf("fold %d blocks %d calls %d bad %d\n", fold, nb, g_calls, g_bad - bad0);
         }
+    // the verify step (8 rows) and a prompt chunk (R rows: the prefill GEMMs,
+    // with and without xdh / workspace)
+    uint16_t* xdh = (uint16_t*)reg("xdh", (size_t)FF / 16 * R);
+    void* work = reg("work", 1 << 20);
+    for (int c = 0; c < 3; ++c) {
+        st.fold = 0; st.n_blocks = 4; st.x_alt = nullptr;
+        st.rows = c == 0 ? 8 : R;
+        st.xdh = c == 2 ? xdh : nullptr; st.work = c == 2 ? work : nullptr; st.work_bytes = c == 2 ? 1 << 20 : 0;
+        g_calls = 0;
+        const int bad0 = g_bad;
+        const int r = bq_decode_enqueue(&st, nullptr);
+        if (r) { printf("  returned %d\n", r); g_bad++; }
+        printf("rows %d scratch %d calls %d bad %d\n", st.rows, c == 2, g_calls, g_bad - bad0);
+    }
+    st.rows = R; st.work = nullptr; st.work_bytes = 16;
+    if (bq_decode_enqueue(&st, nullptr) != BQ_EINVAL) { printf("  work_bytes without work accepted\n"); g_bad++; }
+    st.work_bytes = 0; st.rows = BQ_MAX_STEP_ROWS + 1;
+    if (bq_decode_enqueue(&st, nullptr) != BQ_EINVAL) { printf("  rows above the limit accepted\n"); g_bad++; }
     printf("bad = %d\n", g_bad);
     return g_bad != 0;
 }

@@ -7,7 +7,10 @@ lie inside a buffer with room for what that call touches, no fused call may
 write a row that its workgroups also read, and the 4-block step issues the
 expected number of launches: 21 (fold 0), 17 (fold 1: the gate norm in O, the
 silu*mul in the gate+up epilogue, its norm in down) and 16 (fold 2: also the
-FFN block's residual update in the next QKV GEMV)."""
+FFN block's residual update in the next QKV GEMV).  The 8-row verify step and
+a 40-row prompt chunk (prefill GEMMs with and without the step's xdh and
+workspace, the last row's logits) are checked the same way, and a workspace
+size without a workspace or rows above BQ_MAX_STEP_ROWS are refused."""
 import os
 import re
 import shutil
@@ -43,4 +46,8 @@ def test_decode_call_sequence(tmp_path):
     assert len(runs) == 12, out
     assert all(bad == 0 for _, bad in runs.values()), out
     assert runs[(0, 4)][0] == 21 and runs[(1, 4)][0] == 17 and runs[(2, 4)][0] == 16, runs
+    # the verify step and a 40-row prompt chunk: the same 21 launches (one
+    # prefill GEMM launch per fused GEMV, the last row's logits)
+    rows = re.findall(r"rows (\d+) scratch (\d) calls (\d+) bad (\d+)", out)
+    assert [(int(r), int(c), int(b)) for r, _, c, b in rows] == [(8, 21, 0), (40, 21, 0), (40, 21, 0)], out
     assert "bad = 0" in out

@@ -103,7 +103,7 @@ def _gemv_candidates(gemv, q, flips):
         yield base + sum((deltas[j] for j in range(len(flips)) if mask >> j & 1), np.zeros_like(base))
 
 
-def _oracle_block(oracle, m, bi, x, like=None):
+def _oracle_block(oracle, m, bi, x, like=None, like_xd=False):
     """Block bi (even: attention of layer bi // 2, odd: its FFN) of the
     reference's sequence applied to the fp32 row x, with the oracle's GEMVs
     (double precision over the q8 codes), norms and quantizer.  Returns the
@@ -112,7 +112,10 @@ def _oracle_block(oracle, m, bi, x, like=None):
     like (optional): the GPU's row that x stands for; where the q8 codes of
     the two differ, each such code of x lies on a rounding boundary (checked)
     and the block takes the GPU's code, as it takes the GPU's rounding of the
-    requantized row."""
+    requantized row.  like_xd: also take the GPU row's group scales xd
+    (checked equal within 2e-5 relative: the two rows agree to ~1e-6), for
+    a tier whose fp16 min-term operand half(xd * xsum) turns a 1e-6 xd
+    difference into a 2^-11 one where it crosses an fp16 rounding boundary."""
     f32 = lambda a: np.asarray(a, np.float32)
     L = m["layers"][bi // 2]
     x = x[None]
@@ -128,6 +131,9 @@ def _oracle_block(oracle, m, bi, x, like=None):
             xq = ql[0].copy()
             xs = xq.reshape(1, -1, 32).astype(np.int32).sum(axis=2).astype(q[2].dtype)
             q = (xq, q[1], xs)
+        if like_xd:
+            assert np.allclose(ql[1], q[1], rtol=2e-5, atol=0), "group scales differ by more than the rows do"
+            q = (q[0], ql[1].copy(), q[2])
     outs = []
     if bi % 2 == 0:
         ys = {}

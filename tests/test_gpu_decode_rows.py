@@ -14,7 +14,8 @@ instance of the one-row recurrence, so the checks are that file's, per row:
 * every row's whole chain from x0 stays within 2e-4 of the oracle's chain;
 * the graph of each row count replays bit-identically to its eager run, with
   unrelated eager work between replays;
-* fold = 1 with more than one row is refused (BQ_UNSUPPORTED).
+* fold = 1 with more than one row is refused (BQ_UNSUPPORTED), and more
+  than BQ_MAX_STEP_ROWS rows are invalid.
 """
 import ctypes
 
@@ -171,5 +172,7 @@ def test_decode_rows_rejects_fold(bq):
     st.x, st.xq, st.xd, st.xsum, st.proj = [b.data_ptr() for b in bufs]
     L = bq.load()
     assert L.bq_decode_enqueue(ctypes.byref(st), bq._stream()) == bq.BQ_UNSUPPORTED
-    st.rows = 9
+    st.rows = 9                                     # a prompt chunk: fold = 1 is one-row only
+    assert L.bq_decode_enqueue(ctypes.byref(st), bq._stream()) == bq.BQ_UNSUPPORTED
+    st.rows = 8193                                  # above BQ_MAX_STEP_ROWS
     assert L.bq_decode_enqueue(ctypes.byref(st), bq._stream()) == bq.BQ_EINVAL
