@@ -207,7 +207,11 @@ BQ_DEV void block_sum(float (&v)[X], float* red) {
     }
 }
 
-BQ_DEV float sigmoid_den(float x) { return 1.f + expf(-x); }
+// 1 + exp(-x) with the fast exponential (v_exp_f32 of x * log2(e)), as the
+// reference's __expf (bruce.cu:611, :632): the silu*mul producer has a fifth
+// fewer VALU instructions than with the accurate expf, which shortens the
+// producer in front of the fused down GEMV (decode chain 1.5-2% faster)
+BQ_DEV float sigmoid_den(float x) { return 1.f + __expf(-x); }
 
 // The elementwise parts of the q8 producers (one definition each, so the
 // standalone producers and the GEMV-fused ones compile to the same arithmetic).
