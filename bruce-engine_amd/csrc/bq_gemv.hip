@@ -791,13 +791,20 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     // 10.3 -> 9.8 us, whole stack 1.008 -> 0.998 ms/token, interleaved A/B).
     // q8 staging (DMA of a row the previous kernel just wrote) stays ahead of
     // the weight loads.  (Issuing all of them early for the 9216-value row
-    // measured slower: down 7.4 -> 8.0-8.2 us.)
-    constexpr bool kLate = QN != 0 && KC != 3072 && KC != 4096;
+    // measured slower: down 7.4 -> 8.0-8.2 us.)  A q8 producer (QN < 0) reads
+    // two or three rows and runs its reductions before any dot, so it takes
+    // the late issue at every K.
+    constexpr bool kLate = QN < 0 || (QN > 0 && KC != 3072 && KC != 4096);
     // Steps whose loads go out before the staging wait.  With the late issue
     // the first step's loads still go out before it for the fused quantizer
-    // (down, 2 steps per wave: kernel-event medians 8.19 -> 7.97 us); with a
-    // producer they held up its reductions (down + norm 9.99 -> 16.9 us).
-    constexpr int kEarly = kLate ? (QN > 0 ? (1 < SPS - 1 ? 1 : SPS - 1) : 0) : SPS;
+    // (down, 2 steps per wave: kernel-event medians 8.19 -> 7.97 us) and for
+    // a producer over a 3072 / 4096-value row (the QKV GEMV with the residual
+    // update, the O GEMV with the gate norm: decode chain, fold = 2, 1.291 ->
+    // 1.266 ms/token against all steps first, 1.275 with two steps early); a
+    // 9216-value producer row is held up by them (down + norm 9.99 -> 16.9 us).
+    constexpr int kEarly = !kLate                                   ? SPS
+                           : (QN > 0 || KC == 3072 || KC == 4096) ? (1 < SPS - 1 ? 1 : SPS - 1)
+                                                                    : 0;
     auto issue_weights = [&](int s0, int s1) {
 #pragma unroll
         for (int s = 0; s < SPS; ++s) {
