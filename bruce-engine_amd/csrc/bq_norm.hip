@@ -51,17 +51,18 @@ __global__ void __launch_bounds__(1024) k_norm_q8(NormArgs p) {
     float ss[1] = {0.f};
     if constexpr (OP == kOpResid) {
         // two row norms first (x and upd), then the blend and its norm
-        f32x4 xa[CH][4], ub[CH][4];
+        f32x4 xa[CH][4], ub[CH][4], al[CH][4];
         float s2[2] = {0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int i0 = c * stride + threadIdx.x * 16;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                xa[c][i] = ub[c][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                xa[c][i] = ub[c][i] = al[c][i] = f32x4{0.f, 0.f, 0.f, 0.f};
                 if (i0 < n) {
                     xa[c][i] = *(const f32x4*)(p.a + ro + i0 + 4 * i);
                     ub[c][i] = *(const f32x4*)(p.b + ro + i0 + 4 * i);
+                    al[c][i] = *(const f32x4*)(p.c + i0 + 4 * i);
                 }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -77,11 +78,9 @@ __global__ void __launch_bounds__(1024) k_norm_q8(NormArgs p) {
             const int i0 = c * stride + threadIdx.x * 16;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                f32x4 al = f32x4{0.f, 0.f, 0.f, 0.f};
-                if (i0 < n) al = *(const f32x4*)(p.c + i0 + 4 * i);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float v = resid_blend(xa[c][i][e], ka, ub[c][i][e], kb, al[e]);
+                    const float v = resid_blend(xa[c][i][e], ka, ub[c][i][e], kb, al[c][i][e]);
                     t[c][i][e] = v;
                     ss[0] += v * v;
                 }
