@@ -26,7 +26,9 @@ block):
   are checked on the GPU's final q8 row above, not on the oracle chain's
   row, which requantizes to other codes at the boundaries;
 * the captured graph replays bit-identically to the eager run, with
-  unrelated eager work between replays.
+  unrelated eager work between replays;
+* a 12-row chunk without xdh and workspace (the raw-Q5_K tier, whose exact
+  min term is the plain oracle's) and with a Q6_K head passes the same checks.
 """
 import ctypes
 
@@ -63,7 +65,7 @@ class _W144Oracle:
         return self._o.gemm_q5k_144(r144, rdm, xq, xd, self._o.fill_xdh(xd, xs), raw.shape[0])
 
 
-def _gpu_step_prefill(bq, m, R):
+def _gpu_step_prefill(bq, m, R, scratch=True, head_q6=None):
     import torch
     E, A, FF, V = D.E, D.A, D.FF, D.V
     keep = []
@@ -105,8 +107,12 @@ def _gpu_step_prefill(bq, m, R):
         f.alpha = ptr(Dv(L["alpha_f"]))
         f.gate, f.up, f.down = ctypes.pointer(wg), ctypes.pointer(wu), ctypes.pointer(wd)
         f.s_gate, f.s_up, f.n_ff = ptr(Dv(L["sg"])), ptr(Dv(L["su"])), FF
-    head = bq.quantize_q8s(Dv(m["head"].view(np.int16)), E, V)
-    keep.append(head)
+    if head_q6 is None:
+        head = bq.quantize_q8s(Dv(m["head"].view(np.int16)), E, V)
+        keep.append(head)
+    else:
+        hw = bq.make_weight(Dv(head_q6), bq.TYPE_Q6_K, E, V)
+        keep.append(hw)
     x = torch.empty((R, E), device="cuda")
     xq = torch.empty(R * FF, dtype=torch.int8, device="cuda")
     xd = torch.empty(R * FF // 32, device="cuda")
@@ -124,8 +130,13 @@ def _gpu_step_prefill(bq, m, R):
     st.x, st.input_h = x.data_ptr(), ptr(Dv(m["input_h"]))
     st.xq, st.xd, st.xsum = xq.data_ptr(), xd.data_ptr(), xs.data_ptr()
     st.proj, st.ffn_g, st.ffn_u = proj.data_ptr(), fg.data_ptr(), fu.data_ptr()
-    st.head_q8s, st.head_rs, st.vocab, st.logits = head.data_ptr(), ptr(Dv(m["rs"])), V, logits.data_ptr()
-    st.xdh, st.work, st.work_bytes = xdh.data_ptr(), work.data_ptr(), work.numel() * 4
+    if head_q6 is None:
+        st.head_q8s, st.head_rs = head.data_ptr(), ptr(Dv(m["rs"]))
+    else:
+        st.head = ctypes.pointer(hw)
+    st.vocab, st.logits = V, logits.data_ptr()
+    if scratch:
+        st.xdh, st.work, st.work_bytes = xdh.data_ptr(), work.data_ptr(), work.numel() * 4
     x0 = Dv(m["x0"])
 
     def reset():
@@ -148,11 +159,26 @@ def test_decode_prefill_graph_vs_oracle(bq, oracle, rows):
         D.MAX_AMBIG = saved
 
 
-def _run(bq, oracle, rows):
+def test_decode_prefill_raw_tier_kquant_head(bq, oracle):
+    """A 12-row chunk with no xdh and no workspace: the Q5_K projections take
+    the raw-Q5_K GEMM (exact fp32 min term, so the plain oracle's numerics)
+    unsplit, and a Q6_K head gives the last row's logits through the one-row
+    GEMV on that row's q8 codes."""
+    print("prompt chunk rows=12, raw tier, Q6_K head", flush=True)
+    from helpers import weights
+    saved, D.MAX_AMBIG = D.MAX_AMBIG, 14
+    try:
+        _run(bq, oracle, 12, scratch=False, head_q6=weights(3990, D.V, D.E, "q6k"))
+    finally:
+        D.MAX_AMBIG = saved
+
+
+def _run(bq, oracle, rows, scratch=True, head_q6=None):
     import torch
-    oracle = _W144Oracle(oracle)
+    if scratch:
+        oracle = _W144Oracle(oracle)
     m = DR._model_rows(bq, oracle, rows)
-    st, keep, reset, x, logits = _gpu_step_prefill(bq, m, rows)
+    st, keep, reset, x, logits = _gpu_step_prefill(bq, m, rows, scratch, head_q6)
     check = sorted({0, 1, rows // 3, rows // 2 + 1, rows - 2, rows - 1})
     rms = {r: DR._row_model(m, r) for r in check}
     prev = m["x0"].copy()
@@ -177,14 +203,19 @@ def _run(bq, oracle, rows):
     V = D.V
     assert np.isnan(el[V:]).all(), "logits past the last row's were written"
     last = rows - 1
-    lerr = oracle.normwise_err(el[:V], D._oracle_logits(oracle, rms[last], prev[last]))
+    if head_q6 is None:
+        lref = D._oracle_logits(oracle, rms[last], prev[last])
+    else:
+        q = oracle.q8_rows(prev[last][None])
+        lref = oracle.gemm_q6k(head_q6, q[0], q[1])[0]
+    lerr = oracle.normwise_err(el[:V], lref)
     print(f"  last row's logits vs oracle head: {lerr:.2e}", flush=True)
     assert lerr < 1e-4
     for r in check:
         rx = m["x0"][r].copy()
         for bi in range(4):
             like = gpu_x[bi - 1][r] if bi else None
-            _, rx = D._closest(oracle, gpu_x[bi][r], D._oracle_block(oracle, rms[r], bi, rx, like, like_xd=True)[0])
+            _, rx = D._closest(oracle, gpu_x[bi][r], D._oracle_block(oracle, rms[r], bi, rx, like, like_xd=scratch)[0])
         cx = oracle.normwise_err(prev[r], rx)
         assert cx < 2e-4, (r, cx)
     print(f"  whole chains of the checked rows within bounds", flush=True)
