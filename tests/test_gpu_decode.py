@@ -22,8 +22,9 @@ down Q6_K) and a Q8_0 logits head are run eagerly and from the graph:
 * the logits match the oracle's Q8_0 head on the final q8 row within 1e-4;
 * the whole chain from x0 stays within 2e-4 of the oracle's whole chain, the
   oracle taking at each block the candidate rounding that the GPU's block
-  output matches, and the GPU's q8 code of the block's input where the two
-  input rows (equal to ~2e-7) straddle a rounding boundary;
+  output matches, and the GPU's q8 code of the block's input (and of the
+  final row the logits are taken from) where the two rows (equal to ~2e-7)
+  straddle a rounding boundary;
 * every graph replay is bit-identical to the eager run.
 The folded forms (fold = 1: gate norm inside the O GEMV, silu*mul inside the
 gate+up epilogue, its norm inside the down GEMV; fold = 2: also the resid ->
@@ -161,8 +162,19 @@ def _closest(oracle, got, cands):
     return errs[k], cands[k]
 
 
-def _oracle_logits(oracle, m, x):
+def _oracle_logits(oracle, m, x, like=None):
+    """The oracle's Q8_0 head on the q8 row of x.  like (optional): the GPU's
+    final row that x stands for; where the two rows' q8 codes differ, each
+    such code of x lies on a rounding boundary (checked) and the GPU's code is
+    taken, as _oracle_block takes a block input's codes."""
     q = oracle.q8_rows(x[None])
+    if like is not None:
+        ql = oracle.q8_rows(like[None])
+        diff = np.nonzero(q[0][0] != ql[0][0])[0]
+        if len(diff):
+            amb = {i for i, _ in _q8_flips(oracle, x[None])[1]}
+            assert all(int(i) in amb for i in diff), ("final codes differ off a rounding boundary", diff)
+            q = (ql[0], q[1], q[2])
     return oracle.gemv_q8s(oracle.quantize_q8s(m["head"]), E, q[0], q[1], m["rs"])[0]
 
 
@@ -268,7 +280,7 @@ def test_decode_graph_vs_oracle(bq, oracle, fold):
     for bi in range(4):
         e, rx = _closest(oracle, gpu_x[bi], _oracle_block(oracle, m, bi, rx, gpu_x[bi - 1] if bi else None)[0])
         print(f"  chain block {bi}: closest candidate {e:.2e}", flush=True)
-    cx, cl = oracle.normwise_err(prev, rx), oracle.normwise_err(el, _oracle_logits(oracle, m, rx))
+    cx, cl = oracle.normwise_err(prev, rx), oracle.normwise_err(el, _oracle_logits(oracle, m, rx, prev))
     print(f"  whole chain vs oracle chain: x {cx:.2e}, logits {cl:.2e}", flush=True)
     assert cx < 2e-4 and cl < 2e-4
     # graph replays: bit-identical to the eager run

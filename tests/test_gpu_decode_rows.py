@@ -146,9 +146,10 @@ def _run_rows(bq, oracle, rows):
         assert lerr < 1e-4, (r, lerr)
         rx = m["x0"][r].copy()
         for bi in range(4):
-            _, rx = D._closest(oracle, gpu_x[bi][r], D._oracle_block(oracle, rms[r], bi, rx)[0])
+            like = gpu_x[bi - 1][r] if bi else None
+            _, rx = D._closest(oracle, gpu_x[bi][r], D._oracle_block(oracle, rms[r], bi, rx, like)[0])
         cx = oracle.normwise_err(prev[r], rx)
-        cl = oracle.normwise_err(el[r], D._oracle_logits(oracle, rms[r], rx))
+        cl = oracle.normwise_err(el[r], D._oracle_logits(oracle, rms[r], rx, prev[r]))
         assert cx < 2e-4 and cl < 2e-4, (r, cx, cl)
     print(f"  logits and whole chains of {rows} rows within bounds", flush=True)
     g = bq.DecodeGraph(st)
