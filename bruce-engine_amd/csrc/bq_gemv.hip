@@ -796,15 +796,14 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     // the late issue at every K.
     constexpr bool kLate = QN < 0 || (QN > 0 && KC != 3072 && KC != 4096);
     // Steps whose loads go out before the staging wait.  With the late issue
-    // the first step's loads still go out before it for the fused quantizer
-    // (down, 2 steps per wave: kernel-event medians 8.19 -> 7.97 us) and for
-    // a producer over a 3072 / 4096-value row (the QKV GEMV with the residual
-    // update, the O GEMV with the gate norm: decode chain, fold = 2, 1.291 ->
-    // 1.266 ms/token against all steps first, 1.275 with two steps early); a
-    // 9216-value producer row is held up by them (down + norm 9.99 -> 16.9 us).
-    constexpr int kEarly = !kLate                                   ? SPS
-                           : (QN > 0 || KC == 3072 || KC == 4096) ? (1 < SPS - 1 ? 1 : SPS - 1)
-                                                                    : 0;
+    // the first step's loads still go out before it (of two or more steps):
+    // for the fused quantizer (down, 2 steps per wave: kernel-event medians
+    // 8.19 -> 7.97 us) and for a producer (decode chain, fold = 2: the QKV
+    // GEMV with the residual update and the O GEMV with the gate norm 1.291 ->
+    // 1.266 ms/token against all steps first, 1.275 with two steps early; the
+    // down GEMV with the norm of the silu*mul row 1.256 -> 1.242 against no
+    // step early).
+    constexpr int kEarly = kLate ? (1 < SPS - 1 ? 1 : SPS - 1) : SPS;
     auto issue_weights = [&](int s0, int s1) {
 #pragma unroll
         for (int s = 0; s < SPS; ++s) {
