@@ -114,6 +114,11 @@ LaunchTiming& next_launch_timing() {
     static thread_local LaunchTiming t;
     return t;
 }
+
+ScaledCopy& next_scaled_copy() {
+    static thread_local ScaledCopy c;
+    return c;
+}
 }  // namespace bq
 
 extern "C" {
@@ -286,7 +291,7 @@ int bq_gemv_norm_fused(float* const* ys, const bq_weight* const* ws, int nparts,
     if ((xq != nullptr) != (xd != nullptr) || (xq != nullptr) != (xsum != nullptr)) return BQ_EINVAL;
     // inputs of the op
     if (op != BQ_OP_NORM && !b) return BQ_EINVAL;
-    if (op >= BQ_OP_RESID && !c) return BQ_EINVAL;
+    if (op >= BQ_OP_RESID && op != BQ_OP_GATE && !c) return BQ_EINVAL;  // gate: c NULL = b already scaled
     if (op == BQ_OP_SILU && !d) return BQ_EINVAL;
     if (out && (out == a || out == b)) return BQ_EINVAL;  // read by every workgroup
     const int K = ws[0]->K;

@@ -65,6 +65,14 @@ int flush(const bq_decode_step* s, Resid& rs, bq_stream_t st) {
 // tokens per step: 0 means 1
 int rows_of(const bq_decode_step* s) { return s->rows > 0 ? s->rows : 1; }
 
+// values ffn_u holds per row: the largest n_ff of the step's FFN blocks
+int max_ffn(const bq_decode_step* s) {
+    int m = 0;
+    for (int i = 0; i < s->n_blocks; ++i)
+        if (s->blocks[i].kind == BQ_BLOCK_FFN && s->blocks[i].n_ff > m) m = s->blocks[i].n_ff;
+    return m;
+}
+
 // y [rows][N] of a k-quant weight over the q8 rows: the single-row GEMV at one
 // row (launch_gemv, :7982 / :8008), the prompt-batch dispatcher above
 // (launch_gemm_b, :7750 / :7800: the multi-row kernels at 2..8 rows, the MMQ
@@ -106,15 +114,36 @@ int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, int ro
             wp[nf] = &b.qkv[p];
             yp[nf++] = b.qkv_out[p];
         }
+    // fold >= 1: the QKV launch also writes its gate part times sg (the part
+    // attn_gate starts, at most n_ff rows) into the scratch row ffn_u (unused
+    // by the folded FFN block), so that the O GEMV's workgroups read two rows
+    // instead of three; the same fp32 product the gate norm forms itself, so
+    // the results are unchanged
+    float* gate_s = nullptr;
+    if (s->fold && s->ffn_u && al16(s->ffn_u) && rows == 1)
+        for (int p = 0; p < nf; ++p)
+            if (yp[p] == b.attn_gate && wp[p]->N >= b.n_attn && wp[p]->N <= max_ffn(s)) gate_s = s->ffn_u;
+    auto arm = [&] {
+        if (gate_s) {
+            bq::ScaledCopy& sc = bq::next_scaled_copy();
+            for (int p = 0; p < nf; ++p)
+                if (yp[p] == b.attn_gate) sc.w = wp[p]->raw;
+            sc.y = gate_s;
+            sc.s = b.sgate;
+        }
+    };
+    auto disarm = [&] { bq::next_scaled_copy() = bq::ScaledCopy(); };
     bool qkv_done = false;
     if (nf > 0 && rs.alpha) {
         // the pending resid -> q8 inside the QKV GEMV; its q8 row is written
         // out only for the parts that run as their own GEMVs
         float* nx = other_of(s, rs.cur);
         const bool q8out = nf < b.n_qkv;
+        arm();
         const int r = bq_gemv_norm_fused(yp, wp, nf, BQ_OP_RESID, nx, rs.cur, s->proj, rs.alpha, nullptr,
                                          q8out ? s->xq : nullptr, q8out ? s->xd : nullptr,
                                          q8out ? s->xsum : nullptr, st);
+        disarm();
         if (r != BQ_OK && r != BQ_UNSUPPORTED) return r;
         if (r == BQ_OK) {
             rs.cur = nx;
@@ -123,8 +152,12 @@ int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, int ro
         }
     }
     if (int e = flush(s, rs, st)) return e;
-    if (nf > 0 && !qkv_done)
-        if (int e = parts_rows_of(yp, wp, nf, rows, s, st)) return e;
+    if (nf > 0 && !qkv_done) {
+        arm();
+        const int e = parts_rows_of(yp, wp, nf, rows, s, st);
+        disarm();
+        if (e) return e;
+    }
     for (int p = 0; p < b.n_qkv; ++p)
         if (b.qkv[p].ggml_type != BQ_TYPE_Q5_K)
             if (int e = gemv_rows_of(b.qkv_out[p], &b.qkv[p], rows, s, st)) return e;
@@ -135,6 +168,9 @@ int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, int ro
     if (s->fold) {
         float* yo[1] = {s->proj};
         const bq_weight* po[1] = {b.o};
+        if (gate_s)  // the scaled gate row: gate * sg, sg already applied
+            return bq_gemv_norm_fused(yo, po, 1, BQ_OP_GATE, nullptr, b.attn_out, gate_s, nullptr, nullptr, nullptr,
+                                      nullptr, nullptr, st);
         return bq_gemv_norm_fused(yo, po, 1, BQ_OP_GATE, nullptr, b.attn_out, b.attn_gate, b.sgate, nullptr,
                                   nullptr, nullptr, nullptr, st);
     }

@@ -572,7 +572,9 @@ BQ_DEV void fp_load(f32x4 (&in)[4][4], const FusedQ8& fq, int K, int wave, int l
         for (int i = 0; i < 4; ++i) {
             in[0][i] = *(const f32x4*)(fq.x + v0 + 4 * i);
             if (op != kOpNorm) in[1][i] = *(const f32x4*)(fq.b + v0 + 4 * i);
-            if (op >= kOpResid) in[2][i] = *(const f32x4*)(fq.c + v0 + 4 * i);
+            // gate with no sg row: the gate row is already scaled (sg = 1)
+            if (op >= kOpResid)
+                in[2][i] = fq.c ? *(const f32x4*)(fq.c + v0 + 4 * i) : f32x4{1.f, 1.f, 1.f, 1.f};
             if (op == kOpSilu) in[3][i] = *(const f32x4*)(fq.d + v0 + 4 * i);
         }
     }
@@ -873,7 +875,10 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
                 const float v = row16_sum(acc[m]);
-                if (li == 15 && rowok) Y[(size_t)m * Nloc + row] = v;
+                if (li == 15 && rowok) {
+                    Y[(size_t)m * Nloc + row] = v;
+                    if (MR == 1 && pt.ys && p == pt.sp) pt.ys[row] = v * pt.ss[row];
+                }
             }
         }
         return;
@@ -907,6 +912,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
             float v = 0.f;
             for (int k = 0; k < KS; ++k) v += part_sums[((wave + k) * MR + m) * 4 + g];
             Y[(size_t)m * Nloc + row] = v;
+            if (MR == 1 && pt.ys && p == pt.sp) pt.ys[row] = v * pt.ss[row];
         }
     }
 }
@@ -980,6 +986,16 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     const int blocks = (pt.ntiles + RT - 1) / RT;
     PartTable ptl = pt;
     ptl.prio = blocks <= kPrioMaxBlocks;
+    if (MR == 1 && !PAIR) {
+        ScaledCopy& sc = next_scaled_copy();
+        for (int q = 0; sc.y && q < pt.nparts; ++q)
+            if (pt.W[q] == sc.w) {  // consumed by the launch that holds the part
+                ptl.sp = q;
+                ptl.ys = sc.y;
+                ptl.ss = sc.s;
+                sc = ScaledCopy();
+            }
+    }
     // the launch-bounds class sets the compiler's occupancy target; the
     // single-row decode shapes run compile-time-K instances
     if constexpr (SPS == 3 && (MR == 1 || QN == 0)) {

@@ -22,6 +22,11 @@ struct PartTable {
     int nparts;
     int ntiles;
     int prio = 0;  // GEMV: raise the wave priority during the activation staging
+    // one-row GEMV: part sp's outputs also go to ys scaled by ss (ys[row] =
+    // y[row] * ss[row]); ys NULL: none
+    int sp = 0;
+    float* ys = nullptr;
+    const float* ss = nullptr;
 };
 
 enum class GemvKind { Q5K, Q6KRaw, Q6KRep };
@@ -33,6 +38,17 @@ struct LaunchTiming {
     hipEvent_t start = nullptr, stop = nullptr;
 };
 LaunchTiming& next_launch_timing();
+
+// Optional scaled copy of one part's output for the calling thread's next
+// one-row GEMV launch, the part named by its weight pointer (the decode
+// step's attention gate: gate * sg, which the O GEMV's gate-norm producer
+// then reads instead of the gate and sg rows).  Consumed by that launch.
+struct ScaledCopy {
+    const void* w = nullptr;
+    float* y = nullptr;
+    const float* s = nullptr;
+};
+ScaledCopy& next_scaled_copy();
 
 template <typename F, typename... Args>
 inline void launch_kernel(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {

@@ -101,7 +101,8 @@ __global__ void __launch_bounds__(1024) k_norm_q8(NormArgs p) {
                         v = a + *(const f32x4*)(p.b + ro + i0 + 4 * i);
                     } else if constexpr (OP == kOpGate) {
                         const f32x4 gt = *(const f32x4*)(p.b + ro + i0 + 4 * i);
-                        const f32x4 sg = *(const f32x4*)(p.c + i0 + 4 * i);
+                        // no sg row: the gate row is already scaled (sg = 1)
+                        const f32x4 sg = p.c ? *(const f32x4*)(p.c + i0 + 4 * i) : f32x4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[e] = gate_div(a[e], gt[e], sg[e]);
                     } else {  // kOpSilu

@@ -151,7 +151,8 @@ int bq_gemv_q8_fused(float* const* ys, const bq_weight* const* ws, int nparts, c
  * producers above (op: BQ_OP_NORM, BQ_OP_ADD, BQ_OP_RESID, BQ_OP_GATE,
  * BQ_OP_SILU with the inputs a, b, c, d in the order of bq_norm_q8 ..
  * bq_silu_mul_norm_q8: norm a; add a, h=b; resid x=a, upd=b, alpha=c; gate
- * aout=a, gate=b, sg=c; silu g=a, u=b, sg=c, su=d) computed by every
+ * aout=a, gate=b, sg=c, where c NULL means b already holds gate*sg; silu
+ * g=a, u=b, sg=c, su=d) computed by every
  * workgroup for the one activation row, quantized and consumed by the GEMV
  * over nparts (1..4) matrices sharing K (types as bq_gemv_q8_fused).
  * Replaces the decode pair "q8 producer, then GEMV" of the reference --
@@ -384,7 +385,10 @@ int bq_gguf_load(bq_gguf* g, int64_t i, void* raw, void* rep, void* rep_min, bq_
  * on st (and only there) and write attn_out; NULL leaves attn_out as it is.
  * Every buffer holds `rows` rows, row-major: x, input_h, proj
  * [rows][n_embd]; attn_out, attn_gate [rows][n_attn]; qkv_out[p] [rows][N_p];
- * ffn_g, ffn_u [rows][n_ff] (ffn_u unused when fold >= 1); logits
+ * ffn_g, ffn_u [rows][n_ff] (with fold >= 1 ffn_u, optional, is scratch: when
+ * attn_gate is the start of a Q5_K QKV part's output, the QKV launch also
+ * writes that part times sgate there and the O GEMV's gate norm reads it
+ * instead of attn_gate and sgate, same results); logits
  * [rows][vocab] (a prompt chunk: [vocab]); xq/xd/xsum hold the q8 rows of the
  * widest operand, rows x max(n_embd, n_attn, n_ff) values.  x is updated in
  * place.  A graph captures the pointers and the row count it is created with:

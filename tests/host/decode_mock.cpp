@@ -14,6 +14,13 @@
 #include "bq.h"
 #include "bq_internal.hpp"
 
+namespace bq {
+ScaledCopy& next_scaled_copy() {
+    static ScaledCopy c;
+    return c;
+}
+}
+
 struct Buf { const char* name; size_t bytes; };
 static std::map<uintptr_t, Buf> g_bufs;
 static int g_bad = 0;
@@ -41,11 +48,25 @@ static const char* nm(const void* p) {
 }
 static size_t wbytes(const bq_weight* w) { return (size_t)w->N * (w->K / 256) * (w->ggml_type == BQ_TYPE_Q5_K ? 176 : 210); }
 
+// a launch over these parts consumes an armed scaled copy of the part it names
+static int g_scaled = 0;
+static void consume_scaled(const char* call, const bq_weight* const* ws, int n) {
+    bq::ScaledCopy& sc = bq::next_scaled_copy();
+    for (int p = 0; sc.y && p < n; ++p)
+        if (ws[p]->raw == sc.w) {
+            chk(call, "scaled y", sc.y, 4 * (size_t)ws[p]->N);
+            chk(call, "scaled s", sc.s, 4 * (size_t)ws[p]->N);
+            sc = bq::ScaledCopy();
+            ++g_scaled;
+        }
+}
+
 extern "C" {
 int bq_init(void) { return 0; }
 int bq_verify_fused(float* const* ys, const bq_weight* const* ws, int n, int rows, const int8_t* xq, const float* xd,
                     const int32_t* xs, int, bq_stream_t) {
     ++g_calls; if (g_verbose) printf("verify_fused n=%d rows=%d\n", n, rows);
+    consume_scaled("verify", ws, n);
     for (int p = 0; p < n; ++p) { chk("verify", "y", ys[p], 4 * ws[p]->N * rows); chk("verify", "w", ws[p]->raw, wbytes(ws[p])); }
     chk("verify", "xq", xq, ws[0]->K * rows); chk("verify", "xd", xd, ws[0]->K / 8 * rows); chk("verify", "xs", xs, ws[0]->K / 8 * rows);
     return 0;
@@ -81,10 +102,11 @@ int bq_gemv_norm_fused(float* const* ys, const bq_weight* const* ws, int nparts,
                        const float* b, const float* c, const float* d, int8_t* xq, float* xd, int32_t* xsum, bq_stream_t) {
     const int K = ws[0]->K;
     ++g_calls; if (g_verbose) printf("norm_fused op=%d parts=%d K=%d out=%s a=%s b=%s c=%s d=%s xq=%s\n", op, nparts, K, nm(out), nm(a), nm(b), nm(c), nm(d), nm(xq));
+    consume_scaled("nf", ws, nparts);
     for (int p = 0; p < nparts; ++p) { chk("nf", "y", ys[p], 4 * ws[p]->N); chk("nf", "w", ws[p]->raw, wbytes(ws[p])); }
     chk("nf", "a", a, 4 * K);
     if (op != BQ_OP_NORM) chk("nf", "b", b, 4 * K);
-    if (op >= BQ_OP_RESID) chk("nf", "c", c, 4 * K);
+    if (op >= BQ_OP_RESID && (op != BQ_OP_GATE || c)) chk("nf", "c", c, 4 * K);  // gate: c NULL = b scaled
     if (op == BQ_OP_SILU) chk("nf", "d", d, 4 * K);
     if (out) chk("nf", "out", out, 4 * K);
     if (xq) { chk("nf", "xq", xq, K); chk("nf", "xd", xd, K / 8); chk("nf", "xs", xsum, K / 8); }
@@ -162,7 +184,9 @@ int main(int argc, char** argv) {
             const int bad0 = g_bad;
             const int r = bq_decode_enqueue(&st, nullptr);
             if (r) { printf("  returned %d\n", r); g_bad++; }
-            printf("fold %d blocks %d calls %d bad %d\n", fold, nb, g_calls, g_bad - bad0);
+            if (bq::next_scaled_copy().y) { printf("  scaled copy left armed\n"); g_bad++; }
+            printf("fold %d blocks %d calls %d bad %d scaled %d\n", fold, nb, g_calls, g_bad - bad0, g_scaled);
+            g_scaled = 0;
         }
     // the verify step (8 rows) and a prompt chunk (R rows: the prefill GEMMs,
     // with and without xdh / workspace)

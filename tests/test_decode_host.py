@@ -41,10 +41,14 @@ def test_decode_call_sequence(tmp_path):
                     "-o", str(mock)], check=True, capture_output=True)
     subprocess.run([hipcc, str(dec), str(mock), "-o", str(exe)], check=True, capture_output=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60).stdout
-    runs = {(int(f), int(b)): (int(c), int(bad))
-            for f, b, c, bad in re.findall(r"fold (\d) blocks (\d) calls (\d+) bad (\d+)", out)}
+    runs = {(int(f), int(b)): (int(c), int(bad), int(sc))
+            for f, b, c, bad, sc in re.findall(r"fold (\d) blocks (\d) calls (\d+) bad (\d+) scaled (\d+)", out)}
     assert len(runs) == 12, out
-    assert all(bad == 0 for _, bad in runs.values()), out
+    assert all(r[1] == 0 for r in runs.values()), out
+    # fold >= 1: each attention block's QKV launch writes the scaled gate row
+    # into ffn_u (blocks 0 and 2), once the step has an FFN block to size ffn_u by
+    want = lambda f, nb: 0 if f == 0 or nb == 1 else (nb + 1) // 2
+    assert all(runs[(f, nb)][2] == want(f, nb) for f in range(3) for nb in range(1, 5)), runs
     assert runs[(0, 4)][0] == 21 and runs[(1, 4)][0] == 17 and runs[(2, 4)][0] == 16, runs
     # the verify step and a 40-row prompt chunk: the same 21 launches (one
     # prefill GEMM launch per fused GEMV, the last row's logits)
