@@ -1205,7 +1205,9 @@ template <class F>
 static hipError_t dispatch_producer(const PartTable& pt, int K, const FusedQ8& fq, hipStream_t st) {
     // every workgroup redoes the producer, so the split keeps the fewest
     // workgroups (the fused quantizer's cap 1 for small GEMVs measured slower
-    // here: folded decode chain 1.51 -> 1.68 ms/token)
+    // here: folded decode chain 1.51 -> 1.68 ms/token; with the current
+    // producers, fold = 2 at cap 3 / 2 / 1 for K <= 4096: 1.199-1.200 /
+    // 1.270-1.272 / 1.326-1.327 ms/token)
     int KS, SPS;
     k_split(K, K > 4096 ? 2 : 3, KS, SPS);
     switch (SPS) {
