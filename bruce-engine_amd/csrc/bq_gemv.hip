@@ -1019,10 +1019,19 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
             return hipGetLastError();
         }
     }
-    // one step per wave (the cap-1 K split of the small decode GEMVs: QKV, O)
+    // one step per wave (the cap-1 K split of the small decode GEMVs: QKV, O,
+    // config 3).  K = 3072 splits 3 ways, so a 4-wave workgroup holds one row
+    // tile and a wave that only helps the staging: 3-wave workgroups instead
+    // (9216 x 3072 at one row: 2304 workgroups, 9216 -> 6912 waves, within one
+    // dispatch round of 8 per SIMD; same K split, so the same sums; measured
+    // alternating in one process, medians of 12: 5.87 -> 5.73 us, 3072 x 3072
+    // level).  A producer keeps 4 waves (one 1024-value chunk per wave).
     if constexpr (MR == 1 && SPS == 1 && QN <= 1) {
         if (waves == 4 && KS == kc_ks(K, SPS) && (K == 3072 || K == 4096)) {
-            if (K == 3072)
+            if (K == 3072 && QN >= 0)
+                launch_kernel((k_gemv<F, MR, SPS, QN, 192, 3072, PAIR>), dim3(blocks), dim3(192), lds, st, ptl, K,
+                              KS, xq, xd, xsum, fq);
+            else if (K == 3072)
                 launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K,
                               KS, xq, xd, xsum, fq);
             else
