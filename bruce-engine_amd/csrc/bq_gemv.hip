@@ -23,7 +23,6 @@
 #include "bq_device.hpp"
 #include "bq_internal.hpp"
 
-#include <stdlib.h>
 
 #include <algorithm>
 #include <type_traits>
@@ -1043,7 +1042,15 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     // Q5_K verify rows 2..8 at K = 3072 / 4096 (cap-1 / cap-2 K splits)
     if constexpr (QN == 0 && !PAIR && MR > 1 && SPS < 3 && std::is_same<F, FmtQ5K>::value) {
         if (waves == 4 && KS == kc_ks(K, SPS) && (K == 3072 || K == 4096)) {
-            if (K == 3072)
+            // one step per wave at K = 3072: 3-wave workgroups, as for one
+            // row (rows 2 / 3 at 9216 x 3072 5.75 -> 5.61 / 6.54 -> 6.24 us,
+            // 8 rows at 5120 x 3072 6.06 -> 5.55, 4 rows level; the Q6_K
+            // 9216-value rows keep their fourth wave: 3 waves measured 5%
+            // slower at 1 and 2 rows, the wave shares a 9 KB staging per row)
+            if (K == 3072 && SPS == 1)
+                launch_kernel((k_gemv<F, MR, SPS, QN, 192, 3072, PAIR>), dim3(blocks), dim3(192), lds, st, ptl, K,
+                              KS, xq, xd, xsum, fq);
+            else if (K == 3072)
                 launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K,
                               KS, xq, xd, xsum, fq);
             else
