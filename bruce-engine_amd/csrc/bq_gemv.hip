@@ -23,6 +23,7 @@
 #include "bq_device.hpp"
 #include "bq_internal.hpp"
 
+#include <stdlib.h>
 
 #include <algorithm>
 #include <type_traits>
