@@ -119,6 +119,8 @@ ScaledCopy& next_scaled_copy() {
     static thread_local ScaledCopy c;
     return c;
 }
+
+int device_cus() { return t_dev ? t_dev->cus : 256; }
 }  // namespace bq
 
 extern "C" {

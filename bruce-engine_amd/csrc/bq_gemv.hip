@@ -974,6 +974,30 @@ void k_split(int K, int cap, int& KS, int& SPS) {
 // the activation staging.
 static int gemv_waves(int KS) { return KS <= 4 ? 4 : 16; }
 
+// Row tiles per workgroup of a producer-fused one-row GEMV: the launch takes
+// about as long as its busiest CU, so take the candidate with the fewest row
+// tiles there, ceil(ceil(ntiles / rt) / cus) * rt (the first of equals).  At
+// config 5 that is one workgroup per CU: QKV 5120 x 3072 5 tiles (256
+// workgroups of 5 waves instead of 320 of 4, 64 CUs holding two), O 3072 x
+// 4096 3 tiles x 2 K slices (256 of 6 instead of 384 of 4); the folded
+// decode chain, alternated in one process, fold 1 / 2 1.244 / 1.198 -> 1.235 /
+// 1.163 ms/token.  Every workgroup still runs the producer over the whole row
+// in the same chunk and wave order, so the results are unchanged.  (Sizing
+// the q8 / fused-quantizer gate+up to 6 tiles, 3 workgroups per CU, measured
+// 8.5 -> 10.2 us: without a producer the 4-wave workgroups stay.)
+static int pick_rt(int ntiles, int cus, const int* rts, int n) {
+    int best = rts[0];
+    long long bc = -1;
+    for (int i = 0; i < n; ++i) {
+        const long long nb = (ntiles + rts[i] - 1) / rts[i];
+        const long long c = (nb + cus - 1) / cus * rts[i];
+        if (bc < 0 || c < bc) {
+            bc = c;
+            best = rts[i];
+        }
+    }
+    return best;
+}
 template <class F, int MR, int SPS, int QN = 0, bool PAIR = false>
 static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* xq, const float* xd,
                              const int32_t* xsum, hipStream_t st, FusedQ8 fq = {}) {
@@ -1000,6 +1024,25 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     // single-row decode shapes run compile-time-K instances
     if constexpr (SPS == 3 && (MR == 1 || QN == 0)) {
         if (waves == 4 && K == 3072 && KS == kc_ks(K, SPS)) {
+            if constexpr (MR == 1 && QN < 0) {
+                // three 1024-value steps per wave (KS = 1): 4, 5, 6 or 8 row tiles per workgroup
+                static constexpr int kRts[] = {4, 5, 6, 8};
+                const int rt = pick_rt(pt.ntiles, device_cus(), kRts, 4);
+                const int nb = (pt.ntiles + rt - 1) / rt;
+                const size_t lr = act_lds_bytes<F>(MR, K) + (size_t)rt * MR * 4 * sizeof(float) + 48 * sizeof(float);
+                switch (rt) {
+                    case 5: launch_kernel((k_gemv<F, MR, SPS, QN, 320, 3072, PAIR>), dim3(nb), dim3(320), lr, st, ptl, K,
+                                          KS, xq, xd, xsum, fq);
+                            return hipGetLastError();
+                    case 6: launch_kernel((k_gemv<F, MR, SPS, QN, 384, 3072, PAIR>), dim3(nb), dim3(384), lr, st, ptl, K,
+                                          KS, xq, xd, xsum, fq);
+                            return hipGetLastError();
+                    case 8: launch_kernel((k_gemv<F, MR, SPS, QN, 512, 3072, PAIR>), dim3(nb), dim3(512), lr, st, ptl, K,
+                                          KS, xq, xd, xsum, fq);
+                            return hipGetLastError();
+                    default: break;
+                }
+            }
             launch_kernel((k_gemv<F, MR, SPS, QN, 256, 3072, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
                           xsum, fq);
             return hipGetLastError();
@@ -1014,6 +1057,22 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     }
     if constexpr (MR == 1 && SPS == 2) {
         if (waves == 4 && K == 4096 && KS == kc_ks(K, SPS)) {
+            if constexpr (QN < 0) {
+                // two 2048-value steps per wave, 2 K slices: 2, 3 or 4 row tiles per workgroup
+                static constexpr int kRts[] = {2, 3, 4};
+                const int rt = pick_rt(pt.ntiles, device_cus(), kRts, 3);
+                const int nb = (pt.ntiles + rt - 1) / rt;
+                const size_t lr = act_lds_bytes<F>(MR, K) + (size_t)2 * rt * MR * 4 * sizeof(float) + 48 * sizeof(float);
+                switch (rt) {
+                    case 3: launch_kernel((k_gemv<F, MR, SPS, QN, 384, 4096, PAIR>), dim3(nb), dim3(384), lr, st, ptl, K,
+                                          KS, xq, xd, xsum, fq);
+                            return hipGetLastError();
+                    case 4: launch_kernel((k_gemv<F, MR, SPS, QN, 512, 4096, PAIR>), dim3(nb), dim3(512), lr, st, ptl, K,
+                                          KS, xq, xd, xsum, fq);
+                            return hipGetLastError();
+                    default: break;
+                }
+            }
             launch_kernel((k_gemv<F, MR, SPS, QN, 256, 4096, PAIR>), dim3(blocks), dim3(256), lds, st, ptl, K, KS, xq, xd,
                           xsum, fq);
             return hipGetLastError();

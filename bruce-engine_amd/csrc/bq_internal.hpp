@@ -49,6 +49,8 @@ struct ScaledCopy {
     const float* s = nullptr;
 };
 ScaledCopy& next_scaled_copy();
+// CU count of the current device (set by the entry point's init; 256 before any)
+int device_cus();
 
 template <typename F, typename... Args>
 inline void launch_kernel(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
