@@ -819,6 +819,18 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
     };
+    // PAIR: the epilogue's sg and su of the row are loaded now, ahead of the
+    // weights, rather than after the last dot (folded decode chain, fold 1
+    // 1.237 -> 1.234 ms/token; the same for the scaled gate copy's ss delays
+    // a producer's staging wait: fold 2 1.172 -> 1.187)
+    [[maybe_unused]] float pre_sg = 0.f, pre_su = 0.f;
+    if constexpr (PAIR) {
+        const int rr = min(row, Nloc - 1);
+        pre_sg = fq.c[rr];
+        pre_su = fq.d[rr];
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (kEarly > 0) issue_weights(0, kEarly);
 
     // ---- 3. own DMA / fp32 loads done (only the weight loads may still be outstanding)
@@ -863,7 +875,8 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
         if constexpr (PAIR) {
             const float v = row16_sum(acc[0]);
             const float u = __shfl(v, lane + 32, 64);  // DPP rows 0, 1 <- 2, 3
-            if (g < 2 && li == 15 && rowok) fq.out[row] = silu_mul(v, u, fq.c[row], fq.d[row]);
+            if (g < 2 && li == 15 && rowok)
+                fq.out[row] = silu_mul(v, u, pre_sg, pre_su);
             return;
         }
         if constexpr (kMmLanes) {
@@ -902,7 +915,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
                 v += part_sums[(wave + k) * 4 + g];
                 u += part_sums[(wave + k) * 4 + g + 2];
             }
-            fq.out[row] = silu_mul(v, u, fq.c[row], fq.d[row]);
+            fq.out[row] = silu_mul(v, u, pre_sg, pre_su);
         }
         return;
     }
