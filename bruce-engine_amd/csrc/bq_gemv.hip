@@ -1038,9 +1038,10 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     if constexpr (SPS == 3 && (MR == 1 || QN == 0)) {
         if (waves == 4 && K == 3072 && KS == kc_ks(K, SPS)) {
             if constexpr (MR == 1 && QN < 0) {
-                // three 1024-value steps per wave (KS = 1): 4, 5, 6 or 8 row tiles per workgroup
-                static constexpr int kRts[] = {4, 5, 6, 8};
-                const int rt = pick_rt(pt.ntiles, device_cus(), kRts, 4);
+                // three 1024-value steps per wave (KS = 1): 4, 5 or 6 row tiles per
+                // workgroup (8 never does better than 4 under the rule)
+                static constexpr int kRts[] = {4, 5, 6};
+                const int rt = pick_rt(pt.ntiles, device_cus(), kRts, 3);
                 const int nb = (pt.ntiles + rt - 1) / rt;
                 const size_t lr = act_lds_bytes<F>(MR, K) + (size_t)rt * MR * 4 * sizeof(float) + 48 * sizeof(float);
                 switch (rt) {
@@ -1048,9 +1049,6 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
                                           KS, xq, xd, xsum, fq);
                             return hipGetLastError();
                     case 6: launch_kernel((k_gemv<F, MR, SPS, QN, 384, 3072, PAIR>), dim3(nb), dim3(384), lr, st, ptl, K,
-                                          KS, xq, xd, xsum, fq);
-                            return hipGetLastError();
-                    case 8: launch_kernel((k_gemv<F, MR, SPS, QN, 512, 3072, PAIR>), dim3(nb), dim3(512), lr, st, ptl, K,
                                           KS, xq, xd, xsum, fq);
                             return hipGetLastError();
                     default: break;
@@ -1071,16 +1069,14 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
     if constexpr (MR == 1 && SPS == 2) {
         if (waves == 4 && K == 4096 && KS == kc_ks(K, SPS)) {
             if constexpr (QN < 0) {
-                // two 2048-value steps per wave, 2 K slices: 2, 3 or 4 row tiles per workgroup
-                static constexpr int kRts[] = {2, 3, 4};
-                const int rt = pick_rt(pt.ntiles, device_cus(), kRts, 3);
+                // two 2048-value steps per wave, 2 K slices: 2 or 3 row tiles per
+                // workgroup (4 never does better than 2 under the rule)
+                static constexpr int kRts[] = {2, 3};
+                const int rt = pick_rt(pt.ntiles, device_cus(), kRts, 2);
                 const int nb = (pt.ntiles + rt - 1) / rt;
                 const size_t lr = act_lds_bytes<F>(MR, K) + (size_t)2 * rt * MR * 4 * sizeof(float) + 48 * sizeof(float);
                 switch (rt) {
                     case 3: launch_kernel((k_gemv<F, MR, SPS, QN, 384, 4096, PAIR>), dim3(nb), dim3(384), lr, st, ptl, K,
-                                          KS, xq, xd, xsum, fq);
-                            return hipGetLastError();
-                    case 4: launch_kernel((k_gemv<F, MR, SPS, QN, 512, 4096, PAIR>), dim3(nb), dim3(512), lr, st, ptl, K,
                                           KS, xq, xd, xsum, fq);
                             return hipGetLastError();
                     default: break;
