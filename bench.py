@@ -258,16 +258,16 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
                                      "O GEMV, resid -> q8, gate+up GEMV, silu*mul norm -> q8, down GEMV, resid -> q8; "
                                      "final norm -> q8, lm_head (attention excluded; aout a fixed input)",
                              "ms_per_token": round(chain_ms, 4), "GBps": round(gbs(tot, chain_ms), 1),
-                             "launches_per_token": 8 * LAYERS + 2},
+                             "launches_per_token": 8 * LAYERS + 1},
             "decode_chain_folded": {"what": "the same step with fold = 1: the gate norm inside the O GEMV, the "
                                             "silu*mul in the gate+up epilogue (bq_gate_up_silu) and its norm -> q8 "
                                             "inside the down GEMV (bq_gemv_norm_fused)",
                                     "ms_per_token": round(folded_ms, 4), "GBps": round(gbs(tot, folded_ms), 1),
-                                    "launches_per_token": 6 * LAYERS + 2},
+                                    "launches_per_token": 6 * LAYERS + 1},
             "decode_chain_folded2": {"what": "fold = 2: as fold = 1, and each FFN block's resid -> q8 inside the "
                                              "next layer's QKV GEMV (bq_gemv_norm_fused with BQ_OP_RESID)",
                                      "ms_per_token": round(folded2_ms, 4), "GBps": round(gbs(tot, folded2_ms), 1),
-                                     "launches_per_token": 5 * LAYERS + 3},
+                                     "launches_per_token": 5 * LAYERS + 2},
             "decode_chain_verify": {"what": "the same step (fold = 0) over 2 / 4 / 8 token rows, the speculative-"
                                             "verify step with every row's logits (forward_batch_impl with "
                                             "all_logits, bruce.cu:7610-7843; one captured graph per row count as "

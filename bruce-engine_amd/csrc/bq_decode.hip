@@ -232,9 +232,20 @@ int bq_decode_enqueue(const bq_decode_step* s, bq_stream_t st) {
                                                                                  ? attn_block(s, b, i, rows, rs, st)
                                                                                  : BQ_EINVAL;
         if (r) return r;
+        if (!b.alpha) return BQ_EINVAL;
+        if (b.norm_after) {
+            // the block's resid -> q8 and the loop-end norm (k_resid :8017,
+            // k_norm :8022; rows: :7803-7818) in one launch, bit-identical to
+            // the two; it also takes up a pending update (fold = 2)
+            if (int e = flush(s, rs, st)) return e;
+            const hipError_t he = bq::launch_norm_q8(bq::kOpResidNorm, s->x, rs.cur, s->proj, b.alpha, nullptr, rows,
+                                                     n, s->xq, s->xd, s->xsum, (hipStream_t)st);
+            if (he != hipSuccess) return -(int)he;
+            rs.cur = s->x;
+            continue;
+        }
         // x = resid(x, proj, alpha) -> q8 x (k_resid_vec4, :8017; rows: :7803-7815);
         // fold = 2: left pending for the next block's QKV GEMV
-        if (!b.alpha) return BQ_EINVAL;
         if (s->fold == 2) {
             rs.alpha = b.alpha;
             const bool to_qkv = i + 1 < s->n_blocks && s->blocks[i + 1].kind == BQ_BLOCK_ATTN;
@@ -242,11 +253,6 @@ int bq_decode_enqueue(const bq_decode_step* s, bq_stream_t st) {
                 if (int e = flush(s, rs, st)) return e;
         } else if (int e = bq_resid_q8(s->x, s->proj, b.alpha, rows, n, s->xq, s->xd, s->xsum, st)) {
             return e;
-        }
-        // loop end: x = norm(x) (k_norm, :8022; rows: k_norm_rows :7818)
-        if (b.norm_after) {
-            if (int e = flush(s, rs, st)) return e;
-            if (int e = bq_norm_q8(s->x, s->x, rows, n, s->xq, s->xd, s->xsum, st)) return e;
         }
     }
     if (int e = flush(s, rs, st)) return e;

@@ -117,7 +117,10 @@ hipError_t launch_gemv_q8s(const void* W, int K, int N, int rows, const int8_t* 
 
 // q8 producers: elementwise op -> L2 norm -> q8 (op: 0 norm, 1 add, 2 resid,
 // 3 gate, 4 silu*mul); n % 32 == 0, n <= kNormMaxN
-enum NormOp { kOpNorm = 0, kOpAdd = 1, kOpResid = 2, kOpGate = 3, kOpSilu = 4 };
+enum NormOp { kOpNorm = 0, kOpAdd = 1, kOpResid = 2, kOpGate = 3, kOpSilu = 4,
+              // resid -> q8 followed by the plain norm of its row in one launch
+              // (the decode step's last resid and norm_after; launch_norm_q8 only)
+              kOpResidNorm = 5 };
 constexpr int kNormMaxN = 32768;
 hipError_t launch_norm_q8(int op, float* out, const float* a, const float* b, const float* c,
                           const float* d, int rows, int n, int8_t* xq, float* xd, int32_t* xsum,

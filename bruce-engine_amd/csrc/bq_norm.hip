@@ -49,7 +49,7 @@ __global__ void __launch_bounds__(1024) k_norm_q8(NormArgs p) {
     const int stride = blockDim.x * 16;
     f32x4 t[CH][4];
     float ss[1] = {0.f};
-    if constexpr (OP == kOpResid) {
+    if constexpr (OP == kOpResid || OP == kOpResidNorm) {
         // two row norms first (x and upd), then the blend and its norm
         f32x4 xa[CH][4], ub[CH][4], al[CH][4];
         float s2[2] = {0.f, 0.f};
@@ -120,7 +120,22 @@ __global__ void __launch_bounds__(1024) k_norm_q8(NormArgs p) {
         }
     }
     block_sum<1>(ss, red);
-    const float k = l2_scale(ss[0], n);
+    float k = l2_scale(ss[0], n);
+    if constexpr (OP == kOpResidNorm) {
+        // the resid's row, then k_norm over it (bruce.cu:8017, :8022): the
+        // sums of a separate norm launch over the emitted row, in its order
+        float s3[1] = {0.f};
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                t[c][i] = t[c][i] * k;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) s3[0] += t[c][i][e] * t[c][i][e];
+            }
+        block_sum<1>(s3, red);
+        k = l2_scale(s3[0], n);
+    }
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int i0 = c * stride + threadIdx.x * 16;
@@ -169,6 +184,7 @@ hipError_t launch_norm_q8(int op, float* out, const float* a, const float* b, co
         case kOpAdd: return launch_op<kOpAdd>(args, rows, st);
         case kOpResid: return launch_op<kOpResid>(args, rows, st);
         case kOpGate: return launch_op<kOpGate>(args, rows, st);
+        case kOpResidNorm: return launch_op<kOpResidNorm>(args, rows, st);
         default: return launch_op<kOpSilu>(args, rows, st);
     }
 }
