@@ -369,6 +369,8 @@ int bq_gguf_load(bq_gguf* g, int64_t i, void* raw, void* rep, void* rep_min, bq_
  *   FFN block: gate+up GEMV, silu*mul norm -> q8, down GEMV -> proj (:7994-8012)
  *   x = resid(x, proj, alpha) -> q8                               (k_resid :8017)
  *   norm_after: x = norm(x) -> q8                                 (k_norm :8022)
+ *     (on a block with norm_after, its resid and this norm run as one launch,
+ *     bit-identical to the two)
  * then the logits of every row: the Q8_0 head (head_q8s, bq_gemv_q8s with
  * head_rs) or a k-quant head (head)                                (:8026-8032).
  * fold = 1 (rows = 1 only; BQ_UNSUPPORTED with more) runs the gate norm
