@@ -265,9 +265,10 @@ def whole_stack(B, bq, synth, torch, w_gate, w_up, w_down, sp, ptr, steps=20, wa
                                     "ms_per_token": round(folded_ms, 4), "GBps": round(gbs(tot, folded_ms), 1),
                                     "launches_per_token": 6 * LAYERS + 1},
             "decode_chain_folded2": {"what": "fold = 2: as fold = 1, and each FFN block's resid -> q8 inside the "
-                                             "next layer's QKV GEMV (bq_gemv_norm_fused with BQ_OP_RESID)",
+                                             "next layer's QKV GEMV (bq_gemv_norm_fused with BQ_OP_RESID), the first "
+                                             "layer's loop-start norm inside its QKV GEMV (BQ_OP_ADD)",
                                      "ms_per_token": round(folded2_ms, 4), "GBps": round(gbs(tot, folded2_ms), 1),
-                                     "launches_per_token": 5 * LAYERS + 2},
+                                     "launches_per_token": 5 * LAYERS + 1},
             "decode_chain_verify": {"what": "the same step (fold = 0) over 2 / 4 / 8 token rows, the speculative-"
                                             "verify step with every row's logits (forward_batch_impl with "
                                             "all_logits, bruce.cu:7610-7843; one captured graph per row count as "

@@ -38,7 +38,9 @@ bool dims_ok(const bq_decode_step* s) {
 // attention block runs inside that block's QKV GEMV (bq_gemv_norm_fused with
 // BQ_OP_RESID), which writes the new residual row to the other of x / x_alt:
 // every workgroup of that GEMV reads the old row, so it cannot be updated in
-// place.  `cur` is the buffer holding the residual row; a pending update is
+// place.  An attention block's loop-start norm (norm_before: k_add_norm
+// :7914) runs inside its QKV GEMV the same way (BQ_OP_ADD).  `cur` is the
+// buffer holding the residual row; a pending update is
 // materialised (flush) by the standalone producer into x wherever the QKV
 // GEMV cannot take it: before norm_before / norm_after, when the QKV has no
 // Q5_K part or the fused form refuses it, and at the end of the step, so that
@@ -49,11 +51,19 @@ bool dims_ok(const bq_decode_step* s) {
 struct Resid {
     float* cur = nullptr;
     const float* alpha = nullptr;  // non-null: an update of cur by proj is pending
+    const float* add = nullptr;    // non-null: the loop-start norm of cur + add is pending
 };
 
 float* other_of(const bq_decode_step* s, const float* cur) { return cur == s->x ? s->x_alt : s->x; }
 
 int flush(const bq_decode_step* s, Resid& rs, bq_stream_t st) {
+    if (rs.add) {
+        const hipError_t e = bq::launch_norm_q8(bq::kOpAdd, s->x, rs.cur, rs.add, nullptr, nullptr, 1, s->n_embd,
+                                                s->xq, s->xd, s->xsum, (hipStream_t)st);
+        rs.cur = s->x;
+        rs.add = nullptr;
+        if (e != hipSuccess) return -(int)e;
+    }
     if (!rs.alpha) return BQ_OK;
     const hipError_t e = bq::launch_norm_q8(bq::kOpResid, s->x, rs.cur, s->proj, rs.alpha, nullptr, 1, s->n_embd,
                                             s->xq, s->xd, s->xsum, (hipStream_t)st);
@@ -150,6 +160,22 @@ int attn_block(const bq_decode_step* s, const bq_decode_block& b, int bi, int ro
             rs.alpha = nullptr;
             qkv_done = true;
         }
+    } else if (nf > 0 && rs.add) {
+        // the pending loop-start norm (k_add_norm, :7914) inside the QKV GEMV,
+        // the same way
+        float* nx = other_of(s, rs.cur);
+        const bool q8out = nf < b.n_qkv;
+        arm();
+        const int r = bq_gemv_norm_fused(yp, wp, nf, BQ_OP_ADD, nx, rs.cur, rs.add, nullptr, nullptr,
+                                         q8out ? s->xq : nullptr, q8out ? s->xd : nullptr,
+                                         q8out ? s->xsum : nullptr, st);
+        disarm();
+        if (r != BQ_OK && r != BQ_UNSUPPORTED) return r;
+        if (r == BQ_OK) {
+            rs.cur = nx;
+            rs.add = nullptr;
+            qkv_done = true;
+        }
     }
     if (int e = flush(s, rs, st)) return e;
     if (nf > 0 && !qkv_done) {
@@ -226,7 +252,11 @@ int bq_decode_enqueue(const bq_decode_step* s, bq_stream_t st) {
         if (b.norm_before) {
             if (int e = flush(s, rs, st)) return e;
             if (!s->input_h) return BQ_EINVAL;
-            if (int e = bq_add_norm_q8(s->x, s->input_h, rows, n, s->xq, s->xd, s->xsum, st)) return e;
+            if (s->fold == 2 && b.kind == BQ_BLOCK_ATTN) {
+                rs.add = s->input_h;  // fold = 2: inside the block's QKV GEMV (attn_block)
+            } else if (int e = bq_add_norm_q8(s->x, s->input_h, rows, n, s->xq, s->xd, s->xsum, st)) {
+                return e;
+            }
         }
         const int r = b.kind == BQ_BLOCK_FFN ? ffn_block(s, b, rows, rs, st) : b.kind == BQ_BLOCK_ATTN
                                                                                  ? attn_block(s, b, i, rows, rs, st)

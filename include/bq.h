@@ -379,7 +379,8 @@ int bq_gguf_load(bq_gguf* g, int64_t i, void* raw, void* rep, void* rep_min, bq_
  * per block pair, outputs equal to rounding).  fold = 2 (rows = 1 only)
  * also runs the resid -> q8 of each block that an attention block follows
  * inside that block's QKV GEMV (bq_gemv_norm_fused with BQ_OP_RESID over its
- * Q5_K parts; its q8 row is written out for any other part), which writes
+ * Q5_K parts; its q8 row is written out for any other part), and an
+ * attention block's norm_before the same way (BQ_OP_ADD), which writes
  * the new residual row to the other of x and x_alt; the other updates run as
  * their own launches into x, so x holds the result as in the other modes
  * (needs x_alt; 1 launch fewer per layer than fold = 1).  The attention

@@ -7,8 +7,8 @@ lie inside a buffer with room for what that call touches, no fused call may
 write a row that its workgroups also read, and the 4-block step issues the
 expected number of launches: 20 (fold 0; the last block's resid and the
 loop-end norm are one launch), 16 (fold 1: the gate norm in O, the silu*mul in
-the gate+up epilogue, its norm in down) and 15 (fold 2: also the FFN block's
-residual update in the next QKV GEMV).  The 8-row verify step and
+the gate+up epilogue, its norm in down) and 14 (fold 2: also the FFN block's
+residual update and the first block's loop-start norm in the QKV GEMV).  The 8-row verify step and
 a 40-row prompt chunk (prefill GEMMs with and without the step's xdh and
 workspace, the last row's logits) are checked the same way, and a workspace
 size without a workspace or rows above BQ_MAX_STEP_ROWS are refused."""
@@ -50,7 +50,7 @@ def test_decode_call_sequence(tmp_path):
     # into ffn_u (blocks 0 and 2), once the step has an FFN block to size ffn_u by
     want = lambda f, nb: 0 if f == 0 or nb == 1 else (nb + 1) // 2
     assert all(runs[(f, nb)][2] == want(f, nb) for f in range(3) for nb in range(1, 5)), runs
-    assert runs[(0, 4)][0] == 20 and runs[(1, 4)][0] == 16 and runs[(2, 4)][0] == 15, runs
+    assert runs[(0, 4)][0] == 20 and runs[(1, 4)][0] == 16 and runs[(2, 4)][0] == 14, runs
     # the verify step and a 40-row prompt chunk: the same 20 launches (one
     # prefill GEMM launch per fused GEMV, the last row's logits)
     rows = re.findall(r"rows (\d+) scratch (\d) calls (\d+) bad (\d+)", out)
