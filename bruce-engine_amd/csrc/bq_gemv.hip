@@ -775,11 +775,18 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     const int tile = blockIdx.x * RT + wave / KS, ks = wave % KS;
     const bool active = wave < RT * KS && tile < pt.ntiles;
     const int tl = active ? tile : 0;
+    // PAIR in the K = 3072 decode instance (one K slice): wave w of the
+    // workgroup takes 4 consecutive rows of one matrix (gate for even tiles,
+    // up for odd), as the plain two-output launch reads them, and the pair's
+    // h comes from both waves through LDS (folded decode chain fold 1 / 2
+    // 1.240 / 1.173 -> 1.231 / 1.167 ms/token against 2 gate + 2 up rows
+    // per wave); the sums are the same, so h is unchanged
+    constexpr bool kSplit = PAIR && KC == 3072 && SPS == 3;
     const int p = PAIR ? 0 : find_part(pt, tl);
     const int Nloc = pt.N[p];
-    const int row = PAIR ? 2 * tl + (g & 1) : (tl - pt.tile0[p]) * kRowsPerTile + g;
+    const int row = kSplit ? (tl >> 1) * kRowsPerTile + g : PAIR ? 2 * tl + (g & 1) : (tl - pt.tile0[p]) * kRowsPerTile + g;
     const int tpr = K >> 6;
-    const void* wbase = PAIR ? ((g >> 1) ? pt.W[1] : pt.W[0]) : pt.W[p];
+    const void* wbase = kSplit ? pt.W[tl & 1] : PAIR ? ((g >> 1) ? pt.W[1] : pt.W[0]) : pt.W[p];
     const uint8_t* rowp = (const uint8_t*)wbase + (size_t)min(row, Nloc - 1) * RowBytes<F>::of(K);
     typename F::Task w[SPS];
     // The fused quantizer's fp32 row comes from memory that the whole grid's
@@ -872,6 +879,15 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
     // ---- 5. row sums; K slices combined through LDS
     float* Y = pt.Y[p];
     if (KS == 1) {
+        if constexpr (kSplit) {
+            // tiles 2j, 2j + 1 (gate, up rows 4j..4j+3) are waves 2i, 2i + 1
+            const float v = row16_sum(acc[0]);
+            if (li == 15) part_sums[wave * 4 + g] = v;
+            __syncthreads();
+            if ((wave & 1) == 0 && li == 15 && rowok)
+                fq.out[row] = silu_mul(v, part_sums[(wave + 1) * 4 + g], pre_sg, pre_su);
+            return;
+        }
         if constexpr (PAIR) {
             const float v = row16_sum(acc[0]);
             const float u = __shfl(v, lane + 32, 64);  // DPP rows 0, 1 <- 2, 3
