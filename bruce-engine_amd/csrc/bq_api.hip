@@ -121,6 +121,21 @@ ScaledCopy& next_scaled_copy() {
 }
 
 int device_cus() { return t_dev ? t_dev->cus : 256; }
+
+int gemv_gate_den_fused(float* y, const void* w_raw, int K, int N, const float* a, const float* den, void* st) {
+    if (int r = ensure_init()) return r;
+    if (!y || !w_raw || !a || !den || K <= 0 || N <= 0 || K % 256 != 0) return BQ_EINVAL;
+    if (!al16(w_raw) || !al16(a) || !al16(den)) return BQ_EINVAL;
+    if (!gemv_producer_supported(K)) return BQ_UNSUPPORTED;
+    PartTable pt;
+    memset(&pt, 0, sizeof(pt));
+    pt.W[0] = w_raw;
+    pt.Y[0] = y;
+    pt.N[0] = N;
+    pt.nparts = 1;
+    return from_hip(launch_gemv_producer(GemvKind::Q5K, pt, K, kOpGateDen, nullptr, a, den, nullptr, nullptr, nullptr,
+                                         nullptr, nullptr, (hipStream_t)st));
+}
 }  // namespace bq
 
 extern "C" {

@@ -573,7 +573,7 @@ BQ_DEV void fp_load(f32x4 (&in)[4][4], const FusedQ8& fq, int K, int wave, int l
             in[0][i] = *(const f32x4*)(fq.x + v0 + 4 * i);
             if (op != kOpNorm) in[1][i] = *(const f32x4*)(fq.b + v0 + 4 * i);
             // gate with no sg row: the gate row is already scaled (sg = 1)
-            if (op >= kOpResid)
+            if (op >= kOpResid && op != kOpGateDen)
                 in[2][i] = fq.c ? *(const f32x4*)(fq.c + v0 + 4 * i) : f32x4{1.f, 1.f, 1.f, 1.f};
             if (op == kOpSilu) in[3][i] = *(const f32x4*)(fq.d + v0 + 4 * i);
         }
@@ -636,6 +636,9 @@ BQ_DEV void fp_produce(const f32x4 (&in)[4][4], uint8_t* smem, float* red, int K
             } else if (op == kOpGate) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) t[i][e] = gate_div(in[0][i][e], in[1][i][e], in[2][i][e]);
+            } else if (op == kOpGateDen) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) t[i][e] = over_den(in[0][i][e], in[1][i][e]);
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) t[i][e] = silu_mul(in[0][i][e], in[1][i][e], in[2][i][e], in[3][i][e]);
@@ -680,6 +683,17 @@ BQ_DEV void fp_produce(const f32x4 (&in)[4][4], uint8_t* smem, float* red, int K
     }
     asm volatile("" ::: "memory");
     BQ_WAIT_LGKM0();
+}
+
+// The scaled copy of a one-row GEMV output: v * s, or (den) the sigmoid
+// denominator of that product, 1 + exp(-(v * s)), the value the gate norm
+// forms from it (gate_div with sg = 1); the product is rounded to fp32 first,
+// as it is when stored and read back
+BQ_DEV float scaled_out(float v, float s, int den) {
+    float x = v * s;
+    if (!den) return x;
+    asm("" : "+v"(x));
+    return sigmoid_den(x);
 }
 
 // ---------------------------------------------------------------------------
@@ -906,7 +920,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
                 const float v = row16_sum(acc[m]);
                 if (li == 15 && rowok) {
                     Y[(size_t)m * Nloc + row] = v;
-                    if (MR == 1 && pt.ys && p == pt.sp) pt.ys[row] = v * pt.ss[row];
+                    if (MR == 1 && pt.ys && p == pt.sp) pt.ys[row] = scaled_out(v, pt.ss[row], pt.sden);
                 }
             }
         }
@@ -941,7 +955,7 @@ k_gemv(PartTable pt, int K_, int KS_, const int8_t* __restrict__ xq, const float
             float v = 0.f;
             for (int k = 0; k < KS; ++k) v += part_sums[((wave + k) * MR + m) * 4 + g];
             Y[(size_t)m * Nloc + row] = v;
-            if (MR == 1 && pt.ys && p == pt.sp) pt.ys[row] = v * pt.ss[row];
+            if (MR == 1 && pt.ys && p == pt.sp) pt.ys[row] = scaled_out(v, pt.ss[row], pt.sden);
         }
     }
 }
@@ -1046,6 +1060,7 @@ static hipError_t launch_fmt(const PartTable& pt, int K, int KS, const int8_t* x
                 ptl.sp = q;
                 ptl.ys = sc.y;
                 ptl.ss = sc.s;
+                ptl.sden = sc.den ? 1 : 0;
                 sc = ScaledCopy();
             }
     }

@@ -27,6 +27,7 @@ struct PartTable {
     int sp = 0;
     float* ys = nullptr;
     const float* ss = nullptr;
+    int sden = 0;  // ys[row] = 1 + exp(-(y[row] * ss[row])) instead (the gate's sigmoid denominator)
 };
 
 enum class GemvKind { Q5K, Q6KRaw, Q6KRep };
@@ -47,8 +48,12 @@ struct ScaledCopy {
     const void* w = nullptr;
     float* y = nullptr;
     const float* s = nullptr;
+    bool den = false;  // write the sigmoid denominator of the scaled value
 };
 ScaledCopy& next_scaled_copy();
+// O GEMV with the gate norm over precomputed sigmoid denominators (kOpGateDen;
+// bq_api.hip): y = W * q8(norm(a / den)); BQ_UNSUPPORTED when not taken
+int gemv_gate_den_fused(float* y, const void* w_raw, int K, int N, const float* a, const float* den, void* st);
 // CU count of the current device (set by the entry point's init; 256 before any)
 int device_cus();
 
@@ -120,7 +125,10 @@ hipError_t launch_gemv_q8s(const void* W, int K, int N, int rows, const int8_t* 
 enum NormOp { kOpNorm = 0, kOpAdd = 1, kOpResid = 2, kOpGate = 3, kOpSilu = 4,
               // resid -> q8 followed by the plain norm of its row in one launch
               // (the decode step's last resid and norm_after; launch_norm_q8 only)
-              kOpResidNorm = 5 };
+              kOpResidNorm = 5,
+              // the attention gate with its sigmoid denominators precomputed:
+              // t = a / b (producer-fused GEMV only)
+              kOpGateDen = 6 };
 constexpr int kNormMaxN = 32768;
 hipError_t launch_norm_q8(int op, float* out, const float* a, const float* b, const float* c,
                           const float* d, int rows, int n, int8_t* xq, float* xd, int32_t* xsum,

@@ -390,7 +390,8 @@ int bq_gguf_load(bq_gguf* g, int64_t i, void* raw, void* rep, void* rep_min, bq_
  * [rows][n_embd]; attn_out, attn_gate [rows][n_attn]; qkv_out[p] [rows][N_p];
  * ffn_g, ffn_u [rows][n_ff] (with fold >= 1 ffn_u, optional, is scratch: when
  * attn_gate is the start of a Q5_K QKV part's output, the QKV launch also
- * writes that part times sgate there and the O GEMV's gate norm reads it
+ * writes that part times sgate there, or for a Q5_K O its sigmoid
+ * denominator 1 + exp(-gate * sgate), and the O GEMV's gate norm reads it
  * instead of attn_gate and sgate, same results); logits
  * [rows][vocab] (a prompt chunk: [vocab]); xq/xd/xsum hold the q8 rows of the
  * widest operand, rows x max(n_embd, n_attn, n_ff) values.  x is updated in

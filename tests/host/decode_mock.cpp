@@ -132,6 +132,12 @@ int bq_gemv_q8s(float* y, const void* w, const int8_t* xq, const float* xd, int 
 }
 }
 namespace bq {
+int gemv_gate_den_fused(float* y, const void* w_raw, int K, int N, const float* a, const float* den, void*) {
+    ++g_calls; if (g_verbose) printf("gate_den_fused K=%d N=%d\n", K, N);
+    chk("gden", "y", y, 4 * (size_t)N); chk("gden", "w", w_raw, (size_t)N * (K / 256) * 176);
+    chk("gden", "a", a, 4 * (size_t)K); chk("gden", "den", den, 4 * (size_t)K);
+    return 0;
+}
 hipError_t launch_norm_q8(int op, float* out, const float* a, const float* b, const float* c, const float* d, int rows, int n, int8_t* xq, float* xd, int32_t* xs, hipStream_t) {
     nq(op == 2 ? "launch_norm_q8(resid)" : "launch_norm_q8", out, a, b, c, d, rows, n, xq, xd, xs); return hipSuccess;
 }
